@@ -1,0 +1,158 @@
+/*
+ * moeinfra_hip.h -- C ABI of libmoeinfra_hip.so, the gfx950 (MI355X) MoE
+ * expert-execution path.
+ *
+ * Every entry point takes raw device pointers, 64-bit sizes and a hipStream_t
+ * (passed as void*), enqueues its kernels on that stream, performs no host<->device
+ * synchronisation and allocates no memory: the caller owns every buffer, including the
+ * workspace.  Calls return MOE_STATUS_OK (0) or a negative status; the message of the
+ * last failure on the calling thread is returned by moe_last_error().  Calls on one
+ * stream are ordered; the library keeps no mutable global state besides a per-device
+ * cache of the compute-unit count.
+ *
+ * Data formats (bitsandbytes NF4, as the reference stores it):
+ *   - a weight W[O][I] is the row-major flatten of O*I values quantised in blocks of
+ *     `blocksize` consecutive values (64 on the expert path);
+ *   - packed byte j holds value 2j in its HIGH nibble and value 2j+1 in its low nibble;
+ *   - absmax is fp32, one per block; code is the fp32[16] codebook (quant_map);
+ *   - dequantised value = bf16_round_nearest_even(code[q] * absmax[block]).
+ * Activations are bf16 (raw uint16 bit patterns in memory), routing weights fp32,
+ * expert indices int64 (int32 copies are kept for the kernels).
+ *
+ * Reference citations are into ParshwaPatel-07/MoEInfra.
+ */
+#ifndef MOEINFRA_HIP_H
+#define MOEINFRA_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MOE_STATUS_OK 0
+#define MOE_STATUS_INVALID_ARGUMENT (-1)
+#define MOE_STATUS_HIP_ERROR (-2)
+#define MOE_STATUS_UNSUPPORTED (-3)
+
+/* Largest number of experts one call can address (the pointer table travels as a
+ * kernel argument). */
+#define MOE_MAX_EXPERTS 32
+/* Largest top-k. */
+#define MOE_MAX_TOPK 8
+/* Block size the fused expert kernels require (transfer/nf4_reconstruct.py:9). */
+#define MOE_NF4_BLOCKSIZE 64
+
+/* Device pointers of one NF4 expert: the packed weight, fp32 absmax and fp32[16]
+ * codebook of each projection, w1 [F,H] (gate), w3 [F,H] (up), w2 [H,F] (down).
+ * Mirrors the per-projection state dict {weight, absmax, code} that
+ * transfer/nf4_transfer.py:8-40 produces on the device and
+ * transfer/nf4_reconstruct.py:57-114 wraps. */
+typedef struct moe_nf4_expert {
+    const void *w1_packed;
+    const void *w1_absmax;
+    const void *w1_code;
+    const void *w3_packed;
+    const void *w3_absmax;
+    const void *w3_code;
+    const void *w2_packed;
+    const void *w2_absmax;
+    const void *w2_code;
+} moe_nf4_expert_t;
+
+/* Message of the last failed call on this thread ("" if none). */
+const char *moe_last_error(void);
+
+/* Library version (major*10000 + minor*100 + patch). */
+int moe_version(void);
+
+/* ---------------------------------------------------------------- K1: NF4 dequant
+ * out_bf16[i] = bf16(code[q_i] * absmax[i / blocksize]) for i < numel.
+ * Replaces the bitsandbytes dequantize_4bit that Linear4bit runs on the state built
+ * by _build_quant_state / _reconstruct_linear (transfer/nf4_reconstruct.py:17-114).
+ * numel must be even, blocksize a positive multiple of 32. */
+int moe_nf4_dequant_bf16(const void *packed, const void *absmax, const void *code16,
+                         void *out_bf16, int64_t numel, int32_t blocksize, void *stream);
+
+/* ---------------------------------------------------------------- K0: NF4 quantise
+ * Blockwise NF4 quantisation of bf16 values: absmax = max|w| per block, q = nearest
+ * code value of w*(1/absmax) (midpoint thresholds, ties to the lower code).
+ * Replaces the bitsandbytes quantisation that QuantizedMixtralExpert triggers when
+ * moved to the GPU (model/expert.py:32-63, model/loader.py:404-415).
+ * numel even; blocksize even, 2..4096. absmax_out has ceil(numel/blocksize) floats. */
+int moe_nf4_quantize_bf16(const void *w_bf16, int64_t numel, int32_t blocksize,
+                          const void *code16, void *packed_out, void *absmax_out, void *stream);
+
+/* ---------------------------------------------------------------- K2: router
+ * logits = bf16(x . gate^T); p = softmax(float(logits) [+ bias]); (w, idx) = top-k(p)
+ * in descending order (ties: lower expert index first); w /= sum(w).
+ * Replaces ExpertRouter.logits / route / route_with_logits (engine/router.py:50-94).
+ * x [T,H] bf16, gate [E,H] bf16, bias fp32 [E] or NULL; outputs logits bf16 [T,E]
+ * (may be NULL), weights fp32 [T,k], idx int64 [T,k], idx32 int32 [T,k] (may be NULL).
+ * Requires H % 8 == 0, 1 <= E <= MOE_MAX_EXPERTS, 1 <= k <= min(E, MOE_MAX_TOPK). */
+int moe_router_topk(const void *x_bf16, const void *gate_bf16, const void *bias_f32,
+                    int64_t T, int32_t H, int32_t E, int32_t k, void *logits_bf16,
+                    void *weights_f32, void *idx_i64, void *idx_i32, void *stream);
+
+/* ---------------------------------------------------------------- K3: permute
+ * Groups the T*k (token, slot) pairs by expert, ascending expert id and ascending
+ * token within an expert -- the order model/moe_layer.py:150-185 visits them in
+ * (unique().tolist(), boolean-mask gather).  Outputs (int32):
+ *   counts[E]        tokens per expert
+ *   offsets[E+1]     exclusive prefix sum of counts
+ *   perm_tok[T*k]    token id of each row of the expert-sorted order
+ *   slot_pos[T*k]    row of flat slot t*k+j in that order
+ *   active[E+1]      active[0] = number of experts with tokens, then their ids ascending
+ * idx32 entries must lie in [0,E). */
+int moe_permute(const void *idx_i32, int64_t T, int32_t k, int32_t E, void *counts,
+                void *offsets, void *perm_tok, void *slot_pos, void *active, void *stream);
+
+/* ---------------------------------------------------------------- K4: expert FFN
+ * For every active expert e and its rows r in [offsets[e], offsets[e+1]):
+ *   h[r]  = bf16( bf16(silu(bf16(w1_e x_t))) * bf16(w3_e x_t) )       t = perm_tok[r]
+ *   y[r]  = w2_e h[r]   (fp32; written as `nsplit` partial sums ypart[s][r][H])
+ * with NF4 weights dequantised in registers (blocksize 64) and bf16 MFMA, fp32
+ * accumulation.  Replaces ReconstructedNF4Expert.forward (transfer/nf4_reconstruct.py:
+ * 152-155) / QuantizedMixtralExpert.forward (model/expert.py:65-75) for all routed
+ * experts of a layer at once.  h_ws has T*k*F bf16; ypart has nsplit*T*k*H floats.
+ * Requires H % 256 == 0, F % 256 == 0, 1 <= nsplit <= 16. */
+int moe_expert_ffn_nf4(const moe_nf4_expert_t *experts, int32_t E, const void *x_bf16,
+                       int64_t T, int32_t k, int32_t H, int32_t F, const void *counts,
+                       const void *offsets, const void *perm_tok, const void *active,
+                       void *h_ws_bf16, void *ypart_f32, int32_t nsplit, void *stream);
+
+/* ---------------------------------------------------------------- K5: combine
+ * out[t] = 0; for the k slots of token t in ascending expert order:
+ *   y = bf16(sum_s ypart[s][slot_pos[t*k+j]]);  out[t] = bf16(out[t] + y * w[t,j])
+ * (fp32 product and sum, bf16 destination) -- model/moe_layer.py:147,187-191. */
+int moe_combine(const void *ypart_f32, int32_t nsplit, const void *weights_f32,
+                const void *idx_i32, const void *slot_pos, int64_t T, int32_t k, int32_t H,
+                void *out_bf16, void *stream);
+
+/* ---------------------------------------------------------------- single expert
+ * y[T,H] = bf16(w2 (silu(w1 x) * w3 x)) for one expert on all T rows of x -- the
+ * ReconstructedNF4Expert.__call__ of transfer/nf4_reconstruct.py:152-155.
+ * workspace >= moe_expert_workspace_bytes(T, H, F). */
+int64_t moe_expert_workspace_bytes(int64_t T, int32_t H, int32_t F);
+int moe_expert_swiglu_nf4(const moe_nf4_expert_t *expert, const void *x_bf16, int64_t T,
+                          int32_t H, int32_t F, void *y_bf16, void *workspace,
+                          int64_t workspace_bytes, void *stream);
+
+/* ---------------------------------------------------------------- whole layer
+ * Router (K2) -> permute (K3) -> expert FFN (K4) -> combine (K5) in one call: the
+ * device-resident form of MoELayer._forward_tokens (model/moe_layer.py:117-211) with
+ * every routed expert resident.  experts[e] must be valid for every e < E that the
+ * router can select.  logits_bf16 may be NULL; weights_f32 [T,k] and idx_i64 [T,k]
+ * receive the routing.  workspace >= moe_layer_workspace_bytes(T, k, E, H, F). */
+int64_t moe_layer_workspace_bytes(int64_t T, int32_t k, int32_t E, int32_t H, int32_t F);
+int moe_layer_forward_nf4(const moe_nf4_expert_t *experts, int32_t E, const void *gate_bf16,
+                          const void *bias_f32, const void *x_bf16, int64_t T, int32_t H,
+                          int32_t F, int32_t k, void *out_bf16, void *logits_bf16,
+                          void *weights_f32, void *idx_i64, void *workspace,
+                          int64_t workspace_bytes, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MOEINFRA_HIP_H */

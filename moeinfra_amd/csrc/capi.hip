@@ -1,0 +1,188 @@
+// C-ABI glue: error reporting, device info, workspace layout, and the composed
+// entry points (whole MoE layer, single expert).
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <mutex>
+
+#include "common.h"
+
+namespace moe {
+
+int choose_nsplit(int64_t T, int32_t k, int32_t E, int32_t H);
+int launch_expert_ffn(const moe_nf4_expert_t *experts, int32_t E, const void *x, int64_t T,
+                      int32_t k, int32_t H, int32_t F, const int32_t *counts,
+                      const int32_t *offsets, const int32_t *perm_tok, const int32_t *active,
+                      void *h_ws, void *ypart, int32_t nsplit, int64_t max_tokens_per_expert,
+                      hipStream_t stream);
+int launch_combine(const void *ypart, int32_t nsplit, const void *weights, const void *idx_i32,
+                   const void *slot_pos, int64_t T, int32_t k, int32_t H, void *out,
+                   hipStream_t stream);
+int launch_identity_route(int64_t T, int32_t *counts, int32_t *offsets, int32_t *perm_tok,
+                          int32_t *active, hipStream_t stream);
+int launch_reduce_splits(const float *ypart, int nsplit, int64_t numel, uint16_t *y,
+                         hipStream_t stream);
+
+namespace {
+thread_local char g_last_error[512] = "";
+
+constexpr int kMaxDevices = 64;
+int g_cu_count[kMaxDevices] = {0};
+std::mutex g_cu_mutex;
+
+constexpr int64_t kAlign = 256;
+int64_t align_up(int64_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
+
+// Byte offsets of the layer workspace regions.
+struct LayerWs {
+  int64_t idx32, counts, offsets, perm_tok, slot_pos, active, h, ypart, total;
+  int nsplit;
+};
+
+LayerWs layer_ws(int64_t T, int32_t k, int32_t E, int32_t H, int32_t F) {
+  LayerWs w{};
+  const int64_t rows = T * k;
+  w.nsplit = choose_nsplit(T, k, E, H);
+  int64_t o = 0;
+  w.idx32 = o;    o = align_up(o + rows * 4);
+  w.counts = o;   o = align_up(o + (int64_t)E * 4);
+  w.offsets = o;  o = align_up(o + (int64_t)(E + 1) * 4);
+  w.perm_tok = o; o = align_up(o + rows * 4);
+  w.slot_pos = o; o = align_up(o + rows * 4);
+  w.active = o;   o = align_up(o + (int64_t)(E + 1) * 4);
+  w.h = o;        o = align_up(o + rows * (int64_t)F * 2);
+  w.ypart = o;    o = align_up(o + (int64_t)w.nsplit * rows * H * 4);
+  w.total = o;
+  return w;
+}
+
+struct ExpertWs {
+  int64_t counts, offsets, perm_tok, active, h, ypart, total;
+  int nsplit;
+};
+
+ExpertWs expert_ws(int64_t T, int32_t H, int32_t F) {
+  ExpertWs w{};
+  w.nsplit = choose_nsplit(T, 1, 1, H);
+  int64_t o = 0;
+  w.counts = o;   o = align_up(o + 4);
+  w.offsets = o;  o = align_up(o + 8);
+  w.perm_tok = o; o = align_up(o + T * 4);
+  w.active = o;   o = align_up(o + 8);
+  w.h = o;        o = align_up(o + T * (int64_t)F * 2);
+  w.ypart = o;    o = align_up(o + (int64_t)w.nsplit * T * H * 4);
+  w.total = o;
+  return w;
+}
+
+template <typename P>
+P *at(void *base, int64_t off) {
+  return reinterpret_cast<P *>(static_cast<char *>(base) + off);
+}
+}  // namespace
+
+void set_error(const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_last_error, sizeof g_last_error, fmt, ap);
+  va_end(ap);
+}
+
+int device_cu_count() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256;
+  {
+    std::lock_guard<std::mutex> lock(g_cu_mutex);
+    if (g_cu_count[dev] > 0) return g_cu_count[dev];
+  }
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      cus <= 0)
+    cus = 256;
+  std::lock_guard<std::mutex> lock(g_cu_mutex);
+  g_cu_count[dev] = cus;
+  return cus;
+}
+
+}  // namespace moe
+
+extern "C" const char *moe_last_error(void) { return moe::g_last_error; }
+
+extern "C" int moe_version(void) { return 100; }
+
+extern "C" int64_t moe_layer_workspace_bytes(int64_t T, int32_t k, int32_t E, int32_t H,
+                                             int32_t F) {
+  if (T < 0 || k < 1 || E < 1 || H < 1 || F < 1) return -1;
+  return moe::layer_ws(T, k, E, H, F).total;
+}
+
+extern "C" int moe_layer_forward_nf4(const moe_nf4_expert_t *experts, int32_t E,
+                                     const void *gate_bf16, const void *bias_f32,
+                                     const void *x_bf16, int64_t T, int32_t H, int32_t F,
+                                     int32_t k, void *out_bf16, void *logits_bf16,
+                                     void *weights_f32, void *idx_i64, void *workspace,
+                                     int64_t workspace_bytes, void *stream) {
+  MOE_REQUIRE(T >= 0 && k >= 1 && E >= 1 && H >= 1 && F >= 1, "bad sizes");
+  if (T == 0) return MOE_STATUS_OK;
+  const moe::LayerWs w = moe::layer_ws(T, k, E, H, F);
+  MOE_REQUIRE(workspace != nullptr && workspace_bytes >= w.total,
+              "workspace too small: need %lld bytes, got %lld", (long long)w.total,
+              (long long)workspace_bytes);
+  MOE_REQUIRE(((uintptr_t)workspace % 256) == 0, "workspace must be 256-byte aligned");
+  hipStream_t s = (hipStream_t)stream;
+  int rc = moe_router_topk(x_bf16, gate_bf16, bias_f32, T, H, E, k, logits_bf16, weights_f32,
+                           idx_i64, moe::at<int32_t>(workspace, w.idx32), stream);
+  if (rc != MOE_STATUS_OK) return rc;
+  rc = moe_permute(moe::at<int32_t>(workspace, w.idx32), T, k, E,
+                   moe::at<int32_t>(workspace, w.counts), moe::at<int32_t>(workspace, w.offsets),
+                   moe::at<int32_t>(workspace, w.perm_tok),
+                   moe::at<int32_t>(workspace, w.slot_pos), moe::at<int32_t>(workspace, w.active),
+                   stream);
+  if (rc != MOE_STATUS_OK) return rc;
+  rc = moe::launch_expert_ffn(experts, E, x_bf16, T, k, H, F,
+                              moe::at<int32_t>(workspace, w.counts),
+                              moe::at<int32_t>(workspace, w.offsets),
+                              moe::at<int32_t>(workspace, w.perm_tok),
+                              moe::at<int32_t>(workspace, w.active),
+                              moe::at<void>(workspace, w.h), moe::at<void>(workspace, w.ypart),
+                              w.nsplit, T, s);
+  if (rc != MOE_STATUS_OK) return rc;
+  return moe::launch_combine(moe::at<void>(workspace, w.ypart), w.nsplit, weights_f32,
+                             moe::at<int32_t>(workspace, w.idx32),
+                             moe::at<int32_t>(workspace, w.slot_pos), T, k, H, out_bf16, s);
+}
+
+extern "C" int64_t moe_expert_workspace_bytes(int64_t T, int32_t H, int32_t F) {
+  if (T < 0 || H < 1 || F < 1) return -1;
+  return moe::expert_ws(T, H, F).total;
+}
+
+extern "C" int moe_expert_swiglu_nf4(const moe_nf4_expert_t *expert, const void *x_bf16,
+                                     int64_t T, int32_t H, int32_t F, void *y_bf16,
+                                     void *workspace, int64_t workspace_bytes, void *stream) {
+  MOE_REQUIRE(T >= 0 && T <= 0x7fffffff, "T out of range");
+  MOE_REQUIRE(expert != nullptr, "null expert");
+  if (T == 0) return MOE_STATUS_OK;
+  MOE_REQUIRE(y_bf16 != nullptr && ((uintptr_t)y_bf16 % 8) == 0, "y must be 8-byte aligned");
+  const moe::ExpertWs w = moe::expert_ws(T, H, F);
+  MOE_REQUIRE(workspace != nullptr && workspace_bytes >= w.total,
+              "workspace too small: need %lld bytes, got %lld", (long long)w.total,
+              (long long)workspace_bytes);
+  MOE_REQUIRE(((uintptr_t)workspace % 256) == 0, "workspace must be 256-byte aligned");
+  hipStream_t s = (hipStream_t)stream;
+  int rc = moe::launch_identity_route(T, moe::at<int32_t>(workspace, w.counts),
+                                      moe::at<int32_t>(workspace, w.offsets),
+                                      moe::at<int32_t>(workspace, w.perm_tok),
+                                      moe::at<int32_t>(workspace, w.active), s);
+  if (rc != MOE_STATUS_OK) return rc;
+  rc = moe::launch_expert_ffn(expert, 1, x_bf16, T, 1, H, F,
+                              moe::at<int32_t>(workspace, w.counts),
+                              moe::at<int32_t>(workspace, w.offsets),
+                              moe::at<int32_t>(workspace, w.perm_tok),
+                              moe::at<int32_t>(workspace, w.active),
+                              moe::at<void>(workspace, w.h), moe::at<void>(workspace, w.ypart),
+                              w.nsplit, T, s);
+  if (rc != MOE_STATUS_OK) return rc;
+  return moe::launch_reduce_splits(moe::at<float>(workspace, w.ypart), w.nsplit, T * (int64_t)H,
+                                   (uint16_t *)y_bf16, s);
+}

@@ -1,0 +1,67 @@
+// Shared definitions for the gfx950 MoE expert-path kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/moeinfra_hip.h"
+
+namespace moe {
+
+// Records a printf-style message as the calling thread's last error.
+void set_error(const char *fmt, ...) __attribute__((format(printf, 1, 2)));
+// Number of compute units of the current device (cached per device).
+int device_cu_count();
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------- vector types
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
+
+// ---------------------------------------------------------------- bf16 helpers
+// Round-to-nearest-even float -> bf16 bits (v_cvt_pk_bf16_f32 on gfx950).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  return __builtin_bit_cast(uint16_t, (__bf16)f);
+}
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
+}
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+  return __builtin_bit_cast(float, (uint32_t)h << 16);
+}
+__device__ __forceinline__ float bf16lo_to_f32(uint32_t w) {
+  return __builtin_bit_cast(float, w << 16);
+}
+__device__ __forceinline__ float bf16hi_to_f32(uint32_t w) {
+  return __builtin_bit_cast(float, w & 0xffff0000u);
+}
+
+// ---------------------------------------------------------------- wave reductions
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+}  // namespace moe
+
+// Status helpers for the C-ABI entry points.
+#define MOE_REQUIRE(cond, ...)                                                                     \
+  do {                                                                                             \
+    if (!(cond)) {                                                                                 \
+      ::moe::set_error(__VA_ARGS__);                                                               \
+      return MOE_STATUS_INVALID_ARGUMENT;                                                          \
+    }                                                                                              \
+  } while (0)
+
+#define MOE_HIP_CHECK(expr)                                                                        \
+  do {                                                                                             \
+    hipError_t _moe_err = (expr);                                                                  \
+    if (_moe_err != hipSuccess) {                                                                  \
+      ::moe::set_error("%s failed: %s", #expr, hipGetErrorString(_moe_err));                       \
+      return MOE_STATUS_HIP_ERROR;                                                                 \
+    }                                                                                              \
+  } while (0)
+
+#define MOE_LAUNCH_CHECK() MOE_HIP_CHECK(hipGetLastError())

@@ -1,0 +1,132 @@
+// K0 (NF4 blockwise quantise) and K1 (standalone NF4 -> bf16 dequant) for gfx950.
+//
+// K1 is HBM-bound: 0.5 B read + 2 B written per value (plus 4 B of absmax per 64
+// values).  Each thread owns 32 consecutive values: one 16-byte load of packed nibbles,
+// one absmax, four 16-byte stores of bf16.  The 16-entry codebook sits in LDS; 16
+// distinct entries map to 16 distinct banks, so the lookups never conflict.
+#include "common.h"
+
+namespace moe {
+namespace {
+
+constexpr int kDequantThreads = 256;
+constexpr int kValsPerThread = 32;
+
+__global__ void __launch_bounds__(kDequantThreads)
+nf4_dequant_kernel(const uint8_t *__restrict__ packed, const float *__restrict__ absmax,
+                   const float *__restrict__ code, uint16_t *__restrict__ out, int64_t numel,
+                   int32_t blocksize) {
+  __shared__ float s_code[16];
+  if (threadIdx.x < 16) s_code[threadIdx.x] = code[threadIdx.x];
+  __syncthreads();
+
+  const int64_t nvec = numel / kValsPerThread;
+  const int64_t stride = (int64_t)gridDim.x * kDequantThreads;
+  for (int64_t v = (int64_t)blockIdx.x * kDequantThreads + threadIdx.x; v < nvec; v += stride) {
+    const int64_t base = v * kValsPerThread;
+    const uint4 q = *reinterpret_cast<const uint4 *>(packed + base / 2);
+    // blocksize is a multiple of 32, so all 32 values share one absmax.
+    const float a = absmax[base / blocksize];
+    const uint32_t words[4] = {q.x, q.y, q.z, q.w};
+    uint32_t o[16];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const uint32_t byte = (words[w] >> (8 * b)) & 0xffu;
+        const float hi = s_code[byte >> 4] * a;   // value 2j   (high nibble)
+        const float lo = s_code[byte & 15u] * a;  // value 2j+1 (low nibble)
+        o[w * 4 + b] = pack_bf16x2(hi, lo);
+      }
+    }
+    uint4 *dst = reinterpret_cast<uint4 *>(out + base);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) dst[s] = make_uint4(o[4 * s], o[4 * s + 1], o[4 * s + 2], o[4 * s + 3]);
+  }
+  // Tail: fewer than 32 values left (numel is even); one thread finishes them.
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    for (int64_t i = nvec * kValsPerThread; i < numel; i += 2) {
+      const uint32_t byte = packed[i / 2];
+      out[i] = f32_to_bf16(s_code[byte >> 4] * absmax[i / blocksize]);
+      out[i + 1] = f32_to_bf16(s_code[byte & 15u] * absmax[(i + 1) / blocksize]);
+    }
+  }
+}
+
+constexpr int kQuantThreads = 256;
+
+// One thread per quantisation block.  Not on the timed path (fixture creation).
+__global__ void __launch_bounds__(kQuantThreads)
+nf4_quantize_kernel(const uint16_t *__restrict__ w, int64_t numel, int32_t blocksize,
+                    const float *__restrict__ code, uint8_t *__restrict__ packed,
+                    float *__restrict__ absmax) {
+  __shared__ float s_mid[15];
+  if (threadIdx.x < 15) s_mid[threadIdx.x] = (code[threadIdx.x] + code[threadIdx.x + 1]) * 0.5f;
+  __syncthreads();
+  const int64_t nblocks = (numel + blocksize - 1) / blocksize;
+  const int64_t b = (int64_t)blockIdx.x * kQuantThreads + threadIdx.x;
+  if (b >= nblocks) return;
+  const int64_t lo = b * blocksize;
+  const int64_t hi = lo + blocksize < numel ? lo + blocksize : numel;
+  float amax = 0.0f;
+  for (int64_t i = lo; i < hi; ++i) amax = fmaxf(amax, fabsf(bf16_to_f32(w[i])));
+  absmax[b] = amax;
+  const float r = amax > 0.0f ? 1.0f / amax : 0.0f;
+  for (int64_t i = lo; i < hi; i += 2) {
+    int q[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const float x = bf16_to_f32(w[i + j]) * r;
+      int c = 0;
+#pragma unroll
+      for (int m = 0; m < 15; ++m) c += x > s_mid[m];
+      q[j] = c;
+    }
+    packed[i / 2] = (uint8_t)((q[0] << 4) | q[1]);
+  }
+}
+
+}  // namespace
+}  // namespace moe
+
+extern "C" int moe_nf4_dequant_bf16(const void *packed, const void *absmax, const void *code16,
+                                    void *out_bf16, int64_t numel, int32_t blocksize,
+                                    void *stream) {
+  MOE_REQUIRE(numel >= 0 && numel % 2 == 0, "numel must be even and non-negative (got %lld)",
+              (long long)numel);
+  MOE_REQUIRE(blocksize > 0 && blocksize % 32 == 0,
+              "blocksize must be a positive multiple of 32 (got %d)", blocksize);
+  if (numel == 0) return MOE_STATUS_OK;
+  MOE_REQUIRE(packed && absmax && code16 && out_bf16, "null device pointer");
+  MOE_REQUIRE(((uintptr_t)packed % 16) == 0 && ((uintptr_t)out_bf16 % 16) == 0,
+              "packed and out must be 16-byte aligned");
+  const int64_t nvec = numel / moe::kValsPerThread;
+  int64_t blocks = (nvec + moe::kDequantThreads - 1) / moe::kDequantThreads;
+  const int64_t cap = (int64_t)moe::device_cu_count() * 32;
+  if (blocks > cap) blocks = cap;
+  if (blocks < 1) blocks = 1;
+  hipLaunchKernelGGL(moe::nf4_dequant_kernel, dim3((unsigned)blocks), dim3(moe::kDequantThreads),
+                     0, (hipStream_t)stream, (const uint8_t *)packed, (const float *)absmax,
+                     (const float *)code16, (uint16_t *)out_bf16, numel, blocksize);
+  MOE_LAUNCH_CHECK();
+  return MOE_STATUS_OK;
+}
+
+extern "C" int moe_nf4_quantize_bf16(const void *w_bf16, int64_t numel, int32_t blocksize,
+                                     const void *code16, void *packed_out, void *absmax_out,
+                                     void *stream) {
+  MOE_REQUIRE(numel >= 0 && numel % 2 == 0, "numel must be even and non-negative (got %lld)",
+              (long long)numel);
+  MOE_REQUIRE(blocksize >= 2 && blocksize <= 4096 && blocksize % 2 == 0,
+              "blocksize must be even and in [2, 4096] (got %d)", blocksize);
+  if (numel == 0) return MOE_STATUS_OK;
+  MOE_REQUIRE(w_bf16 && code16 && packed_out && absmax_out, "null device pointer");
+  const int64_t nblocks = (numel + blocksize - 1) / blocksize;
+  const int64_t grid = (nblocks + moe::kQuantThreads - 1) / moe::kQuantThreads;
+  MOE_REQUIRE(grid <= 0x7fffffff, "numel too large");
+  hipLaunchKernelGGL(moe::nf4_quantize_kernel, dim3((unsigned)grid), dim3(moe::kQuantThreads), 0,
+                     (hipStream_t)stream, (const uint16_t *)w_bf16, numel, blocksize,
+                     (const float *)code16, (uint8_t *)packed_out, (float *)absmax_out);
+  MOE_LAUNCH_CHECK();
+  return MOE_STATUS_OK;
+}

@@ -1,0 +1,90 @@
+"""Shared test helpers: oracle-quantised NF4 experts, device staging, bf16 bit views."""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from oracle import moe_oracle as orc
+
+
+def bits(t: torch.Tensor) -> np.ndarray:
+    """bf16 tensor (any device) -> numpy uint16 bit patterns."""
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def from_bits(a: np.ndarray, device="cpu") -> torch.Tensor:
+    a = np.ascontiguousarray(a, dtype=np.uint16)
+    return torch.from_numpy(a.view(np.int16)).view(torch.bfloat16).to(device)
+
+
+def quantize_np(w: torch.Tensor):
+    """bf16 CPU tensor -> (packed uint8 [n/2], absmax fp32) with the oracle quantiser."""
+    return orc.nf4_quantize(bits(w).reshape(-1))
+
+
+class NF4Expert:
+    """One expert quantised on the CPU by the oracle: numpy state + device copies."""
+
+    def __init__(self, w1: torch.Tensor, w3: torch.Tensor, w2: torch.Tensor):
+        self.inter, self.hidden = w1.shape
+        self.np = {"w1": quantize_np(w1), "w3": quantize_np(w3), "w2": quantize_np(w2)}
+        self.dev = None
+
+    def to(self, device):
+        code = torch.from_numpy(orc.NF4_CODE.copy()).to(device)
+        self.dev = {}
+        for name, (p, a) in self.np.items():
+            self.dev[name] = (torch.from_numpy(p.copy()).to(device),
+                              torch.from_numpy(a.copy()).to(device), code.clone())
+        return self
+
+    def c_struct(self):
+        from moeinfra_amd._lib import MoeNf4Expert
+
+        d = self.dev
+        return MoeNf4Expert(
+            d["w1"][0].data_ptr(), d["w1"][1].data_ptr(), d["w1"][2].data_ptr(),
+            d["w3"][0].data_ptr(), d["w3"][1].data_ptr(), d["w3"][2].data_ptr(),
+            d["w2"][0].data_ptr(), d["w2"][1].data_ptr(), d["w2"][2].data_ptr(),
+        )
+
+    def dequant_np(self):
+        return orc.dequant_expert(self.np, self.hidden, self.inter)
+
+
+def build_layer(hidden: int, inter: int, num_experts: int, tokens: int, seed: int):
+    """Seeded layer (gate, NF4 experts quantised by the oracle, activations), CPU-side."""
+    from moeinfra_amd import synth
+
+    gen = synth.make_generator(seed)
+    lw = synth.make_layer(hidden, inter, num_experts, gen,
+                          expert_sink=lambda e, w1, w3, w2: NF4Expert(w1, w3, w2))
+    x = synth.make_activations(tokens, hidden, gen)
+    return lw.gate, lw.experts, x
+
+
+def oracle_layer(gate: torch.Tensor, experts, x: torch.Tensor, k: int = 2, bias=None):
+    """Oracle MoE layer output (bf16 bits) and routing for oracle-quantised experts."""
+    cache = {}
+
+    def expert_fn(e, rows):
+        if e not in cache:
+            cache[e] = experts[e].dequant_np()
+        w1, w3, w2 = cache[e]
+        return orc.swiglu(rows, w1, w3, w2)
+
+    b = None if bias is None else bias.detach().cpu().numpy()
+    return orc.moe_layer(bits(x), bits(gate), expert_fn, k=k, bias=b)
+
+
+def near_tie_rows(logits_bits: np.ndarray, bias=None, k: int = 2) -> np.ndarray:
+    """Rows whose k-th and (k+1)-th largest fp32 logits are within 1 bf16 ulp."""
+    lf = orc.bf16_to_f32(logits_bits).astype(np.float64)
+    if bias is not None:
+        lf = lf + np.asarray(bias, dtype=np.float64)[None, :]
+    s = -np.sort(-lf, axis=-1)
+    if s.shape[1] <= k:
+        return np.zeros(s.shape[0], dtype=bool)
+    gap = s[:, k - 1] - s[:, k]
+    ulp = np.maximum(np.abs(s[:, k - 1]), 1e-30) * 2.0 ** -7
+    return gap <= ulp

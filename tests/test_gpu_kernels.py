@@ -1,0 +1,157 @@
+"""GPU parity of the individual kernels (K0-K5) against the CPU oracle."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import NF4Expert, bits, build_layer, from_bits, near_tie_rows, oracle_layer
+from oracle import moe_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+
+def _code(dev):
+    return torch.from_numpy(orc.NF4_CODE.copy()).to(dev)
+
+
+# ------------------------------------------------------------------------------ K1
+@pytest.mark.parametrize("numel", [64, 96, 4096 + 32 + 2, 3584 * 1024])
+def test_dequant_bitexact(cuda_device, numel):
+    from moeinfra_amd import ops
+
+    rng = np.random.default_rng(numel)
+    packed = rng.integers(0, 256, size=(numel + 1) // 2, dtype=np.uint8)
+    absmax = (rng.random((numel + 63) // 64, dtype=np.float32) * 0.1).astype(np.float32)
+    absmax[0] = 0.0
+    want = orc.nf4_dequant(packed, absmax, numel=numel)
+    got = ops.nf4_dequant(torch.from_numpy(packed).to(cuda_device),
+                          torch.from_numpy(absmax).to(cuda_device), _code(cuda_device), (numel,))
+    np.testing.assert_array_equal(bits(got), want)
+
+
+def test_dequant_full_expert_projection(cuda_device):
+    """One Mixtral-8x7B w1 [14336, 4096] from real quantised bf16 N(0, 0.02) weights."""
+    from moeinfra_amd import ops, synth
+
+    gen = synth.make_generator(2)
+    w = synth._normal((14336, 4096), gen, "cpu", 0.02)
+    packed, absmax = orc.nf4_quantize(bits(w).reshape(-1))
+    want = orc.nf4_dequant(packed, absmax)
+    got = ops.nf4_dequant(torch.from_numpy(packed).to(cuda_device),
+                          torch.from_numpy(absmax).to(cuda_device), _code(cuda_device),
+                          (14336, 4096))
+    np.testing.assert_array_equal(bits(got).reshape(-1), want)
+
+
+# ------------------------------------------------------------------------------ K0
+@pytest.mark.parametrize("shape", [(64, 64), (256, 1024), (3, 130)])
+def test_quantize_bitexact(cuda_device, shape):
+    from moeinfra_amd import ops, synth
+
+    gen = synth.make_generator(11)
+    w = synth._normal(shape, gen, "cpu", 0.02)
+    w.view(-1)[5] = 0.0
+    p_want, a_want = orc.nf4_quantize(bits(w).reshape(-1))
+    p_got, a_got, _ = ops.nf4_quantize(w.to(cuda_device))
+    np.testing.assert_array_equal(p_got.cpu().numpy().reshape(-1), p_want)
+    np.testing.assert_array_equal(a_got.cpu().numpy(), a_want)
+
+
+# ------------------------------------------------------------------------------ K2
+@pytest.mark.parametrize("T,H,E,skew", [(1, 4096, 8, False), (16, 1024, 8, False),
+                                        (40, 4096, 8, True), (513, 4096, 8, False),
+                                        (7, 256, 16, False)])
+def test_router_matches_oracle(cuda_device, T, H, E, skew):
+    from moeinfra_amd import ops, synth
+
+    gen = synth.make_generator(T * 31 + H)
+    gate = synth._normal((E, H), gen, "cpu", 0.02)
+    x = synth.make_activations(T, H, gen)
+    bias = synth.zipf_bias(E, seed=T) if skew else None
+    lg_want, w_want, i_want = orc.router(bits(x), bits(gate), k=2,
+                                         bias=None if bias is None else bias.numpy())
+    lg, w, idx = ops.router_topk(x.to(cuda_device), gate.to(cuda_device), 2,
+                                 bias=None if bias is None else bias.to(cuda_device))
+    lg_b = bits(lg).astype(np.int32)
+    # fp32 accumulation order differs from the oracle's; bf16 logits agree within 1 ulp.
+    assert np.abs(lg_b - lg_want.astype(np.int32)).max() <= 1
+    keep = ~near_tie_rows(lg_want, None if bias is None else bias.numpy())
+    assert keep.sum() >= max(1, T // 2)
+    np.testing.assert_array_equal(idx.cpu().numpy()[keep], i_want[keep])
+    np.testing.assert_allclose(w.cpu().numpy()[keep], w_want[keep], rtol=2e-5, atol=1e-6)
+    np.testing.assert_allclose(w.sum(-1).cpu().numpy(), 1.0, atol=1e-5)
+
+
+# ------------------------------------------------------------------------------ K3
+@pytest.mark.parametrize("T,E", [(1, 8), (16, 8), (600, 8), (4096, 8), (33, 32)])
+def test_permute_stable_grouping(cuda_device, T, E):
+    from moeinfra_amd import ops
+
+    rng = np.random.default_rng(T)
+    idx = np.stack([rng.choice(E, size=2, replace=False) for _ in range(T)]).astype(np.int32)
+    r = ops.permute(torch.from_numpy(idx).to(cuda_device), E)
+    flat = idx.reshape(-1)
+    order = np.argsort(flat, kind="stable")
+    counts = np.bincount(flat, minlength=E)
+    np.testing.assert_array_equal(r["counts"].cpu().numpy(), counts)
+    np.testing.assert_array_equal(r["offsets"].cpu().numpy(), np.concatenate([[0], np.cumsum(counts)]))
+    np.testing.assert_array_equal(r["perm_tok"].cpu().numpy(), order // 2)
+    pos = np.empty_like(order)
+    pos[order] = np.arange(order.size)
+    np.testing.assert_array_equal(r["slot_pos"].cpu().numpy(), pos)
+    act = r["active"].cpu().numpy()
+    present = np.nonzero(counts)[0]
+    assert act[0] == present.size
+    np.testing.assert_array_equal(act[1:1 + present.size], present)
+
+
+# ------------------------------------------------------------------------------ K4 + K5
+def _layer_case(dev, H, F, E, T, seed, skew=False):
+    from moeinfra_amd import ops, synth
+
+    gate, experts, x = build_layer(H, F, E, T, seed)
+    bias = synth.zipf_bias(E, seed) if skew else None
+    want, (lg_w, w_w, i_w) = oracle_layer(gate, experts, x, bias=bias)
+    for ex in experts:
+        ex.to(dev)
+    table = ops.expert_table([ex.c_struct() for ex in experts])
+    out, lg, w, idx = ops.layer_forward(table, E, gate.to(dev), x.to(dev), 2, F,
+                                        bias=None if bias is None else bias.to(dev),
+                                        want_logits=True)
+    torch.cuda.synchronize()
+    return want, i_w, bits(out), idx.cpu().numpy(), lg_w
+
+
+@pytest.mark.parametrize("H,F,E,T,seed,skew", [
+    (256, 512, 8, 16, 3, False),
+    (256, 512, 8, 1, 4, False),
+    (1024, 3584, 8, 16, 0, False),      # the reduced Mixtral layer
+    (512, 1024, 8, 37, 5, True),
+    (256, 768, 4, 5, 6, False),
+])
+def test_layer_matches_oracle(cuda_device, H, F, E, T, seed, skew):
+    want, i_want, got, i_got, lg = _layer_case(cuda_device, H, F, E, T, seed, skew)
+    tie = near_tie_rows(lg)
+    np.testing.assert_array_equal(i_got[~tie], i_want[~tie])
+    ok = ~tie
+    err = orc.rel_l2(orc.bf16_to_f32(got[ok]), orc.bf16_to_f32(want[ok]))
+    assert err <= 1e-2, err
+
+
+@pytest.mark.parametrize("T,H,F", [(1, 256, 512), (3, 1024, 3584), (20, 512, 768)])
+def test_single_expert_matches_oracle(cuda_device, T, H, F):
+    from moeinfra_amd import ops, synth
+
+    gen = synth.make_generator(T + H)
+    w1 = synth._normal((F, H), gen, "cpu", 0.02)
+    w3 = synth._normal((F, H), gen, "cpu", 0.02)
+    w2 = synth._normal((H, F), gen, "cpu", 0.02)
+    x = synth.make_activations(T, H, gen)
+    ex = NF4Expert(w1, w3, w2)
+    d1, d3, d2 = ex.dequant_np()
+    want = orc.swiglu(bits(x), d1, d3, d2)
+    ex.to(cuda_device)
+    got = ops.expert_swiglu(ex.c_struct(), x.to(cuda_device), H, F)
+    err = orc.rel_l2(orc.bf16_to_f32(bits(got)), orc.bf16_to_f32(want))
+    assert err <= 1e-2, err
