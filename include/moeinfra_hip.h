@@ -121,6 +121,19 @@ int moe_expert_ffn_nf4(const moe_nf4_expert_t *experts, int32_t E, const void *x
                        const void *offsets, const void *perm_tok, const void *active,
                        void *h_ws_bf16, void *ypart_f32, int32_t nsplit, void *stream);
 
+/* The two halves of moe_expert_ffn_nf4, for callers that interleave other work:
+ * gate/up (`gate = self.w1(x); up = self.w3(x); F.silu(gate) * up`,
+ * transfer/nf4_reconstruct.py:153-155) writes h; down (`self.w2(...)`, :155) reads h and
+ * writes the nsplit partial sums. */
+int moe_expert_gateup_nf4(const moe_nf4_expert_t *experts, int32_t E, const void *x_bf16,
+                          int64_t T, int32_t k, int32_t H, int32_t F, const void *counts,
+                          const void *offsets, const void *perm_tok, const void *active,
+                          void *h_ws_bf16, void *stream);
+int moe_expert_down_nf4(const moe_nf4_expert_t *experts, int32_t E, int64_t T, int32_t k,
+                        int32_t H, int32_t F, const void *counts, const void *offsets,
+                        const void *perm_tok, const void *active, const void *h_ws_bf16,
+                        void *ypart_f32, int32_t nsplit, void *stream);
+
 /* ---------------------------------------------------------------- K5: combine
  * out[t] = 0; for the k slots of token t in ascending expert order:
  *   y = bf16(sum_s ypart[s][slot_pos[t*k+j]]);  out[t] = bf16(out[t] + y * w[t,j])

@@ -46,6 +46,10 @@ SIGNATURES = {
     "moe_permute": ([_vp, _i64, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp], ctypes.c_int),
     "moe_expert_ffn_nf4": ([ctypes.POINTER(MoeNf4Expert), _i32, _vp, _i64, _i32, _i32, _i32,
                             _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp], ctypes.c_int),
+    "moe_expert_gateup_nf4": ([ctypes.POINTER(MoeNf4Expert), _i32, _vp, _i64, _i32, _i32, _i32,
+                               _vp, _vp, _vp, _vp, _vp, _vp], ctypes.c_int),
+    "moe_expert_down_nf4": ([ctypes.POINTER(MoeNf4Expert), _i32, _i64, _i32, _i32, _i32,
+                             _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp], ctypes.c_int),
     "moe_combine": ([_vp, _i32, _vp, _vp, _vp, _i64, _i32, _i32, _vp, _vp], ctypes.c_int),
     "moe_expert_workspace_bytes": ([_i64, _i32, _i32], ctypes.c_int64),
     "moe_expert_swiglu_nf4": ([ctypes.POINTER(MoeNf4Expert), _vp, _i64, _i32, _i32, _vp, _vp,

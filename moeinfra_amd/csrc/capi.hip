@@ -14,7 +14,7 @@ int launch_expert_ffn(const moe_nf4_expert_t *experts, int32_t E, const void *x,
                       int32_t k, int32_t H, int32_t F, const int32_t *counts,
                       const int32_t *offsets, const int32_t *perm_tok, const int32_t *active,
                       void *h_ws, void *ypart, int32_t nsplit, int64_t max_tokens_per_expert,
-                      hipStream_t stream);
+                      int phases, hipStream_t stream);
 int launch_combine(const void *ypart, int32_t nsplit, const void *weights, const void *idx_i32,
                    const void *slot_pos, int64_t T, int32_t k, int32_t H, void *out,
                    hipStream_t stream);
@@ -145,7 +145,7 @@ extern "C" int moe_layer_forward_nf4(const moe_nf4_expert_t *experts, int32_t E,
                               moe::at<int32_t>(workspace, w.perm_tok),
                               moe::at<int32_t>(workspace, w.active),
                               moe::at<void>(workspace, w.h), moe::at<void>(workspace, w.ypart),
-                              w.nsplit, T, s);
+                              w.nsplit, T, 3, s);
   if (rc != MOE_STATUS_OK) return rc;
   return moe::launch_combine(moe::at<void>(workspace, w.ypart), w.nsplit, weights_f32,
                              moe::at<int32_t>(workspace, w.idx32),
@@ -181,7 +181,7 @@ extern "C" int moe_expert_swiglu_nf4(const moe_nf4_expert_t *expert, const void 
                               moe::at<int32_t>(workspace, w.perm_tok),
                               moe::at<int32_t>(workspace, w.active),
                               moe::at<void>(workspace, w.h), moe::at<void>(workspace, w.ypart),
-                              w.nsplit, T, s);
+                              w.nsplit, T, 3, s);
   if (rc != MOE_STATUS_OK) return rc;
   return moe::launch_reduce_splits(moe::at<float>(workspace, w.ypart), w.nsplit, T * (int64_t)H,
                                    (uint16_t *)y_bf16, s);

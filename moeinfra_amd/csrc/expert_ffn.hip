@@ -25,101 +25,114 @@
 // The code value is rounded to bf16 before the absmax scaling (the scaling happens in
 // fp32 after the MFMA), so an effective weight is bf16(code)*absmax instead of
 // bf16(code*absmax): a relative difference below 2^-8 per weight.
-#include "common.h"
+#include "nf4_tile.h"
 
 namespace moe {
 namespace {
 
-constexpr int kFfnWaves = 4;
-constexpr int kFfnThreads = kFfnWaves * kWave;
-constexpr int kTableWords = 256 * 64;
-
-struct ExpertTable {
-  moe_nf4_expert_t e[MOE_MAX_EXPERTS];
+// ----------------------------------------------------------------------------- pipeline
+// Registers of one pipeline stage: U consecutive NF4 blocks of NP projections for the
+// lane's weight row (8 packed bytes each), their absmax, and the activations of the
+// lane's token row for MT token tiles.  A wave keeps D stages in flight: the loads of
+// stage i+D-1 are issued before stage i is consumed.
+template <int NP, int MT, int U>
+struct Stage {
+  uint2 q[NP][U];
+  float s[NP][U];
+  uint4 xa[MT][U][2];
 };
 
-struct Route {
-  const int32_t *counts;
-  const int32_t *offsets;
-  const int32_t *perm_tok;
-  const int32_t *active;
-};
-
-__device__ __forceinline__ bf16x8 as_bf16x8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
-  return __builtin_bit_cast(bf16x8, make_uint4(a, b, c, d));
-}
-__device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
-
-__device__ __forceinline__ uint32_t lds_lookup(const uint32_t *tbl, uint32_t byte_addr) {
-  return *reinterpret_cast<const uint32_t *>(reinterpret_cast<const char *>(tbl) + byte_addr);
-}
-
-// Eight packed bytes (values 2j, 2j+1 per byte) -> eight bf16 pairs.  `lane_const` is the
-// lane's replica byte offset (< 256); selector byte 1 takes packed byte j, byte 0 the
-// replica offset, bytes 2-3 are zero.
-__device__ __forceinline__ void lookup8(const uint32_t *tbl, uint2 q, uint32_t lane_const,
-                                        uint32_t out[8]) {
+// Activation rows of empty token slots point at a valid row: row m of an MFMA result
+// depends only on row m of A and such rows are never stored, so the loads need no branch
+// (a branch would make the compiler wait for the whole pipeline).
+template <int NP, int MT, int U>
+__device__ __forceinline__ void load_stage(Stage<NP, MT, U> &st, const uint8_t *const (&wq)[NP],
+                                           const float *const (&wa)[NP],
+                                           const uint16_t *const (&xr)[MT], int b) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    out[j] = lds_lookup(tbl, __builtin_amdgcn_perm(q.x, lane_const, 0x0c0c0400u + (j << 8)));
-    out[4 + j] = lds_lookup(tbl, __builtin_amdgcn_perm(q.y, lane_const, 0x0c0c0400u + (j << 8)));
-  }
-}
-
-// Loads the work item's codebooks and (re)builds the lookup table when they differ from
-// the resident ones.  Must be called by every thread of the workgroup; acts as a barrier.
-__device__ __forceinline__ void ensure_table(uint32_t *tbl, uint32_t *s_raw, float *s_code,
-                                             const float *code_lo, const float *code_hi,
-                                             bool &built) {
-  const int tid = threadIdx.x;
-  uint32_t mine = 0;
-  int diff = 0;
-  if (tid < 32) {
-    mine = __builtin_bit_cast(uint32_t, (tid < 16 ? code_lo : code_hi)[tid & 15]);
-    diff = !built || mine != s_raw[tid];
-  }
-  if (__syncthreads_or(diff)) {
-    if (tid < 32) {
-      s_raw[tid] = mine;
-      s_code[tid] = __builtin_bit_cast(float, mine);
+  for (int u = 0; u < U; ++u) {
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      st.q[p][u] = *reinterpret_cast<const uint2 *>(wq[p] + (size_t)(b + u) * 32);
+      st.s[p][u] = wa[p][b + u];
     }
-    __syncthreads();
-    for (int i = tid; i < kTableWords; i += kFfnThreads) {
-      const int v = i >> 6;                   // packed byte value
-      const int half = (i & 32) ? 16 : 0;     // replicas 32-63 use the second codebook
-      tbl[i] = pack_bf16x2(s_code[half + (v >> 4)], s_code[half + (v & 15)]);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const uint4 *px = reinterpret_cast<const uint4 *>(xr[mt] + (size_t)(b + u) * 64);
+      st.xa[mt][u][0] = px[0];
+      st.xa[mt][u][1] = px[1];
     }
-    __syncthreads();
-    built = true;
   }
 }
 
-__device__ __forceinline__ f32x4 mfma_block(bf16x8 a0, bf16x8 b0, bf16x8 a1, bf16x8 b1) {
-  f32x4 t = {0.0f, 0.0f, 0.0f, 0.0f};
-  t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b0, t, 0, 0, 0);
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1, t, 0, 0, 0);
+template <int NP, int MT, int U>
+__device__ __forceinline__ void compute_stage(const Stage<NP, MT, U> &st, const uint32_t *tbl,
+                                              const uint32_t (&lane_const)[NP],
+                                              f32x4 (&acc)[NP][MT]) {
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      uint32_t l[8];
+      lookup8(tbl, st.q[p][u], lane_const[p], l);
+      const bf16x8 b0 = as_bf16x8(l[0], l[1], l[2], l[3]);
+      const bf16x8 b1 = as_bf16x8(l[4], l[5], l[6], l[7]);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+        scale_acc(acc[p][mt],
+                  mfma_block(as_bf16x8(st.xa[mt][u][0]), b0, as_bf16x8(st.xa[mt][u][1]), b1),
+                  st.s[p][u]);
+    }
+  }
 }
 
-__device__ __forceinline__ void scale_acc(f32x4 &acc, const f32x4 &t, float s) {
-  acc[0] = fmaf(s, t[0], acc[0]);
-  acc[1] = fmaf(s, t[1], acc[1]);
-  acc[2] = fmaf(s, t[2], acc[2]);
-  acc[3] = fmaf(s, t[3], acc[3]);
+// Streams blocks [b_lo, b_hi) of the lane's weight row(s) through the D-stage pipeline.
+// Prefetches are unconditional: past the last full stage they re-read it (unused data).
+template <int NP, int MT, int U, int D>
+__device__ __forceinline__ void stream_blocks(const uint32_t *tbl, const uint8_t *const (&wq)[NP],
+                                              const float *const (&wa)[NP],
+                                              const uint16_t *const (&xr)[MT],
+                                              const uint32_t (&lane_const)[NP], int b_lo,
+                                              int b_hi, f32x4 (&acc)[NP][MT]) {
+  const int ns = (b_hi - b_lo) / U;
+  if (ns > 0) {
+    Stage<NP, MT, U> st[D];
+    const int last = b_lo + (ns - 1) * U;
+    int bl = b_lo;  // next stage to load
+#pragma unroll
+    for (int d = 0; d < D - 1; ++d) {
+      load_stage(st[d], wq, wa, xr, bl);
+      bl = bl + U < last ? bl + U : last;
+    }
+    for (int s0 = 0; s0 < ns; s0 += D) {
+#pragma unroll
+      for (int d = 0; d < D; ++d) {
+        load_stage(st[(d + D - 1) % D], wq, wa, xr, bl);
+        bl = bl + U < last ? bl + U : last;
+        if (s0 + d < ns) compute_stage(st[d], tbl, lane_const, acc);
+      }
+    }
+  }
+  for (int b = b_lo + ns * U; b < b_hi; ++b) {
+    Stage<NP, MT, 1> t;
+    load_stage(t, wq, wa, xr, b);
+    compute_stage(t, tbl, lane_const, acc);
+  }
 }
-
-__device__ __forceinline__ float silu_f32(float v) { return v / (1.0f + expf(-v)); }
 
 // ----------------------------------------------------------------------------- gate/up
-// Work item = (active expert, 16-row tile of w1/w3).  The four waves split H; the
-// workgroup reduces the four partial sums in LDS in a fixed order and writes
+// A workgroup item is a group of 4/wpt consecutive 16-row tiles of one active expert's
+// w1/w3; each tile is streamed by `wpt` waves that split H (wpt = 1: one wave streams
+// the whole row tile and no reduction is needed).  After a fixed-order reduction of the
+// K slices, the tile's rows of
 //   h[off_e + r][row] = bf16( bf16(silu(bf16(g))) * bf16(u) )
-// for the expert's rows r, in token tiles of 16*MT.
-template <int MT, int U>
+// are written for the expert's rows r, in token tiles of 16*MT.
+template <int MT, int U, int D>
 __global__ void __launch_bounds__(kFfnThreads, 2)
 gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x, int H, int F, Route rt,
-              uint16_t *__restrict__ h_ws) {
+              uint16_t *__restrict__ h_ws, int wpt) {
   __shared__ __attribute__((aligned(16))) uint32_t s_tbl[kTableWords];
-  __shared__ f32x4 s_red[kFfnWaves - 1][2][MT][kWave];
+  __shared__ f32x4 s_red[kFfnWaves][2][MT][kWave];
   __shared__ uint32_t s_raw[32];
   __shared__ float s_code[32];
 
@@ -128,160 +141,104 @@ gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x, int H, int 
   const int wave = tid >> 6;
   const int n = lane & 15;
   const int g = lane >> 4;
-  const int tiles = F >> 4;
   const int NB = H >> 6;
-  const int b_lo = NB * wave / kFfnWaves;
-  const int b_hi = NB * (wave + 1) / kFfnWaves;
-  const uint32_t lane1 = (uint32_t)(lane & 31) << 2;
-  const uint32_t lane3 = lane1 | 128u;
-  const int n_items = rt.active[0] * tiles;
+  const int tpw = kFfnWaves / wpt;
+  const int groups_e = (F >> 4) / tpw;
+  const int n_groups = rt.active[0] * groups_e;
+  const int ks = wave % wpt;
+  const int b_lo = NB * ks / wpt;
+  const int b_hi = NB * (ks + 1) / wpt;
+  const uint32_t lc1 = (uint32_t)(lane & 31) << 2;
+  const uint32_t lane_const[2] = {lc1, lc1 | 128u};
   bool built = false;
 
-  for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
-    const int e = rt.active[1 + item / tiles];
-    const int row0 = (item % tiles) << 4;
+  for (int grp = blockIdx.x; grp < n_groups; grp += gridDim.x) {
+    const int e = rt.active[1 + grp / groups_e];
     const moe_nf4_expert_t &ex = tab.e[e];
     if (ex.w1_packed == nullptr) continue;  // absent expert (uniform across the workgroup)
     ensure_table(s_tbl, s_raw, s_code, (const float *)ex.w1_code, (const float *)ex.w3_code,
                  built);
 
+    const int row0 = ((grp % groups_e) * tpw + wave / wpt) << 4;
     const int cnt = rt.counts[e];
     const int off = rt.offsets[e];
-    const uint8_t *w1 = (const uint8_t *)ex.w1_packed + (size_t)(row0 + n) * (H >> 1) + g * 8;
-    const uint8_t *w3 = (const uint8_t *)ex.w3_packed + (size_t)(row0 + n) * (H >> 1) + g * 8;
-    const float *a1 = (const float *)ex.w1_absmax + (size_t)(row0 + n) * NB;
-    const float *a3 = (const float *)ex.w3_absmax + (size_t)(row0 + n) * NB;
+    const size_t roff = (size_t)(row0 + n);
+    const uint8_t *const wq[2] = {(const uint8_t *)ex.w1_packed + roff * (H >> 1) + g * 8,
+                                  (const uint8_t *)ex.w3_packed + roff * (H >> 1) + g * 8};
+    const float *const wa[2] = {(const float *)ex.w1_absmax + roff * NB,
+                                (const float *)ex.w3_absmax + roff * NB};
 
     for (int tt = 0; tt < cnt; tt += 16 * MT) {
       const uint16_t *xr[MT];
-      bool ok[MT];
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         const int r = tt + mt * 16 + n;
-        ok[mt] = r < cnt;
-        const int tok = ok[mt] ? rt.perm_tok[off + r] : 0;
+        const int tok = rt.perm_tok[off + (r < cnt ? r : 0)];
         xr[mt] = x + (size_t)tok * H + g * 16;
       }
-      f32x4 acc1[MT], acc3[MT];
+      f32x4 acc[2][MT];
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        acc1[mt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        acc3[mt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-      }
+      for (int p = 0; p < 2; ++p)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[p][mt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-      int b = b_lo;
-      for (; b + U <= b_hi; b += U) {
-        uint2 q1[U], q3[U];
-        float s1[U], s3[U];
-        uint4 xa[U][MT][2];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          q1[u] = *reinterpret_cast<const uint2 *>(w1 + (size_t)(b + u) * 32);
-          q3[u] = *reinterpret_cast<const uint2 *>(w3 + (size_t)(b + u) * 32);
-          s1[u] = a1[b + u];
-          s3[u] = a3[b + u];
+      stream_blocks<2, MT, U, D>(s_tbl, wq, wa, xr, lane_const, b_lo, b_hi, acc);
+
+      if (wpt > 1) {
+        if (ks > 0) {
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt) {
-            if (ok[mt]) {
-              const uint4 *p = reinterpret_cast<const uint4 *>(xr[mt] + (b + u) * 64);
-              xa[u][mt][0] = p[0];
-              xa[u][mt][1] = p[1];
-            } else {
-              xa[u][mt][0] = make_uint4(0, 0, 0, 0);
-              xa[u][mt][1] = make_uint4(0, 0, 0, 0);
+            s_red[wave][0][mt][lane] = acc[0][mt];
+            s_red[wave][1][mt][lane] = acc[1][mt];
+          }
+        }
+        __syncthreads();
+        if (ks == 0) {
+          for (int w = 1; w < wpt; ++w) {
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+              const f32x4 gp = s_red[wave + w][0][mt][lane];
+              const f32x4 up = s_red[wave + w][1][mt][lane];
+#pragma unroll
+              for (int i = 0; i < 4; ++i) {
+                acc[0][mt][i] += gp[i];
+                acc[1][mt][i] += up[i];
+              }
             }
           }
         }
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          uint32_t l1[8], l3[8];
-          lookup8(s_tbl, q1[u], lane1, l1);
-          lookup8(s_tbl, q3[u], lane3, l3);
-          const bf16x8 b1a = as_bf16x8(l1[0], l1[1], l1[2], l1[3]);
-          const bf16x8 b1b = as_bf16x8(l1[4], l1[5], l1[6], l1[7]);
-          const bf16x8 b3a = as_bf16x8(l3[0], l3[1], l3[2], l3[3]);
-          const bf16x8 b3b = as_bf16x8(l3[4], l3[5], l3[6], l3[7]);
-#pragma unroll
-          for (int mt = 0; mt < MT; ++mt) {
-            const bf16x8 x0 = as_bf16x8(xa[u][mt][0]);
-            const bf16x8 x1 = as_bf16x8(xa[u][mt][1]);
-            scale_acc(acc1[mt], mfma_block(x0, b1a, x1, b1b), s1[u]);
-            scale_acc(acc3[mt], mfma_block(x0, b3a, x1, b3b), s3[u]);
-          }
-        }
       }
-      for (; b < b_hi; ++b) {
-        const uint2 q1 = *reinterpret_cast<const uint2 *>(w1 + (size_t)b * 32);
-        const uint2 q3 = *reinterpret_cast<const uint2 *>(w3 + (size_t)b * 32);
-        uint32_t l1[8], l3[8];
-        lookup8(s_tbl, q1, lane1, l1);
-        lookup8(s_tbl, q3, lane3, l3);
-        const bf16x8 b1a = as_bf16x8(l1[0], l1[1], l1[2], l1[3]);
-        const bf16x8 b1b = as_bf16x8(l1[4], l1[5], l1[6], l1[7]);
-        const bf16x8 b3a = as_bf16x8(l3[0], l3[1], l3[2], l3[3]);
-        const bf16x8 b3b = as_bf16x8(l3[4], l3[5], l3[6], l3[7]);
+      if (ks == 0) {
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
-          uint4 xa0 = make_uint4(0, 0, 0, 0), xa1 = make_uint4(0, 0, 0, 0);
-          if (ok[mt]) {
-            const uint4 *p = reinterpret_cast<const uint4 *>(xr[mt] + b * 64);
-            xa0 = p[0];
-            xa1 = p[1];
-          }
-          scale_acc(acc1[mt], mfma_block(as_bf16x8(xa0), b1a, as_bf16x8(xa1), b1b), a1[b]);
-          scale_acc(acc3[mt], mfma_block(as_bf16x8(xa0), b3a, as_bf16x8(xa1), b3b), a3[b]);
-        }
-      }
-
-      // Fixed-order reduction of the four K slices, then the SwiGLU epilogue.
-      if (wave > 0) {
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          s_red[wave - 1][0][mt][lane] = acc1[mt];
-          s_red[wave - 1][1][mt][lane] = acc3[mt];
-        }
-      }
-      __syncthreads();
-      if (wave == 0) {
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          f32x4 gs = acc1[mt], us = acc3[mt];
-#pragma unroll
-          for (int w = 0; w < kFfnWaves - 1; ++w) {
-            const f32x4 gp = s_red[w][0][mt][lane];
-            const f32x4 up = s_red[w][1][mt][lane];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              gs[i] += gp[i];
-              us[i] += up[i];
-            }
-          }
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int r = tt + mt * 16 + g * 4 + i;
             if (r < cnt) {
-              const float gb = bf16_to_f32(f32_to_bf16(gs[i]));
-              const float ub = bf16_to_f32(f32_to_bf16(us[i]));
+              const float gb = bf16_to_f32(f32_to_bf16(acc[0][mt][i]));
+              const float ub = bf16_to_f32(f32_to_bf16(acc[1][mt][i]));
               const float sb = bf16_to_f32(f32_to_bf16(silu_f32(gb)));
               h_ws[(size_t)(off + r) * F + row0 + n] = f32_to_bf16(sb * ub);
             }
           }
         }
       }
-      __syncthreads();
+      if (wpt > 1) __syncthreads();
     }
   }
 }
 
 // ----------------------------------------------------------------------------- down
-// Work item = (active expert, 16-row tile of w2, K slice).  Writes the fp32 partial
-//   ypart[ks][off_e + r][row] = sum over the slice of w2[row][k] * h[off_e + r][k].
-template <int MT, int U>
+// A workgroup item is (active expert, group of 4/wpt consecutive 16-row tiles of w2,
+// split sp of nsplit).  Each tile's K range (split sp) is streamed by `wpt` waves and
+// reduced in LDS in a fixed order; the result is written as the fp32 partial sum
+//   ypart[sp][off_e + r][row] = sum_{k in split sp} w2[row][k] * h[off_e + r][k].
+template <int MT, int U, int D>
 __global__ void __launch_bounds__(kFfnThreads, 2)
 down_kernel(const ExpertTable tab, int H, int F, Route rt, const uint16_t *__restrict__ h_ws,
-            float *__restrict__ ypart, int64_t rows_total, int nsplit) {
+            float *__restrict__ ypart, int64_t rows_total, int nsplit, int wpt) {
   __shared__ __attribute__((aligned(16))) uint32_t s_tbl[kTableWords];
-  __shared__ f32x4 s_red[kFfnWaves - 1][MT][kWave];
+  __shared__ f32x4 s_red[kFfnWaves][MT][kWave];
   __shared__ uint32_t s_raw[32];
   __shared__ float s_code[32];
 
@@ -290,169 +247,130 @@ down_kernel(const ExpertTable tab, int H, int F, Route rt, const uint16_t *__res
   const int wave = tid >> 6;
   const int n = lane & 15;
   const int g = lane >> 4;
-  const int tiles = H >> 4;
   const int NB = F >> 6;
-  const uint32_t lane2 = (uint32_t)lane << 2;
-  const int per_expert = tiles * nsplit;
-  const int n_items = rt.active[0] * per_expert;
+  const int tpw = kFfnWaves / wpt;
+  const int groups_e = (H >> 4) / tpw * nsplit;
+  const int n_groups = rt.active[0] * groups_e;
+  const int ks = wave % wpt;
+  const uint32_t lane_const[1] = {(uint32_t)lane << 2};
   bool built = false;
 
-  for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
-    const int e = rt.active[1 + item / per_expert];
-    const int rem = item % per_expert;
-    const int row0 = (rem / nsplit) << 4;
-    const int ks = rem % nsplit;
+  for (int grp = blockIdx.x; grp < n_groups; grp += gridDim.x) {
+    const int e = rt.active[1 + grp / groups_e];
     const moe_nf4_expert_t &ex = tab.e[e];
     if (ex.w2_packed == nullptr) continue;  // absent expert (uniform across the workgroup)
     ensure_table(s_tbl, s_raw, s_code, (const float *)ex.w2_code, (const float *)ex.w2_code,
                  built);
-
-    const int kb0 = NB * ks / nsplit;
-    const int kb1 = NB * (ks + 1) / nsplit;
-    const int b_lo = kb0 + (kb1 - kb0) * wave / kFfnWaves;
-    const int b_hi = kb0 + (kb1 - kb0) * (wave + 1) / kFfnWaves;
+    const int rem = grp % groups_e;
+    const int sp = rem % nsplit;
+    const int row0 = ((rem / nsplit) * tpw + wave / wpt) << 4;
+    const int slice = sp * wpt + ks;
+    const int nslice = nsplit * wpt;
+    const int b_lo = NB * slice / nslice;
+    const int b_hi = NB * (slice + 1) / nslice;
     const int cnt = rt.counts[e];
     const int off = rt.offsets[e];
-    const uint8_t *w2 = (const uint8_t *)ex.w2_packed + (size_t)(row0 + n) * (F >> 1) + g * 8;
-    const float *a2 = (const float *)ex.w2_absmax + (size_t)(row0 + n) * NB;
+    const size_t roff = (size_t)(row0 + n);
+    const uint8_t *const wq[1] = {(const uint8_t *)ex.w2_packed + roff * (F >> 1) + g * 8};
+    const float *const wa[1] = {(const float *)ex.w2_absmax + roff * NB};
 
     for (int tt = 0; tt < cnt; tt += 16 * MT) {
       const uint16_t *hr[MT];
-      bool ok[MT];
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         const int r = tt + mt * 16 + n;
-        ok[mt] = r < cnt;
-        hr[mt] = h_ws + (size_t)(off + (ok[mt] ? r : 0)) * F + g * 16;
+        hr[mt] = h_ws + (size_t)(off + (r < cnt ? r : 0)) * F + g * 16;
       }
-      f32x4 acc[MT];
+      f32x4 acc[1][MT];
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      for (int mt = 0; mt < MT; ++mt) acc[0][mt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-      int b = b_lo;
-      for (; b + U <= b_hi; b += U) {
-        uint2 q[U];
-        float s[U];
-        uint4 xa[U][MT][2];
+      stream_blocks<1, MT, U, D>(s_tbl, wq, wa, hr, lane_const, b_lo, b_hi, acc);
+
+      if (wpt > 1) {
+        if (ks > 0) {
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-          q[u] = *reinterpret_cast<const uint2 *>(w2 + (size_t)(b + u) * 32);
-          s[u] = a2[b + u];
+          for (int mt = 0; mt < MT; ++mt) s_red[wave][mt][lane] = acc[0][mt];
+        }
+        __syncthreads();
+        if (ks == 0) {
+          for (int w = 1; w < wpt; ++w) {
 #pragma unroll
-          for (int mt = 0; mt < MT; ++mt) {
-            if (ok[mt]) {
-              const uint4 *p = reinterpret_cast<const uint4 *>(hr[mt] + (size_t)(b + u) * 64);
-              xa[u][mt][0] = p[0];
-              xa[u][mt][1] = p[1];
-            } else {
-              xa[u][mt][0] = make_uint4(0, 0, 0, 0);
-              xa[u][mt][1] = make_uint4(0, 0, 0, 0);
+            for (int mt = 0; mt < MT; ++mt) {
+              const f32x4 yp = s_red[wave + w][mt][lane];
+#pragma unroll
+              for (int i = 0; i < 4; ++i) acc[0][mt][i] += yp[i];
             }
           }
         }
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          uint32_t l[8];
-          lookup8(s_tbl, q[u], lane2, l);
-          const bf16x8 ba = as_bf16x8(l[0], l[1], l[2], l[3]);
-          const bf16x8 bb = as_bf16x8(l[4], l[5], l[6], l[7]);
-#pragma unroll
-          for (int mt = 0; mt < MT; ++mt)
-            scale_acc(acc[mt],
-                      mfma_block(as_bf16x8(xa[u][mt][0]), ba, as_bf16x8(xa[u][mt][1]), bb), s[u]);
-        }
       }
-      for (; b < b_hi; ++b) {
-        const uint2 q = *reinterpret_cast<const uint2 *>(w2 + (size_t)b * 32);
-        uint32_t l[8];
-        lookup8(s_tbl, q, lane2, l);
-        const bf16x8 ba = as_bf16x8(l[0], l[1], l[2], l[3]);
-        const bf16x8 bb = as_bf16x8(l[4], l[5], l[6], l[7]);
+      if (ks == 0) {
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
-          uint4 xa0 = make_uint4(0, 0, 0, 0), xa1 = make_uint4(0, 0, 0, 0);
-          if (ok[mt]) {
-            const uint4 *p = reinterpret_cast<const uint4 *>(hr[mt] + (size_t)b * 64);
-            xa0 = p[0];
-            xa1 = p[1];
-          }
-          scale_acc(acc[mt], mfma_block(as_bf16x8(xa0), ba, as_bf16x8(xa1), bb), a2[b]);
-        }
-      }
-
-      if (wave > 0) {
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) s_red[wave - 1][mt][lane] = acc[mt];
-      }
-      __syncthreads();
-      if (wave == 0) {
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          f32x4 ys = acc[mt];
-#pragma unroll
-          for (int w = 0; w < kFfnWaves - 1; ++w) {
-            const f32x4 yp = s_red[w][mt][lane];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) ys[i] += yp[i];
-          }
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int r = tt + mt * 16 + g * 4 + i;
-            if (r < cnt) ypart[((size_t)ks * rows_total + off + r) * H + row0 + n] = ys[i];
+            if (r < cnt) ypart[((size_t)sp * rows_total + off + r) * H + row0 + n] = acc[0][mt][i];
           }
         }
       }
-      __syncthreads();
+      if (wpt > 1) __syncthreads();
     }
   }
 }
 
 // ----------------------------------------------------------------------------- combine
-// One workgroup per token; each thread handles 4 consecutive columns per step.
+// Workgroup (t, c) combines columns [1024c, 1024c + 1024) of token t; each thread owns
+// 4 consecutive columns.
 constexpr int kCombineThreads = 256;
+constexpr int kCombineCols = kCombineThreads * 4;
 
 __global__ void __launch_bounds__(kCombineThreads)
 combine_kernel(const float *__restrict__ ypart, int nsplit, int64_t rows_total,
                const float *__restrict__ wts, const int32_t *__restrict__ idx,
                const int32_t *__restrict__ slot_pos, int k, int H, uint16_t *__restrict__ out) {
   const int64_t t = blockIdx.x;
+  const int c = blockIdx.y * kCombineCols + threadIdx.x * 4;
+  if (c >= H) return;
   int ord[MOE_MAX_TOPK];
-  for (int j = 0; j < k; ++j) ord[j] = j;
+  int e_of[MOE_MAX_TOPK];
+  for (int j = 0; j < k; ++j) {
+    ord[j] = j;
+    e_of[j] = idx[t * k + j];
+  }
   // Ascending expert id (insertion sort; k is tiny).
   for (int j = 1; j < k; ++j) {
     const int cur = ord[j];
     int p = j - 1;
-    while (p >= 0 && idx[t * k + ord[p]] > idx[t * k + cur]) {
+    while (p >= 0 && e_of[ord[p]] > e_of[cur]) {
       ord[p + 1] = ord[p];
       --p;
     }
     ord[p + 1] = cur;
   }
   const size_t split_stride = (size_t)rows_total * H;
-  for (int c = threadIdx.x * 4; c < H; c += kCombineThreads * 4) {
-    float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int jj = 0; jj < k; ++jj) {
-      const int j = ord[jj];
-      const int pos = slot_pos[t * k + j];
-      if (pos < 0 || pos >= rows_total) continue;
-      const float w = wts[t * k + j];
-      float4 y = *reinterpret_cast<const float4 *>(ypart + (size_t)pos * H + c);
-      for (int s = 1; s < nsplit; ++s) {
-        const float4 v = *reinterpret_cast<const float4 *>(ypart + s * split_stride + (size_t)pos * H + c);
-        y.x += v.x;
-        y.y += v.y;
-        y.z += v.z;
-        y.w += v.w;
-      }
-      const float yv[4] = {y.x, y.y, y.z, y.w};
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float p = bf16_to_f32(f32_to_bf16(yv[i])) * w;  // bf16 expert output x fp32 weight
-        o[i] = bf16_to_f32(f32_to_bf16(o[i] + p));            // bf16 destination
-      }
+  float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int jj = 0; jj < k; ++jj) {
+    const int j = ord[jj];
+    const int pos = slot_pos[t * k + j];
+    if (pos < 0 || pos >= rows_total) continue;
+    const float w = wts[t * k + j];
+    float4 y = *reinterpret_cast<const float4 *>(ypart + (size_t)pos * H + c);
+    for (int s = 1; s < nsplit; ++s) {
+      const float4 v = *reinterpret_cast<const float4 *>(ypart + s * split_stride + (size_t)pos * H + c);
+      y.x += v.x;
+      y.y += v.y;
+      y.z += v.z;
+      y.w += v.w;
     }
-    *reinterpret_cast<uint2 *>(out + t * H + c) = make_uint2(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]));
+    const float yv[4] = {y.x, y.y, y.z, y.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float p = bf16_to_f32(f32_to_bf16(yv[i])) * w;  // bf16 expert output x fp32 weight
+      o[i] = bf16_to_f32(f32_to_bf16(o[i] + p));            // bf16 destination
+    }
   }
+  *reinterpret_cast<uint2 *>(out + t * H + c) = make_uint2(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]));
 }
 
 // Single-expert helpers: identity routing tables and the split reduction.
@@ -507,30 +425,38 @@ int token_tiles_for(int64_t max_tokens_per_expert) { return max_tokens_per_exper
 
 }  // namespace
 
-// Split of the down projection's K range so that small token counts still fill the chip.
+// Default number of cross-workgroup K splits of the down projection.  Inside a workgroup
+// four waves already split each w2 tile's K range, which fills the chip at batch 1, so a
+// single split (no partial sums to add in the combine) is the default.
 int choose_nsplit(int64_t T, int32_t k, int32_t E, int32_t H) {
-  const int64_t active_max = T * k < E ? T * k : E;
-  const int64_t items = active_max * (H / 16);
-  const int64_t target = 2048;
-  int64_t s = items > 0 ? (target + items - 1) / items : 1;
-  if (s < 1) s = 1;
-  if (s > 8) s = 8;
-  return (int)s;
+  (void)T;
+  (void)k;
+  (void)E;
+  (void)H;
+  return 1;
 }
 
+bool gemv4_supported(int64_t max_tokens_per_expert, int32_t H, int32_t F);
+int launch_gemv4(const void *tab, const void *x, int32_t H, int32_t F, const void *route,
+                 void *h_ws, void *ypart, int phases, int64_t active_max, hipStream_t stream);
+
+// phases: bit 0 = gate/up (x -> h), bit 1 = down (h -> ypart).  Up to 4 tokens per expert
+// use the 4x4x4 MFMA GEMV (expert_gemv4.hip); more use the 16x16x32 tiles below.
 int launch_expert_ffn(const moe_nf4_expert_t *experts, int32_t E, const void *x, int64_t T,
                       int32_t k, int32_t H, int32_t F, const int32_t *counts,
                       const int32_t *offsets, const int32_t *perm_tok, const int32_t *active,
                       void *h_ws, void *ypart, int32_t nsplit, int64_t max_tokens_per_expert,
-                      hipStream_t stream) {
+                      int phases, hipStream_t stream) {
   MOE_REQUIRE(E >= 1 && E <= MOE_MAX_EXPERTS, "num_experts must be in [1, %d]", MOE_MAX_EXPERTS);
   MOE_REQUIRE(H > 0 && H % 256 == 0, "hidden size must be a positive multiple of 256 (got %d)", H);
   MOE_REQUIRE(F > 0 && F % 256 == 0, "FFN size must be a positive multiple of 256 (got %d)", F);
   MOE_REQUIRE(nsplit >= 1 && nsplit <= 16, "nsplit must be in [1, 16]");
+  MOE_REQUIRE(k >= 1 && k <= MOE_MAX_TOPK, "top-k must be in [1, %d]", MOE_MAX_TOPK);
   MOE_REQUIRE(T >= 0 && T * k <= 0x7fffffff, "T out of range");
   if (T == 0) return MOE_STATUS_OK;
-  MOE_REQUIRE(experts && x && counts && offsets && perm_tok && active && h_ws && ypart,
-              "null pointer");
+  MOE_REQUIRE(experts && counts && offsets && perm_tok && active && h_ws, "null pointer");
+  MOE_REQUIRE(!(phases & 1) || x != nullptr, "null activations");
+  MOE_REQUIRE(!(phases & 2) || ypart != nullptr, "null ypart");
   MOE_REQUIRE(((uintptr_t)x % 16) == 0 && ((uintptr_t)h_ws % 16) == 0 &&
                   ((uintptr_t)ypart % 16) == 0,
               "x, h workspace and ypart must be 16-byte aligned");
@@ -550,25 +476,33 @@ int launch_expert_ffn(const moe_nf4_expert_t *experts, int32_t E, const void *x,
   const int64_t wg_cap = (int64_t)device_cu_count() * 2;
   const int mt = token_tiles_for(max_tokens_per_expert);
 
-  int64_t g1 = active_max * (F / 16);
+  if (nsplit == 1 && gemv4_supported(max_tokens_per_expert, H, F))
+    return launch_gemv4(&tab, x, H, F, &rt, h_ws, ypart, phases, active_max, stream);
+  const int wpt_gu = 1;  // a wave streams a whole w1/w3 row tile
+  const int wpt_dn = 4;  // four waves split each w2 row tile's K range
+  int64_t g1 = active_max * (F / 16) / (kFfnWaves / wpt_gu);
   if (g1 > wg_cap) g1 = wg_cap;
-  int64_t g2 = active_max * (H / 16) * nsplit;
+  int64_t g2 = active_max * (H / 16) / (kFfnWaves / wpt_dn) * nsplit;
   if (g2 > wg_cap) g2 = wg_cap;
   const dim3 blk(kFfnThreads);
-  if (mt == 1) {
-    hipLaunchKernelGGL((gateup_kernel<1, 4>), dim3((unsigned)g1), blk, 0, stream, tab,
-                       (const uint16_t *)x, H, F, rt, (uint16_t *)h_ws);
+  if (phases & 1) {
+    if (mt == 1)
+      hipLaunchKernelGGL((gateup_kernel<1, 2, 4>), dim3((unsigned)g1), blk, 0, stream, tab,
+                         (const uint16_t *)x, H, F, rt, (uint16_t *)h_ws, wpt_gu);
+    else
+      hipLaunchKernelGGL((gateup_kernel<2, 2, 2>), dim3((unsigned)g1), blk, 0, stream, tab,
+                         (const uint16_t *)x, H, F, rt, (uint16_t *)h_ws, wpt_gu);
     MOE_LAUNCH_CHECK();
-    hipLaunchKernelGGL((down_kernel<1, 4>), dim3((unsigned)g2), blk, 0, stream, tab, H, F, rt,
-                       (const uint16_t *)h_ws, (float *)ypart, rows_total, nsplit);
-  } else {
-    hipLaunchKernelGGL((gateup_kernel<2, 2>), dim3((unsigned)g1), blk, 0, stream, tab,
-                       (const uint16_t *)x, H, F, rt, (uint16_t *)h_ws);
-    MOE_LAUNCH_CHECK();
-    hipLaunchKernelGGL((down_kernel<2, 2>), dim3((unsigned)g2), blk, 0, stream, tab, H, F, rt,
-                       (const uint16_t *)h_ws, (float *)ypart, rows_total, nsplit);
   }
-  MOE_LAUNCH_CHECK();
+  if (phases & 2) {
+    if (mt == 1)
+      hipLaunchKernelGGL((down_kernel<1, 2, 4>), dim3((unsigned)g2), blk, 0, stream, tab, H, F,
+                         rt, (const uint16_t *)h_ws, (float *)ypart, rows_total, nsplit, wpt_dn);
+    else
+      hipLaunchKernelGGL((down_kernel<2, 2, 3>), dim3((unsigned)g2), blk, 0, stream, tab, H, F,
+                         rt, (const uint16_t *)h_ws, (float *)ypart, rows_total, nsplit, wpt_dn);
+    MOE_LAUNCH_CHECK();
+  }
   return MOE_STATUS_OK;
 }
 
@@ -583,7 +517,8 @@ int launch_combine(const void *ypart, int32_t nsplit, const void *weights, const
   MOE_REQUIRE(ypart && weights && idx_i32 && slot_pos && out, "null device pointer");
   MOE_REQUIRE(((uintptr_t)ypart % 16) == 0 && ((uintptr_t)out % 8) == 0,
               "ypart must be 16-byte and out 8-byte aligned");
-  hipLaunchKernelGGL(combine_kernel, dim3((unsigned)T), dim3(kCombineThreads), 0, stream,
+  const unsigned cgrid = (unsigned)((H + kCombineCols - 1) / kCombineCols);
+  hipLaunchKernelGGL(combine_kernel, dim3((unsigned)T, cgrid), dim3(kCombineThreads), 0, stream,
                      (const float *)ypart, nsplit, T * k, (const float *)weights,
                      (const int32_t *)idx_i32, (const int32_t *)slot_pos, k, H, (uint16_t *)out);
   MOE_LAUNCH_CHECK();
@@ -615,11 +550,32 @@ extern "C" int moe_expert_ffn_nf4(const moe_nf4_expert_t *experts, int32_t E, co
                                   int64_t T, int32_t k, int32_t H, int32_t F, const void *counts,
                                   const void *offsets, const void *perm_tok, const void *active,
                                   void *h_ws_bf16, void *ypart_f32, int32_t nsplit, void *stream) {
-  MOE_REQUIRE(k >= 1 && k <= MOE_MAX_TOPK, "top-k must be in [1, %d]", MOE_MAX_TOPK);
   return moe::launch_expert_ffn(experts, E, x_bf16, T, k, H, F, (const int32_t *)counts,
                                 (const int32_t *)offsets, (const int32_t *)perm_tok,
-                                (const int32_t *)active, h_ws_bf16, ypart_f32, nsplit, T,
+                                (const int32_t *)active, h_ws_bf16, ypart_f32, nsplit, T, 3,
                                 (hipStream_t)stream);
+}
+
+extern "C" int moe_expert_gateup_nf4(const moe_nf4_expert_t *experts, int32_t E,
+                                     const void *x_bf16, int64_t T, int32_t k, int32_t H,
+                                     int32_t F, const void *counts, const void *offsets,
+                                     const void *perm_tok, const void *active, void *h_ws_bf16,
+                                     void *stream) {
+  return moe::launch_expert_ffn(experts, E, x_bf16, T, k, H, F, (const int32_t *)counts,
+                                (const int32_t *)offsets, (const int32_t *)perm_tok,
+                                (const int32_t *)active, h_ws_bf16, nullptr, 1, T, 1,
+                                (hipStream_t)stream);
+}
+
+extern "C" int moe_expert_down_nf4(const moe_nf4_expert_t *experts, int32_t E, int64_t T,
+                                   int32_t k, int32_t H, int32_t F, const void *counts,
+                                   const void *offsets, const void *perm_tok, const void *active,
+                                   const void *h_ws_bf16, void *ypart_f32, int32_t nsplit,
+                                   void *stream) {
+  return moe::launch_expert_ffn(experts, E, nullptr, T, k, H, F, (const int32_t *)counts,
+                                (const int32_t *)offsets, (const int32_t *)perm_tok,
+                                (const int32_t *)active, const_cast<void *>(h_ws_bf16),
+                                ypart_f32, nsplit, T, 2, (hipStream_t)stream);
 }
 
 extern "C" int moe_combine(const void *ypart_f32, int32_t nsplit, const void *weights_f32,

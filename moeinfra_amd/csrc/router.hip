@@ -1,38 +1,43 @@
-// K2: gate linear + fp32 softmax + top-k + renormalise, one wavefront per token.
+// K2: gate linear + fp32 softmax + top-k + renormalise, one workgroup per token.
 //
 // Follows ExpertRouter.route_with_logits (engine/router.py:50-94):
 //   logits = bf16(x . gate^T)          F.linear in the activation dtype  (:66-69)
 //   p      = softmax(float(logits))    fp32                               (:81-84)
 //   w, idx = topk(p, k)                descending                         (:86-90)
 //   w     /= w.sum(-1)                                                    (:92)
-// The dot products accumulate in fp32 (each lane a strided slice of H, then a
-// butterfly reduction).  An optional fp32 per-expert bias is added to float(logits)
-// before the softmax (skewed-routing workloads).  Ties in p keep the lower index.
+// The dot products accumulate in fp32 (each thread a strided slice of H, then a
+// butterfly reduction per wave and a fixed-order sum over the waves).  An optional fp32
+// per-expert bias is added to float(logits) before the softmax (skewed-routing
+// workloads).  Ties in p keep the lower index.
 #include "common.h"
 
 namespace moe {
 namespace {
 
-constexpr int kRouterWaves = 4;
+constexpr int kRouterThreads = 256;
+constexpr int kRouterWaves = kRouterThreads / kWave;
 
+// One workgroup per token: the 256 threads split H (8 values per thread per step, 16-byte
+// loads of x and of every gate row), reduce within each wave and then across the four
+// waves in a fixed order; wave 0 finishes the softmax and top-k.
 template <int EMAX>
-__global__ void __launch_bounds__(kRouterWaves * kWave)
+__global__ void __launch_bounds__(kRouterThreads)
 router_topk_kernel(const uint16_t *__restrict__ x, const uint16_t *__restrict__ gate,
                    const float *__restrict__ bias, int64_t T, int H, int E, int k,
                    uint16_t *__restrict__ logits_out, float *__restrict__ w_out,
                    int64_t *__restrict__ idx_out, int32_t *__restrict__ idx32_out) {
-  const int lane = threadIdx.x & (kWave - 1);
-  const int64_t t = (int64_t)blockIdx.x * kRouterWaves + (threadIdx.x >> 6);
-  if (t >= T) return;
+  __shared__ float s_part[kRouterWaves][EMAX];
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = tid >> 6;
+  const int64_t t = blockIdx.x;
 
   float acc[EMAX];
 #pragma unroll
   for (int e = 0; e < EMAX; ++e) acc[e] = 0.0f;
 
   const uint16_t *xr = x + t * (int64_t)H;
-  // Each lane takes 8 consecutive values per 512-value chunk: 16-byte loads, and the
-  // wave reads each chunk of x and of every gate row contiguously.
-  for (int c = lane * 8; c < H; c += kWave * 8) {
+  for (int c = tid * 8; c < H; c += kRouterThreads * 8) {
     const uint4 xv = *reinterpret_cast<const uint4 *>(xr + c);
     const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
     float xf[8];
@@ -54,13 +59,25 @@ router_topk_kernel(const uint16_t *__restrict__ x, const uint16_t *__restrict__ 
       }
     }
   }
+#pragma unroll
+  for (int e = 0; e < EMAX; ++e) {
+    if (e < E) {
+      const float v = wave_sum(acc[e]);
+      if (lane == 0) s_part[wave][e] = v;
+    }
+  }
+  __syncthreads();
+  if (wave != 0) return;
 
   float p[EMAX];
   float m = -INFINITY;
 #pragma unroll
   for (int e = 0; e < EMAX; ++e) {
     if (e < E) {
-      const uint16_t lb = f32_to_bf16(wave_sum(acc[e]));
+      float v = s_part[0][e];
+#pragma unroll
+      for (int w = 1; w < kRouterWaves; ++w) v += s_part[w][e];
+      const uint16_t lb = f32_to_bf16(v);
       if (logits_out != nullptr && lane == e) logits_out[t * E + e] = lb;
       float l = bf16_to_f32(lb);
       if (bias != nullptr) l = l + bias[e];
@@ -130,9 +147,8 @@ extern "C" int moe_router_topk(const void *x_bf16, const void *gate_bf16, const 
   MOE_REQUIRE(x_bf16 && gate_bf16 && weights_f32 && idx_i64, "null device pointer");
   MOE_REQUIRE(((uintptr_t)x_bf16 % 16) == 0 && ((uintptr_t)gate_bf16 % 16) == 0,
               "x and gate must be 16-byte aligned");
-  const int64_t grid = (T + moe::kRouterWaves - 1) / moe::kRouterWaves;
-  MOE_REQUIRE(grid <= 0x7fffffff, "too many tokens");
-  const dim3 g((unsigned)grid), b(moe::kRouterWaves * moe::kWave);
+  MOE_REQUIRE(T <= 0x7fffffff, "too many tokens");
+  const dim3 g((unsigned)T), b(moe::kRouterThreads);
   hipStream_t s = (hipStream_t)stream;
   auto args = [&](auto kern) {
     hipLaunchKernelGGL(kern, g, b, 0, s, (const uint16_t *)x_bf16, (const uint16_t *)gate_bf16,

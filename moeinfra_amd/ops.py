@@ -163,11 +163,8 @@ def expert_table(experts: Sequence[Optional[MoeNf4Expert]]):
 
 
 def choose_nsplit(T: int, k: int, E: int, H: int) -> int:
-    """Mirror of the library's K-split choice for the down projection."""
-    active_max = min(T * k, E)
-    items = active_max * (H // 16)
-    s = -(-2048 // items) if items > 0 else 1
-    return max(1, min(8, s))
+    """Mirror of the library's default number of cross-workgroup K splits (one)."""
+    return 1
 
 
 def expert_ffn(table, num_experts: int, x: torch.Tensor, k: int, hidden: int, inter: int,

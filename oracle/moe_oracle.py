@@ -120,8 +120,10 @@ def bf16_to_f32(u) -> np.ndarray:
 
 # --------------------------------------------------------------------------- NF4
 def nf4_dequant(packed: np.ndarray, absmax: np.ndarray, code: np.ndarray = NF4_CODE,
-                numel: Optional[int] = None, blocksize: int = NF4_BLOCKSIZE) -> np.ndarray:
-    """Packed NF4 -> bf16 bit patterns (flat).  Restates nf4_oracle.c:oracle_nf4_dequant."""
+                numel: Optional[int] = None, blocksize: int = NF4_BLOCKSIZE,
+                threads: int = 1) -> np.ndarray:
+    """Packed NF4 -> bf16 bit patterns (flat) via nf4_oracle.c:oracle_nf4_dequant, optionally
+    split over ``threads`` host threads (the C call releases the GIL)."""
     packed = np.ascontiguousarray(packed, dtype=np.uint8).reshape(-1)
     absmax = np.ascontiguousarray(absmax, dtype=np.float32).reshape(-1)
     code = np.ascontiguousarray(code, dtype=np.float32).reshape(-1)
@@ -129,9 +131,26 @@ def nf4_dequant(packed: np.ndarray, absmax: np.ndarray, code: np.ndarray = NF4_C
         numel = packed.size * 2
     assert packed.size * 2 >= numel and absmax.size * blocksize >= numel and code.size == 16
     out = np.empty(numel, dtype=np.uint16)
-    rc = lib().oracle_nf4_dequant(_ptr(packed), _ptr(absmax), _ptr(code), numel, blocksize,
-                                  _ptr(out))
-    if rc != 0:
+    threads = max(1, int(threads))
+    # Chunks start on quantisation-block boundaries so each call sees whole blocks.
+    step = -(-numel // threads)
+    step = -(-step // (2 * blocksize)) * (2 * blocksize)
+    chunks = [(s, min(numel, s + step)) for s in range(0, numel, step)] or [(0, 0)]
+
+    def run(lo_hi):
+        lo, hi = lo_hi
+        return lib().oracle_nf4_dequant(
+            packed.ctypes.data + lo // 2, absmax.ctypes.data + (lo // blocksize) * 4,
+            _ptr(code), hi - lo, blocksize, out.ctypes.data + lo * 2)
+
+    if len(chunks) == 1:
+        rcs = [run(chunks[0])]
+    else:
+        from concurrent.futures import ThreadPoolExecutor
+
+        with ThreadPoolExecutor(max_workers=len(chunks)) as pool:
+            rcs = list(pool.map(run, chunks))
+    if any(rc != 0 for rc in rcs):
         raise ValueError("oracle_nf4_dequant rejected its arguments")
     return out
 
@@ -235,11 +254,13 @@ def swiglu(x: np.ndarray, w1: np.ndarray, w3: np.ndarray, w2: np.ndarray) -> np.
     return bf16_round(bf16_to_f32(h) @ bf16_to_f32(w2).T)
 
 
-def dequant_expert(state: dict, hidden: int, inter: int, code: np.ndarray = NF4_CODE):
+def dequant_expert(state: dict, hidden: int, inter: int, code: np.ndarray = NF4_CODE,
+                   threads: int = 1):
     """{'w1'|'w2'|'w3': (packed, absmax)} -> bf16 bits (w1 [F,H], w3 [F,H], w2 [H,F])."""
-    w1 = nf4_dequant(*state["w1"], code=code, numel=inter * hidden).reshape(inter, hidden)
-    w3 = nf4_dequant(*state["w3"], code=code, numel=inter * hidden).reshape(inter, hidden)
-    w2 = nf4_dequant(*state["w2"], code=code, numel=hidden * inter).reshape(hidden, inter)
+    n = inter * hidden
+    w1 = nf4_dequant(*state["w1"], code=code, numel=n, threads=threads).reshape(inter, hidden)
+    w3 = nf4_dequant(*state["w3"], code=code, numel=n, threads=threads).reshape(inter, hidden)
+    w2 = nf4_dequant(*state["w2"], code=code, numel=n, threads=threads).reshape(hidden, inter)
     return w1, w3, w2
 
 

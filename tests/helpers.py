@@ -25,13 +25,15 @@ def quantize_np(w: torch.Tensor):
 class NF4Expert:
     """One expert quantised on the CPU by the oracle: numpy state + device copies."""
 
-    def __init__(self, w1: torch.Tensor, w3: torch.Tensor, w2: torch.Tensor):
+    def __init__(self, w1: torch.Tensor, w3: torch.Tensor, w2: torch.Tensor, code=None):
         self.inter, self.hidden = w1.shape
-        self.np = {"w1": quantize_np(w1), "w3": quantize_np(w3), "w2": quantize_np(w2)}
+        self.code = orc.NF4_CODE if code is None else np.asarray(code, dtype=np.float32)
+        q = lambda w: orc.nf4_quantize(bits(w).reshape(-1), code=self.code)
+        self.np = {"w1": q(w1), "w3": q(w3), "w2": q(w2)}
         self.dev = None
 
     def to(self, device):
-        code = torch.from_numpy(orc.NF4_CODE.copy()).to(device)
+        code = torch.from_numpy(self.code.copy()).to(device)
         self.dev = {}
         for name, (p, a) in self.np.items():
             self.dev[name] = (torch.from_numpy(p.copy()).to(device),
@@ -49,16 +51,19 @@ class NF4Expert:
         )
 
     def dequant_np(self):
-        return orc.dequant_expert(self.np, self.hidden, self.inter)
+        return orc.dequant_expert(self.np, self.hidden, self.inter, code=self.code)
 
 
-def build_layer(hidden: int, inter: int, num_experts: int, tokens: int, seed: int):
-    """Seeded layer (gate, NF4 experts quantised by the oracle, activations), CPU-side."""
+def build_layer(hidden: int, inter: int, num_experts: int, tokens: int, seed: int,
+                codes=None):
+    """Seeded layer (gate, NF4 experts quantised by the oracle, activations), CPU-side.
+    ``codes`` optionally maps expert id -> a codebook to use instead of NF4."""
     from moeinfra_amd import synth
 
+    codes = codes or {}
     gen = synth.make_generator(seed)
     lw = synth.make_layer(hidden, inter, num_experts, gen,
-                          expert_sink=lambda e, w1, w3, w2: NF4Expert(w1, w3, w2))
+                          expert_sink=lambda e, w1, w3, w2: NF4Expert(w1, w3, w2, codes.get(e)))
     x = synth.make_activations(tokens, hidden, gen)
     return lw.gate, lw.experts, x
 

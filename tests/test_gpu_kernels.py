@@ -107,10 +107,10 @@ def test_permute_stable_grouping(cuda_device, T, E):
 
 
 # ------------------------------------------------------------------------------ K4 + K5
-def _layer_case(dev, H, F, E, T, seed, skew=False):
+def _layer_case(dev, H, F, E, T, seed, skew=False, codes=None):
     from moeinfra_amd import ops, synth
 
-    gate, experts, x = build_layer(H, F, E, T, seed)
+    gate, experts, x = build_layer(H, F, E, T, seed, codes=codes)
     bias = synth.zipf_bias(E, seed) if skew else None
     want, (lg_w, w_w, i_w) = oracle_layer(gate, experts, x, bias=bias)
     for ex in experts:
@@ -129,9 +129,25 @@ def _layer_case(dev, H, F, E, T, seed, skew=False):
     (1024, 3584, 8, 16, 0, False),      # the reduced Mixtral layer
     (512, 1024, 8, 37, 5, True),
     (256, 768, 4, 5, 6, False),
+    (512, 1024, 8, 2, 7, False),        # <= 4 tokens per expert: 4x4x4 MFMA GEMV
+    (1024, 3584, 8, 4, 8, True),
+    (512, 1536, 8, 3, 9, False),
 ])
 def test_layer_matches_oracle(cuda_device, H, F, E, T, seed, skew):
     want, i_want, got, i_got, lg = _layer_case(cuda_device, H, F, E, T, seed, skew)
+    tie = near_tie_rows(lg)
+    np.testing.assert_array_equal(i_got[~tie], i_want[~tie])
+    ok = ~tie
+    err = orc.rel_l2(orc.bf16_to_f32(got[ok]), orc.bf16_to_f32(want[ok]))
+    assert err <= 1e-2, err
+
+
+@pytest.mark.parametrize("H,F,T", [(512, 1024, 3), (256, 512, 12)])
+def test_layer_mixed_codebooks(cuda_device, H, F, T):
+    """Experts whose codebooks differ from the first active one (per-expert fallback)."""
+    codes = {e: (orc.NF4_CODE * np.float32(0.75 + 0.05 * e)).astype(np.float32)
+             for e in (1, 4, 6)}
+    want, i_want, got, i_got, lg = _layer_case(cuda_device, H, F, 8, T, 10 + T, codes=codes)
     tie = near_tie_rows(lg)
     np.testing.assert_array_equal(i_got[~tie], i_want[~tie])
     ok = ~tie
