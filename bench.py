@@ -2,15 +2,17 @@
 """Benchmark of the MI355X MoE expert path: Mixtral-8x7B-shaped NF4 experts, batch-1 decode.
 
 One step = one decode token (T=1 by default) through 32 MoE layers (hidden 4096, FFN 14336,
-8 NF4 experts per layer, top-2): router -> permute -> fused-dequant gate/up -> down ->
-combine on the HIP kernels, with every expert resident in HBM (32 x 8 x 99,090,432 B NF4).
+8 NF4 experts per layer, top-2), each a call of the library's whole-layer entry point
+(routing + grouping, fused-dequant gate/up, down + combine), with every expert resident in
+HBM (32 x 8 x 99,090,432 B NF4).
 Weights are synthetic bf16 N(0, 0.02) drawn on the GPU from a seed and NF4-quantised by the
 library's quantiser; activations are bf16 N(0, 1), a fixed input per layer.
 
 Prints ONE JSON line.  ``value`` is decode tokens/s of the 32-layer MoE path; ``roofline``
-is for the dominant kernel (the fused NF4 gate/up GEMV), timed with HIP events around each
-of its launches inside the timed region; ``cpu_baseline`` times the CPU oracle (C NF4
-dequant + numpy fp32 SwiGLU) on a bounded sample of the same layers.
+is for the dominant kernel (the fused NF4 gate/up GEMV), timed with HIP events that the
+profiled layer entry records around each of its launches inside the timed region;
+``cpu_baseline`` times the CPU oracle (C NF4 dequant + numpy fp32 SwiGLU) on a bounded
+sample of the same layers.
 """
 from __future__ import annotations
 
@@ -66,7 +68,7 @@ def layer_bytes(u: int, h: int, f: int, t: int, e: int) -> int:
 
 
 def main() -> int:
-    args = parse_args()
+    args = args_ns = parse_args()  # noqa: F841 (both names are used below)
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}, WORLD_SIZE {world}): "
@@ -109,90 +111,54 @@ def main() -> int:
     torch.cuda.synchronize()
     setup_s = time.time() - t_setup
 
-    # ------------------------------------------------------------------ per-layer buffers
+    # ------------------------------------------------------------------ buffers
     nsplit = ops.choose_nsplit(T, K, E, H)
-    i32 = dict(dtype=torch.int32, device=dev)
-    bufs = []
-    for l in range(L):
-        bufs.append({
-            "w": torch.empty((T, K), dtype=torch.float32, device=dev),
-            "idx": torch.empty((T, K), dtype=torch.int64, device=dev),
-            "idx32": torch.empty((T, K), **i32),
-            "counts": torch.empty((E,), **i32), "offsets": torch.empty((E + 1,), **i32),
-            "perm": torch.empty((T * K,), **i32), "slot": torch.empty((T * K,), **i32),
-            "active": torch.empty((E + 1,), **i32),
-            "h": torch.empty((T * K, F), dtype=torch.bfloat16, device=dev),
-            "ypart": torch.empty((nsplit, T * K, H), dtype=torch.float32, device=dev),
-            "out": torch.empty((T, H), dtype=torch.bfloat16, device=dev),
-        })
+    ws_bytes = lib.moe_layer_workspace_bytes(T, K, E, H, F)
+    ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=dev)
+    outs = [torch.empty((T, H), dtype=torch.bfloat16, device=dev) for _ in range(L)]
+    wts = [torch.empty((T, K), dtype=torch.float32, device=dev) for _ in range(L)]
+    idxs = [torch.empty((T, K), dtype=torch.int64, device=dev) for _ in range(L)]
     stream = torch.cuda.current_stream(dev).cuda_stream
     bias_ptr = None if bias is None else bias.data_ptr()
-
-    # Pre-bound argument tuples keep the host-side cost of a step to the ctypes calls.
-    calls = []
-    for l in range(L):
-        b, lay = bufs[l], layers[l]
-        calls.append((
-            (xs[l].data_ptr(), lay["gate"].data_ptr(), bias_ptr, T, H, E, K, None,
-             b["w"].data_ptr(), b["idx"].data_ptr(), b["idx32"].data_ptr(), stream),
-            (b["idx32"].data_ptr(), T, K, E, b["counts"].data_ptr(), b["offsets"].data_ptr(),
-             b["perm"].data_ptr(), b["slot"].data_ptr(), b["active"].data_ptr(), stream),
-            (lay["table"], E, xs[l].data_ptr(), T, K, H, F, b["counts"].data_ptr(),
-             b["offsets"].data_ptr(), b["perm"].data_ptr(), b["active"].data_ptr(),
-             b["h"].data_ptr(), stream),
-            (lay["table"], E, T, K, H, F, b["counts"].data_ptr(), b["offsets"].data_ptr(),
-             b["perm"].data_ptr(), b["active"].data_ptr(), b["h"].data_ptr(),
-             b["ypart"].data_ptr(), nsplit, stream),
-            (b["ypart"].data_ptr(), nsplit, b["w"].data_ptr(), b["idx32"].data_ptr(),
-             b["slot"].data_ptr(), T, K, H, b["out"].data_ptr(), stream),
-        ))
-    f_router, f_perm = lib.moe_router_topk, lib.moe_permute
-    f_gu, f_down, f_comb = lib.moe_expert_gateup_nf4, lib.moe_expert_down_nf4, lib.moe_combine
+    call_args = [(layers[l]["table"], E, layers[l]["gate"].data_ptr(), bias_ptr, xs[l].data_ptr(), T,
+             H, F, K, outs[l].data_ptr(), None, wts[l].data_ptr(), idxs[l].data_ptr(),
+             ws.data_ptr(), ws_bytes) for l in range(L)]
+    f_layer, f_prof = lib.moe_layer_forward_nf4, lib.moe_layer_forward_nf4_profiled
+    hip = _HipEvents() if not args_ns.no_kernel_events else None
 
     def step(ev=None):
         for l in range(L):
-            a_r, a_p, a_g, a_d, a_c = calls[l]
-            rc = f_router(*a_r) | f_perm(*a_p)
-            if ev is not None:
-                ev[l][0].record()
-            rc |= f_gu(*a_g)
-            if ev is not None:
-                ev[l][1].record()
-            rc |= f_down(*a_d)
-            if ev is not None:
-                ev[l][2].record()
-            rc |= f_comb(*a_c)
+            if ev is None:
+                rc = f_layer(*call_args[l], stream)
+            else:
+                rc = f_prof(*call_args[l], ev[l], stream)
             if rc:
-                _lib.check(-2 if rc < -1 else rc, "bench step")
+                _lib.check(rc, "moe_layer_forward_nf4")
 
-    for _ in range(args.warmup):
+    for _ in range(args_ns.warmup):
         step()
     torch.cuda.synchronize()
 
     # Routed experts per layer (inputs are fixed, so routing is the same every step).
-    u_per_layer = [int(torch.unique(bufs[l]["idx"]).numel()) for l in range(L)]
+    u_per_layer = [int(torch.unique(idxs[l]).numel()) for l in range(L)]
 
-    use_ev = not args.no_kernel_events
-    evs = ([[[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(L)]
-            for _ in range(args.steps)] if use_ev else None)
+    evs = ([[hip.array4() for _ in range(L)] for _ in range(args_ns.steps)] if hip else None)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for s in range(args.steps):
-        step(evs[s] if use_ev else None)
+    for s_ in range(args_ns.steps):
+        step(evs[s_] if hip else None)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    ms_per_step = elapsed * 1e3 / args.steps
+    ms_per_step = elapsed * 1e3 / args_ns.steps
 
     # ------------------------------------------------------------------ kernel times
-    gu_us = down_us = None
-    if use_ev:
-        gu = [evs[s][l][0].elapsed_time(evs[s][l][1]) for s in range(args.steps) for l in range(L)]
-        dn = [evs[s][l][1].elapsed_time(evs[s][l][2]) for s in range(args.steps) for l in range(L)]
-        gu_us = 1e3 * sum(gu) / len(gu)
-        down_us = 1e3 * sum(dn) / len(dn)
+    gu_us = down_us = route_us = None
+    if hip:
+        route_us = hip.mean_us([(e[0], e[1]) for st in evs for e in st])
+        gu_us = hip.mean_us([(e[1], e[2]) for st in evs for e in st])
+        down_us = hip.mean_us([(e[2], e[3]) for st in evs for e in st])
     u_mean = sum(u_per_layer) / L
     gu_bytes = sum(gateup_bytes(u, H, F, T, K) for u in u_per_layer) / L
-    dn_bytes = sum(down_bytes(u, H, F, T, K, nsplit) for u in u_per_layer) / L
     ly_bytes = sum(layer_bytes(u, H, F, T, E) for u in u_per_layer) / L
     layer_us = ms_per_step * 1e3 / L
     layer_gbps = ly_bytes / (layer_us * 1e-6) / 1e9
@@ -202,7 +168,7 @@ def main() -> int:
         ach = gu_bytes / (gu_us * 1e-6) / 1e9
         roofline = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBPS,
                     "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBPS, 4),
-                    "traffic": _traffic("gateup_nf4_decode_t%d" % T), "kernel": "gateup_kernel",
+                    "traffic": _traffic("gateup_nf4_decode_t%d" % T), "kernel": "gemv4_kernel<true> (gate/up)",
                     "bytes_per_launch": int(gu_bytes), "avg_launch_us": round(gu_us, 2)}
 
     # ------------------------------------------------------------------ CPU baseline
@@ -236,13 +202,48 @@ def main() -> int:
         "layer_hbm_gbps": round(layer_gbps, 1),
         "layer_hbm_frac": round(layer_gbps / HBM_PEAK_GBPS, 4),
         "routed_experts_per_layer": round(u_mean, 3),
-        "kernels_us": {"gateup": None if gu_us is None else round(gu_us, 2),
-                       "down": None if down_us is None else round(down_us, 2)},
-        "kernel_events_in_timed_region": use_ev,
+        "kernels_us": {"route": None if route_us is None else round(route_us, 2),
+                       "gateup": None if gu_us is None else round(gu_us, 2),
+                       "down_combine": None if down_us is None else round(down_us, 2)},
+        "kernel_events_in_timed_region": hip is not None,
         "setup_s": round(setup_s, 1),
     }
     print(json.dumps(result), flush=True)
     return 0
+
+
+class _HipEvents:
+    """Raw hipEvent_t handles (libamdhip64) for the profiled layer entry point."""
+
+    def __init__(self):
+        import ctypes
+
+        self.ct = ctypes
+        self.hip = ctypes.CDLL("libamdhip64.so")
+        self.hip.hipEventCreateWithFlags.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint]
+        self.hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p,
+                                                 ctypes.c_void_p]
+        self.hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+        self.all = []
+
+    def array4(self):
+        arr = (self.ct.c_void_p * 4)()
+        for i in range(4):
+            h = self.ct.c_void_p()
+            if self.hip.hipEventCreateWithFlags(self.ct.byref(h), 0) != 0:
+                raise RuntimeError("hipEventCreateWithFlags failed")
+            arr[i] = h
+            self.all.append(h)
+        return arr
+
+    def mean_us(self, pairs):
+        ms = self.ct.c_float()
+        tot = 0.0
+        for a, b in pairs:
+            if self.hip.hipEventElapsedTime(self.ct.byref(ms), a, b) != 0:
+                raise RuntimeError("hipEventElapsedTime failed")
+            tot += ms.value
+        return 1e3 * tot / len(pairs)
 
 
 def _traffic(name: str):

@@ -154,7 +154,9 @@ int moe_expert_swiglu_nf4(const moe_nf4_expert_t *expert, const void *x_bf16, in
 /* ---------------------------------------------------------------- whole layer
  * Router (K2) -> permute (K3) -> expert FFN (K4) -> combine (K5) in one call: the
  * device-resident form of MoELayer._forward_tokens (model/moe_layer.py:117-211) with
- * every routed expert resident.  experts[e] must be valid for every e < E that the
+ * every routed expert resident.  Batches of up to 16 tokens route and group in one
+ * kernel; with up to 4 tokens the combine runs inside the down projection, so a layer is
+ * three kernel launches.  experts[e] must be valid for every e < E that the
  * router can select.  logits_bf16 may be NULL; weights_f32 [T,k] and idx_i64 [T,k]
  * receive the routing.  workspace >= moe_layer_workspace_bytes(T, k, E, H, F). */
 int64_t moe_layer_workspace_bytes(int64_t T, int32_t k, int32_t E, int32_t H, int32_t F);
@@ -163,6 +165,16 @@ int moe_layer_forward_nf4(const moe_nf4_expert_t *experts, int32_t E, const void
                           int32_t F, int32_t k, void *out_bf16, void *logits_bf16,
                           void *weights_f32, void *idx_i64, void *workspace,
                           int64_t workspace_bytes, void *stream);
+
+/* moe_layer_forward_nf4 with hipEventRecord marks on the stream: events[0] before the
+ * routing, events[1] after routing + grouping, events[2] after gate/up, events[3] after
+ * down + combine.  The kernels are those of moe_layer_forward_nf4; for profiling. */
+int moe_layer_forward_nf4_profiled(const moe_nf4_expert_t *experts, int32_t E,
+                                   const void *gate_bf16, const void *bias_f32,
+                                   const void *x_bf16, int64_t T, int32_t H, int32_t F,
+                                   int32_t k, void *out_bf16, void *logits_bf16,
+                                   void *weights_f32, void *idx_i64, void *workspace,
+                                   int64_t workspace_bytes, void *const *events, void *stream);
 
 #ifdef __cplusplus
 }

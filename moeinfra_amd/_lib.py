@@ -57,6 +57,9 @@ SIGNATURES = {
     "moe_layer_workspace_bytes": ([_i64, _i32, _i32, _i32, _i32], ctypes.c_int64),
     "moe_layer_forward_nf4": ([ctypes.POINTER(MoeNf4Expert), _i32, _vp, _vp, _vp, _i64, _i32,
                                _i32, _i32, _vp, _vp, _vp, _vp, _vp, _i64, _vp], ctypes.c_int),
+    "moe_layer_forward_nf4_profiled": ([ctypes.POINTER(MoeNf4Expert), _i32, _vp, _vp, _vp, _i64,
+                                        _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _i64,
+                                        ctypes.POINTER(_vp), _vp], ctypes.c_int),
 }
 
 _lock = threading.Lock()

@@ -5,7 +5,7 @@
 
 #include <mutex>
 
-#include "common.h"
+#include "nf4_tile.h"
 
 namespace moe {
 
@@ -14,7 +14,13 @@ int launch_expert_ffn(const moe_nf4_expert_t *experts, int32_t E, const void *x,
                       int32_t k, int32_t H, int32_t F, const int32_t *counts,
                       const int32_t *offsets, const int32_t *perm_tok, const int32_t *active,
                       void *h_ws, void *ypart, int32_t nsplit, int64_t max_tokens_per_expert,
-                      int phases, hipStream_t stream);
+                      int phases, hipStream_t stream, const FusedCombine *fused);
+bool gemv4_supported(int64_t max_tokens_per_expert, int32_t H, int32_t F);
+bool route_small_supported(int64_t T, int32_t k);
+int launch_route_small(const void *x, const void *gate, const void *bias, int64_t T, int32_t H,
+                       int32_t E, int32_t k, void *logits, void *w, void *idx64, void *idx32,
+                       void *counts, void *offsets, void *perm_tok, void *slot_pos, void *active,
+                       void *zero_word, hipStream_t stream);
 int launch_combine(const void *ypart, int32_t nsplit, const void *weights, const void *idx_i32,
                    const void *slot_pos, int64_t T, int32_t k, int32_t H, void *out,
                    hipStream_t stream);
@@ -35,7 +41,7 @@ int64_t align_up(int64_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
 // Byte offsets of the layer workspace regions.
 struct LayerWs {
-  int64_t idx32, counts, offsets, perm_tok, slot_pos, active, h, ypart, total;
+  int64_t idx32, counts, offsets, perm_tok, slot_pos, active, counter, h, ypart, total;
   int nsplit;
 };
 
@@ -50,6 +56,7 @@ LayerWs layer_ws(int64_t T, int32_t k, int32_t E, int32_t H, int32_t F) {
   w.perm_tok = o; o = align_up(o + rows * 4);
   w.slot_pos = o; o = align_up(o + rows * 4);
   w.active = o;   o = align_up(o + (int64_t)(E + 1) * 4);
+  w.counter = o;  o = align_up(o + 4);
   w.h = o;        o = align_up(o + rows * (int64_t)F * 2);
   w.ypart = o;    o = align_up(o + (int64_t)w.nsplit * rows * H * 4);
   w.total = o;
@@ -116,40 +123,98 @@ extern "C" int64_t moe_layer_workspace_bytes(int64_t T, int32_t k, int32_t E, in
   return moe::layer_ws(T, k, E, H, F).total;
 }
 
+namespace moe {
+namespace {
+// Router -> grouping -> gate/up -> down -> combine.  Small batches use the fused routing
+// kernel and fold the combine into the down projection (three launches per layer).
+// `ev`, when given, receives hipEventRecord marks before the routing and after each of
+// the three phases (route, gate/up, down + combine).
+int layer_forward(const moe_nf4_expert_t *experts, int32_t E, const void *gate_bf16,
+                  const void *bias_f32, const void *x_bf16, int64_t T, int32_t H, int32_t F,
+                  int32_t k, void *out_bf16, void *logits_bf16, void *weights_f32, void *idx_i64,
+                  void *workspace, int64_t workspace_bytes, hipStream_t s, hipEvent_t *ev) {
+  MOE_REQUIRE(T >= 0 && k >= 1 && E >= 1 && H >= 1 && F >= 1, "bad sizes");
+  if (T == 0) return MOE_STATUS_OK;
+  MOE_REQUIRE(out_bf16 && weights_f32 && idx_i64, "null output pointer");
+  const LayerWs w = layer_ws(T, k, E, H, F);
+  MOE_REQUIRE(workspace != nullptr && workspace_bytes >= w.total,
+              "workspace too small: need %lld bytes, got %lld", (long long)w.total,
+              (long long)workspace_bytes);
+  MOE_REQUIRE(((uintptr_t)workspace % 256) == 0, "workspace must be 256-byte aligned");
+  int32_t *idx32 = at<int32_t>(workspace, w.idx32);
+  int32_t *counts = at<int32_t>(workspace, w.counts);
+  int32_t *offsets = at<int32_t>(workspace, w.offsets);
+  int32_t *perm_tok = at<int32_t>(workspace, w.perm_tok);
+  int32_t *slot_pos = at<int32_t>(workspace, w.slot_pos);
+  int32_t *active = at<int32_t>(workspace, w.active);
+  uint32_t *counter = at<uint32_t>(workspace, w.counter);
+  if (ev) MOE_HIP_CHECK(hipEventRecord(ev[0], s));
+  const bool small = route_small_supported(T, k);
+  int rc;
+  if (small) {
+    rc = launch_route_small(x_bf16, gate_bf16, bias_f32, T, H, E, k, logits_bf16, weights_f32,
+                            idx_i64, idx32, counts, offsets, perm_tok, slot_pos, active, counter,
+                            s);
+  } else {
+    rc = moe_router_topk(x_bf16, gate_bf16, bias_f32, T, H, E, k, logits_bf16, weights_f32,
+                         idx_i64, idx32, s);
+    if (rc == MOE_STATUS_OK)
+      rc = moe_permute(idx32, T, k, E, counts, offsets, perm_tok, slot_pos, active, s);
+  }
+  if (rc != MOE_STATUS_OK) return rc;
+  if (ev) MOE_HIP_CHECK(hipEventRecord(ev[1], s));
+  rc = launch_expert_ffn(experts, E, x_bf16, T, k, H, F, counts, offsets, perm_tok, active,
+                         at<void>(workspace, w.h), at<void>(workspace, w.ypart), w.nsplit, T, 1,
+                         s, nullptr);
+  if (rc != MOE_STATUS_OK) return rc;
+  if (ev) MOE_HIP_CHECK(hipEventRecord(ev[2], s));
+  // The down projection can also fold the combine into its last workgroup (FusedCombine);
+  // on MI355X the device-scope fences that needs cost more than the separate launch, so the
+  // layer uses the stand-alone combine kernel.
+  const bool fuse = false;
+  const FusedCombine fc{(const float *)weights_f32, idx32, slot_pos, (uint16_t *)out_bf16, counter,
+                        (int)T, k};
+  rc = launch_expert_ffn(experts, E, nullptr, T, k, H, F, counts, offsets, perm_tok, active,
+                         at<void>(workspace, w.h), at<void>(workspace, w.ypart), w.nsplit, T, 2,
+                         s, fuse ? &fc : nullptr);
+  if (rc != MOE_STATUS_OK) return rc;
+  if (!fuse) {
+    rc = launch_combine(at<void>(workspace, w.ypart), w.nsplit, weights_f32, idx32, slot_pos, T,
+                        k, H, out_bf16, s);
+    if (rc != MOE_STATUS_OK) return rc;
+  }
+  if (ev) MOE_HIP_CHECK(hipEventRecord(ev[3], s));
+  return MOE_STATUS_OK;
+}
+}  // namespace
+}  // namespace moe
+
 extern "C" int moe_layer_forward_nf4(const moe_nf4_expert_t *experts, int32_t E,
                                      const void *gate_bf16, const void *bias_f32,
                                      const void *x_bf16, int64_t T, int32_t H, int32_t F,
                                      int32_t k, void *out_bf16, void *logits_bf16,
                                      void *weights_f32, void *idx_i64, void *workspace,
                                      int64_t workspace_bytes, void *stream) {
-  MOE_REQUIRE(T >= 0 && k >= 1 && E >= 1 && H >= 1 && F >= 1, "bad sizes");
-  if (T == 0) return MOE_STATUS_OK;
-  const moe::LayerWs w = moe::layer_ws(T, k, E, H, F);
-  MOE_REQUIRE(workspace != nullptr && workspace_bytes >= w.total,
-              "workspace too small: need %lld bytes, got %lld", (long long)w.total,
-              (long long)workspace_bytes);
-  MOE_REQUIRE(((uintptr_t)workspace % 256) == 0, "workspace must be 256-byte aligned");
-  hipStream_t s = (hipStream_t)stream;
-  int rc = moe_router_topk(x_bf16, gate_bf16, bias_f32, T, H, E, k, logits_bf16, weights_f32,
-                           idx_i64, moe::at<int32_t>(workspace, w.idx32), stream);
-  if (rc != MOE_STATUS_OK) return rc;
-  rc = moe_permute(moe::at<int32_t>(workspace, w.idx32), T, k, E,
-                   moe::at<int32_t>(workspace, w.counts), moe::at<int32_t>(workspace, w.offsets),
-                   moe::at<int32_t>(workspace, w.perm_tok),
-                   moe::at<int32_t>(workspace, w.slot_pos), moe::at<int32_t>(workspace, w.active),
-                   stream);
-  if (rc != MOE_STATUS_OK) return rc;
-  rc = moe::launch_expert_ffn(experts, E, x_bf16, T, k, H, F,
-                              moe::at<int32_t>(workspace, w.counts),
-                              moe::at<int32_t>(workspace, w.offsets),
-                              moe::at<int32_t>(workspace, w.perm_tok),
-                              moe::at<int32_t>(workspace, w.active),
-                              moe::at<void>(workspace, w.h), moe::at<void>(workspace, w.ypart),
-                              w.nsplit, T, 3, s);
-  if (rc != MOE_STATUS_OK) return rc;
-  return moe::launch_combine(moe::at<void>(workspace, w.ypart), w.nsplit, weights_f32,
-                             moe::at<int32_t>(workspace, w.idx32),
-                             moe::at<int32_t>(workspace, w.slot_pos), T, k, H, out_bf16, s);
+  return moe::layer_forward(experts, E, gate_bf16, bias_f32, x_bf16, T, H, F, k, out_bf16,
+                            logits_bf16, weights_f32, idx_i64, workspace, workspace_bytes,
+                            (hipStream_t)stream, nullptr);
+}
+
+extern "C" int moe_layer_forward_nf4_profiled(const moe_nf4_expert_t *experts, int32_t E,
+                                              const void *gate_bf16, const void *bias_f32,
+                                              const void *x_bf16, int64_t T, int32_t H,
+                                              int32_t F, int32_t k, void *out_bf16,
+                                              void *logits_bf16, void *weights_f32,
+                                              void *idx_i64, void *workspace,
+                                              int64_t workspace_bytes, void *const *events,
+                                              void *stream) {
+  MOE_REQUIRE(events != nullptr && events[0] && events[1] && events[2] && events[3],
+              "four HIP events are required");
+  hipEvent_t ev[4] = {(hipEvent_t)events[0], (hipEvent_t)events[1], (hipEvent_t)events[2],
+                      (hipEvent_t)events[3]};
+  return moe::layer_forward(experts, E, gate_bf16, bias_f32, x_bf16, T, H, F, k, out_bf16,
+                            logits_bf16, weights_f32, idx_i64, workspace, workspace_bytes,
+                            (hipStream_t)stream, ev);
 }
 
 extern "C" int64_t moe_expert_workspace_bytes(int64_t T, int32_t H, int32_t F) {
@@ -181,7 +246,7 @@ extern "C" int moe_expert_swiglu_nf4(const moe_nf4_expert_t *expert, const void 
                               moe::at<int32_t>(workspace, w.perm_tok),
                               moe::at<int32_t>(workspace, w.active),
                               moe::at<void>(workspace, w.h), moe::at<void>(workspace, w.ypart),
-                              w.nsplit, T, 3, s);
+                              w.nsplit, T, 3, s, nullptr);
   if (rc != MOE_STATUS_OK) return rc;
   return moe::launch_reduce_splits(moe::at<float>(workspace, w.ypart), w.nsplit, T * (int64_t)H,
                                    (uint16_t *)y_bf16, s);

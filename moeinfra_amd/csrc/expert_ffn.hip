@@ -438,7 +438,8 @@ int choose_nsplit(int64_t T, int32_t k, int32_t E, int32_t H) {
 
 bool gemv4_supported(int64_t max_tokens_per_expert, int32_t H, int32_t F);
 int launch_gemv4(const void *tab, const void *x, int32_t H, int32_t F, const void *route,
-                 void *h_ws, void *ypart, int phases, int64_t active_max, hipStream_t stream);
+                 void *h_ws, void *ypart, int phases, int64_t active_max, int64_t rows_total,
+                 const void *fused_combine, hipStream_t stream);
 
 // phases: bit 0 = gate/up (x -> h), bit 1 = down (h -> ypart).  Up to 4 tokens per expert
 // use the 4x4x4 MFMA GEMV (expert_gemv4.hip); more use the 16x16x32 tiles below.
@@ -446,7 +447,7 @@ int launch_expert_ffn(const moe_nf4_expert_t *experts, int32_t E, const void *x,
                       int32_t k, int32_t H, int32_t F, const int32_t *counts,
                       const int32_t *offsets, const int32_t *perm_tok, const int32_t *active,
                       void *h_ws, void *ypart, int32_t nsplit, int64_t max_tokens_per_expert,
-                      int phases, hipStream_t stream) {
+                      int phases, hipStream_t stream, const FusedCombine *fused) {
   MOE_REQUIRE(E >= 1 && E <= MOE_MAX_EXPERTS, "num_experts must be in [1, %d]", MOE_MAX_EXPERTS);
   MOE_REQUIRE(H > 0 && H % 256 == 0, "hidden size must be a positive multiple of 256 (got %d)", H);
   MOE_REQUIRE(F > 0 && F % 256 == 0, "FFN size must be a positive multiple of 256 (got %d)", F);
@@ -477,7 +478,9 @@ int launch_expert_ffn(const moe_nf4_expert_t *experts, int32_t E, const void *x,
   const int mt = token_tiles_for(max_tokens_per_expert);
 
   if (nsplit == 1 && gemv4_supported(max_tokens_per_expert, H, F))
-    return launch_gemv4(&tab, x, H, F, &rt, h_ws, ypart, phases, active_max, stream);
+    return launch_gemv4(&tab, x, H, F, &rt, h_ws, ypart, phases, active_max, rows_total, fused,
+                        stream);
+  MOE_REQUIRE(fused == nullptr, "a fused combine needs the small-batch GEMV path");
   const int wpt_gu = 1;  // a wave streams a whole w1/w3 row tile
   const int wpt_dn = 4;  // four waves split each w2 row tile's K range
   int64_t g1 = active_max * (F / 16) / (kFfnWaves / wpt_gu);
@@ -553,7 +556,7 @@ extern "C" int moe_expert_ffn_nf4(const moe_nf4_expert_t *experts, int32_t E, co
   return moe::launch_expert_ffn(experts, E, x_bf16, T, k, H, F, (const int32_t *)counts,
                                 (const int32_t *)offsets, (const int32_t *)perm_tok,
                                 (const int32_t *)active, h_ws_bf16, ypart_f32, nsplit, T, 3,
-                                (hipStream_t)stream);
+                                (hipStream_t)stream, nullptr);
 }
 
 extern "C" int moe_expert_gateup_nf4(const moe_nf4_expert_t *experts, int32_t E,
@@ -564,7 +567,7 @@ extern "C" int moe_expert_gateup_nf4(const moe_nf4_expert_t *experts, int32_t E,
   return moe::launch_expert_ffn(experts, E, x_bf16, T, k, H, F, (const int32_t *)counts,
                                 (const int32_t *)offsets, (const int32_t *)perm_tok,
                                 (const int32_t *)active, h_ws_bf16, nullptr, 1, T, 1,
-                                (hipStream_t)stream);
+                                (hipStream_t)stream, nullptr);
 }
 
 extern "C" int moe_expert_down_nf4(const moe_nf4_expert_t *experts, int32_t E, int64_t T,
@@ -575,7 +578,7 @@ extern "C" int moe_expert_down_nf4(const moe_nf4_expert_t *experts, int32_t E, i
   return moe::launch_expert_ffn(experts, E, nullptr, T, k, H, F, (const int32_t *)counts,
                                 (const int32_t *)offsets, (const int32_t *)perm_tok,
                                 (const int32_t *)active, const_cast<void *>(h_ws_bf16),
-                                ypart_f32, nsplit, T, 2, (hipStream_t)stream);
+                                ypart_f32, nsplit, T, 2, (hipStream_t)stream, nullptr);
 }
 
 extern "C" int moe_combine(const void *ypart_f32, int32_t nsplit, const void *weights_f32,

@@ -253,10 +253,49 @@ __device__ __forceinline__ const float *code_hi(const moe_nf4_expert_t &ex) {
   return (const float *)(GATEUP ? ex.w3_code : ex.w2_code);
 }
 
+__device__ void combine_tokens(const FusedCombine &fc, const float *y, int H, int64_t rows) {
+  for (int t = 0; t < fc.T; ++t) {
+    int ord[MOE_MAX_TOPK];
+    int e_of[MOE_MAX_TOPK];
+    for (int j = 0; j < fc.k; ++j) {
+      ord[j] = j;
+      e_of[j] = fc.idx32[t * fc.k + j];
+    }
+    for (int j = 1; j < fc.k; ++j) {
+      const int cur = ord[j];
+      int p = j - 1;
+      while (p >= 0 && e_of[ord[p]] > e_of[cur]) {
+        ord[p + 1] = ord[p];
+        --p;
+      }
+      ord[p + 1] = cur;
+    }
+    for (int c = threadIdx.x * 4; c < H; c += kFfnThreads * 4) {
+      float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      for (int jj = 0; jj < fc.k; ++jj) {
+        const int j = ord[jj];
+        const int pos = fc.slot_pos[t * fc.k + j];
+        if (pos < 0 || pos >= rows) continue;
+        const float w = fc.weights[t * fc.k + j];
+        const float4 yv4 = *reinterpret_cast<const float4 *>(y + (size_t)pos * H + c);
+        const float yv[4] = {yv4.x, yv4.y, yv4.z, yv4.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float p = bf16_to_f32(f32_to_bf16(yv[i])) * w;
+          o[i] = bf16_to_f32(f32_to_bf16(o[i] + p));
+        }
+      }
+      *reinterpret_cast<uint2 *>(fc.out + (size_t)t * H + c) =
+          make_uint2(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]));
+    }
+  }
+}
+
 template <bool GATEUP, int DB, int DN>
 __global__ void __launch_bounds__(kFfnThreads, 2)
 gemv4_kernel(const ExpertTable tab, const uint16_t *__restrict__ act, int H, int F, Route rt,
-             uint16_t *__restrict__ h_out, float *__restrict__ y_out) {
+             uint16_t *__restrict__ h_out, float *__restrict__ y_out, FusedCombine fc,
+             int64_t rows_total) {
   __shared__ __attribute__((aligned(16))) uint32_t s_tbl[kTableWords];
   __shared__ float s_code[32];
   __shared__ float s_slow[kFfnWaves][32];
@@ -278,10 +317,11 @@ gemv4_kernel(const ExpertTable tab, const uint16_t *__restrict__ act, int H, int
       break;
     }
   }
-  if (e0 < 0) return;  // uniform: no present expert has tokens
-  const float *t_lo = code_lo<GATEUP>(tab.e[e0]);
-  const float *t_hi = code_hi<GATEUP>(tab.e[e0]);
-  const float t_mine = lane < 32 ? (lane < 16 ? t_lo : t_hi)[lane & 15] : 0.0f;
+  // e0 < 0 (no present expert has tokens): no tile work, but the workgroup still takes
+  // part in the completion count of a fused combine.
+  const float *t_lo = e0 >= 0 ? code_lo<GATEUP>(tab.e[e0]) : nullptr;
+  const float *t_hi = e0 >= 0 ? code_hi<GATEUP>(tab.e[e0]) : nullptr;
+  const float t_mine = (e0 >= 0 && lane < 32) ? (lane < 16 ? t_lo : t_hi)[lane & 15] : 0.0f;
 
   // Every wave calls this exactly once (it contains workgroup barriers): inside its
   // first tile stream, after the first loads are issued, or at the end if it has no work.
@@ -300,7 +340,7 @@ gemv4_kernel(const ExpertTable tab, const uint16_t *__restrict__ act, int H, int
   };
 
   // Balanced contiguous range of the flattened (active expert, 4-row tile) list.
-  const int64_t N = (int64_t)n_active * tiles_e;
+  const int64_t N = e0 >= 0 ? (int64_t)n_active * tiles_e : 0;
   const int64_t W = (int64_t)gridDim.x * kFfnWaves;
   const int64_t wid = (int64_t)blockIdx.x * kFfnWaves + wave;
   int64_t t = wid * N / W;
@@ -335,6 +375,18 @@ gemv4_kernel(const ExpertTable tab, const uint16_t *__restrict__ act, int H, int
       stream_tiles<GATEUP, DN, true, false>(ex, act, K, R, rt, e, tile0, ntiles, s_tbl, sc, h_out, y_out, build_table);
   }
   build_table();
+
+  if (!GATEUP && fc.out != nullptr) {
+    __shared__ uint32_t s_last;
+    __threadfence();  // publish this workgroup's y rows (device scope)
+    __syncthreads();
+    if (tid == 0) s_last = atomicAdd(fc.counter, 1u) == gridDim.x - 1;
+    __syncthreads();
+    if (s_last) {
+      __threadfence();  // every other workgroup's y rows are visible now
+      combine_tokens(fc, y_out, H, rows_total);
+    }
+  }
 }
 
 }  // namespace
@@ -344,22 +396,27 @@ bool gemv4_supported(int64_t max_tokens_per_expert, int32_t H, int32_t F) {
 }
 
 int launch_gemv4(const void *tab_ptr, const void *x, int32_t H, int32_t F, const void *route,
-                 void *h_ws, void *ypart, int phases, int64_t active_max, hipStream_t stream) {
+                 void *h_ws, void *ypart, int phases, int64_t active_max, int64_t rows_total,
+                 const void *fused_combine, hipStream_t stream) {
   const ExpertTable &tab = *static_cast<const ExpertTable *>(tab_ptr);
   const Route &rt = *static_cast<const Route *>(route);
+  FusedCombine fc{};
+  if (fused_combine != nullptr) fc = *static_cast<const FusedCombine *>(fused_combine);
   const int64_t cap = (int64_t)device_cu_count() * 2;
   if (phases & 1) {
     int64_t g = (active_max * (F / 4) + kFfnWaves - 1) / kFfnWaves;
     if (g > cap) g = cap;
     hipLaunchKernelGGL((gemv4_kernel<true, 6, 4>), dim3((unsigned)g), dim3(kFfnThreads), 0, stream,
-                       tab, (const uint16_t *)x, H, F, rt, (uint16_t *)h_ws, (float *)nullptr);
+                       tab, (const uint16_t *)x, H, F, rt, (uint16_t *)h_ws, (float *)nullptr,
+                       FusedCombine{}, rows_total);
     MOE_LAUNCH_CHECK();
   }
   if (phases & 2) {
     int64_t g = (active_max * (H / 4) + kFfnWaves - 1) / kFfnWaves;
     if (g > cap) g = cap;
     hipLaunchKernelGGL((gemv4_kernel<false, 8, 4>), dim3((unsigned)g), dim3(kFfnThreads), 0, stream,
-                       tab, (const uint16_t *)h_ws, H, F, rt, (uint16_t *)nullptr, (float *)ypart);
+                       tab, (const uint16_t *)h_ws, H, F, rt, (uint16_t *)nullptr, (float *)ypart,
+                       fc, rows_total);
     MOE_LAUNCH_CHECK();
   }
   return MOE_STATUS_OK;

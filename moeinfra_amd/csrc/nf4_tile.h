@@ -22,6 +22,19 @@ struct Route {
   const int32_t *active;
 };
 
+// Optional combine fused into the down projection: the last workgroup to finish computes
+// out[t] from the y rows of token t's k slots (ascending expert order, bf16 destination),
+// the work of the stand-alone combine kernel.
+struct FusedCombine {
+  const float *weights;     // [T, k]
+  const int32_t *idx32;     // [T, k]
+  const int32_t *slot_pos;  // [T*k]
+  uint16_t *out;            // [T, H] (null: no fused combine)
+  uint32_t *counter;        // zeroed before the launch
+  int T;
+  int k;
+};
+
 namespace {
 
 constexpr int kFfnWaves = 4;

@@ -14,6 +14,30 @@
 namespace moe {
 namespace {
 
+// One 8-value step of the gate products for every expert row.  All EMAX row loads are
+// issued before any product (rows e >= E re-read row E-1; their sums are discarded), so a
+// step costs one memory round trip.
+template <int EMAX>
+__device__ __forceinline__ void gate_step(const uint16_t *__restrict__ gate, int H, int E, int c,
+                                          const float (&xf)[8], float (&acc)[EMAX]) {
+  uint4 gv[EMAX];
+#pragma unroll
+  for (int e = 0; e < EMAX; ++e) {
+    const int ee = e < E ? e : E - 1;
+    gv[e] = *reinterpret_cast<const uint4 *>(gate + (int64_t)ee * H + c);
+  }
+  __builtin_amdgcn_sched_barrier(0);  // keep every load ahead of the products
+#pragma unroll
+  for (int e = 0; e < EMAX; ++e) {
+    const uint32_t gw[4] = {gv[e].x, gv[e].y, gv[e].z, gv[e].w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      acc[e] = fmaf(xf[2 * j], bf16lo_to_f32(gw[j]), acc[e]);
+      acc[e] = fmaf(xf[2 * j + 1], bf16hi_to_f32(gw[j]), acc[e]);
+    }
+  }
+}
+
 constexpr int kRouterThreads = 256;
 constexpr int kRouterWaves = kRouterThreads / kWave;
 
@@ -46,18 +70,7 @@ router_topk_kernel(const uint16_t *__restrict__ x, const uint16_t *__restrict__ 
       xf[2 * j] = bf16lo_to_f32(xw[j]);
       xf[2 * j + 1] = bf16hi_to_f32(xw[j]);
     }
-#pragma unroll
-    for (int e = 0; e < EMAX; ++e) {
-      if (e < E) {
-        const uint4 gv = *reinterpret_cast<const uint4 *>(gate + (int64_t)e * H + c);
-        const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          acc[e] = fmaf(xf[2 * j], bf16lo_to_f32(gw[j]), acc[e]);
-          acc[e] = fmaf(xf[2 * j + 1], bf16hi_to_f32(gw[j]), acc[e]);
-        }
-      }
-    }
+    gate_step<EMAX>(gate, H, E, c, xf, acc);
   }
 #pragma unroll
   for (int e = 0; e < EMAX; ++e) {
@@ -164,3 +177,181 @@ extern "C" int moe_router_topk(const void *x_bf16, const void *gate_bf16, const 
   MOE_LAUNCH_CHECK();
   return MOE_STATUS_OK;
 }
+
+// ----------------------------------------------------------------------------- K2+K3 fused
+// Decode-sized batches (T <= 16): routing and the expert grouping in one 1024-thread
+// workgroup.  Token t is handled by a group of 16/T waves that split H; the group's
+// partial logits are summed in a fixed order, then one thread per token finishes the
+// softmax / top-k exactly as router_topk_kernel does.  The grouping (stable counting
+// sort over the T*k slots) follows in the same workgroup, and `zero_word` (if given) is
+// cleared for a later kernel's completion counter.
+namespace moe {
+namespace {
+
+constexpr int kRouteThreads = 1024;
+constexpr int kRouteWaves = kRouteThreads / kWave;
+constexpr int kRouteMaxTokens = 16;
+
+template <int EMAX>
+__global__ void __launch_bounds__(kRouteThreads)
+route_small_kernel(const uint16_t *__restrict__ x, const uint16_t *__restrict__ gate,
+                   const float *__restrict__ bias, int T, int H, int E, int k,
+                   uint16_t *__restrict__ logits_out, float *__restrict__ w_out,
+                   int64_t *__restrict__ idx_out, int32_t *__restrict__ idx32_out,
+                   int32_t *__restrict__ counts, int32_t *__restrict__ offsets,
+                   int32_t *__restrict__ perm_tok, int32_t *__restrict__ slot_pos,
+                   int32_t *__restrict__ active, uint32_t *__restrict__ zero_word) {
+  __shared__ float s_part[kRouteWaves][EMAX];
+  __shared__ int32_t s_idx[kRouteMaxTokens * MOE_MAX_TOPK];
+  __shared__ int32_t s_off[MOE_MAX_EXPERTS + 1];
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = tid >> 6;
+  const int wpt = kRouteWaves / T;           // waves per token
+  const int t = wave / wpt;                  // this wave's token (t >= T: idle)
+  const int gtid = (wave - t * wpt) * kWave + lane;
+  const int gsize = wpt * kWave;
+
+  if (tid == 0 && zero_word != nullptr) *zero_word = 0u;
+
+  float acc[EMAX];
+#pragma unroll
+  for (int e = 0; e < EMAX; ++e) acc[e] = 0.0f;
+  if (t < T) {
+    const uint16_t *xr = x + (int64_t)t * H;
+    for (int c = gtid * 8; c < H; c += gsize * 8) {
+      const uint4 xv = *reinterpret_cast<const uint4 *>(xr + c);
+      const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
+      float xf[8];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        xf[2 * j] = bf16lo_to_f32(xw[j]);
+        xf[2 * j + 1] = bf16hi_to_f32(xw[j]);
+      }
+      gate_step<EMAX>(gate, H, E, c, xf, acc);
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < EMAX; ++e) {
+    const float v = wave_sum(acc[e]);
+    if (lane == 0) s_part[wave][e] = v;
+  }
+  __syncthreads();
+
+  if (tid < T) {
+    const int tt = tid;
+    float p[EMAX];
+    float m = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < EMAX; ++e) {
+      if (e < E) {
+        float v = s_part[tt * wpt][e];
+        for (int w = 1; w < wpt; ++w) v += s_part[tt * wpt + w][e];
+        const uint16_t lb = f32_to_bf16(v);
+        if (logits_out != nullptr) logits_out[(int64_t)tt * E + e] = lb;
+        float l = bf16_to_f32(lb);
+        if (bias != nullptr) l = l + bias[e];
+        p[e] = l;
+        m = fmaxf(m, l);
+      }
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int e = 0; e < EMAX; ++e) {
+      if (e < E) {
+        p[e] = expf(p[e] - m);
+        s += p[e];
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < EMAX; ++e)
+      if (e < E) p[e] = p[e] / s;
+    float topw[MOE_MAX_TOPK];
+    int topi[MOE_MAX_TOPK];
+    uint64_t taken = 0;
+    float wsum = 0.0f;
+    for (int j = 0; j < k; ++j) {
+      float best = -INFINITY;
+      int bi = -1;
+#pragma unroll
+      for (int e = 0; e < EMAX; ++e) {
+        if (e < E && !((taken >> e) & 1ull) && (bi < 0 || p[e] > best)) {
+          best = p[e];
+          bi = e;
+        }
+      }
+      taken |= 1ull << bi;
+      topw[j] = best;
+      topi[j] = bi;
+      wsum += best;
+    }
+    for (int j = 0; j < k; ++j) {
+      w_out[tt * k + j] = topw[j] / wsum;
+      idx_out[tt * k + j] = topi[j];
+      if (idx32_out != nullptr) idx32_out[tt * k + j] = topi[j];
+      s_idx[tt * k + j] = topi[j];
+    }
+  }
+  __syncthreads();
+
+  // Grouping: same outputs as permute_kernel (ascending expert, then ascending slot).
+  const int n_slots = T * k;
+  if (tid == 0) {
+    int run = 0, na = 0;
+    for (int e = 0; e < E; ++e) {
+      int c = 0;
+      for (int s = 0; s < n_slots; ++s) c += s_idx[s] == e;
+      counts[e] = c;
+      offsets[e] = run;
+      s_off[e] = run;
+      if (c > 0) active[1 + na++] = e;
+      run += c;
+    }
+    offsets[E] = run;
+    active[0] = na;
+    for (int e = na; e < E; ++e) active[1 + e] = -1;
+  }
+  __syncthreads();
+  if (tid < n_slots) {
+    const int e = s_idx[tid];
+    int rank = 0;
+    for (int s = 0; s < tid; ++s) rank += s_idx[s] == e;
+    const int pos = s_off[e] + rank;
+    perm_tok[pos] = tid / k;
+    slot_pos[tid] = pos;
+  }
+}
+
+}  // namespace
+
+bool route_small_supported(int64_t T, int32_t k) {
+  return T >= 1 && T <= kRouteMaxTokens && k <= MOE_MAX_TOPK;
+}
+
+int launch_route_small(const void *x, const void *gate, const void *bias, int64_t T, int32_t H,
+                       int32_t E, int32_t k, void *logits, void *w, void *idx64, void *idx32,
+                       void *counts, void *offsets, void *perm_tok, void *slot_pos, void *active,
+                       void *zero_word, hipStream_t stream) {
+  MOE_REQUIRE(route_small_supported(T, k), "fused routing needs 1 <= T <= %d", kRouteMaxTokens);
+  MOE_REQUIRE(H > 0 && H % 8 == 0, "hidden size must be a positive multiple of 8 (got %d)", H);
+  MOE_REQUIRE(E >= 1 && E <= MOE_MAX_EXPERTS && k >= 1 && k <= E, "bad E or k");
+  MOE_REQUIRE(((uintptr_t)x % 16) == 0 && ((uintptr_t)gate % 16) == 0,
+              "x and gate must be 16-byte aligned");
+  auto go = [&](auto kern) {
+    hipLaunchKernelGGL(kern, dim3(1), dim3(kRouteThreads), 0, stream, (const uint16_t *)x,
+                       (const uint16_t *)gate, (const float *)bias, (int)T, H, E, k,
+                       (uint16_t *)logits, (float *)w, (int64_t *)idx64, (int32_t *)idx32,
+                       (int32_t *)counts, (int32_t *)offsets, (int32_t *)perm_tok,
+                       (int32_t *)slot_pos, (int32_t *)active, (uint32_t *)zero_word);
+  };
+  if (E <= 8)
+    go(route_small_kernel<8>);
+  else if (E <= 16)
+    go(route_small_kernel<16>);
+  else
+    go(route_small_kernel<32>);
+  MOE_LAUNCH_CHECK();
+  return MOE_STATUS_OK;
+}
+
+}  // namespace moe
