@@ -9,8 +9,10 @@ Weights are synthetic bf16 N(0, 0.02) drawn on the GPU from a seed and NF4-quant
 library's quantiser; activations are bf16 N(0, 1), a fixed input per layer.
 
 Prints ONE JSON line.  ``value`` is decode tokens/s of the 32-layer MoE path; ``roofline``
-is for the dominant kernel (the fused NF4 gate/up GEMV), timed with HIP events that the
-profiled layer entry records around each of its launches inside the timed region;
+is for the dominant kernel (the fused NF4 gate/up GEMV), timed with HIP events inside the
+timed region: in each step one layer (layer s mod 32 at step s) goes through the profiled
+layer entry, which records timing-only events (no system-scope fence) between its launches,
+so every step carries four event records and the kernels' average covers all layers.
 ``cpu_baseline`` times the CPU oracle (C NF4 dequant + numpy fp32 SwiGLU) on a bounded
 sample of the same layers.
 """
@@ -126,12 +128,12 @@ def main() -> int:
     f_layer, f_prof = lib.moe_layer_forward_nf4, lib.moe_layer_forward_nf4_profiled
     hip = _HipEvents() if not args_ns.no_kernel_events else None
 
-    def step(ev=None):
+    def step(ev=None, prof_layer=-1):
         for l in range(L):
-            if ev is None:
+            if l != prof_layer:
                 rc = f_layer(*call_args[l], stream)
             else:
-                rc = f_prof(*call_args[l], ev[l], stream)
+                rc = f_prof(*call_args[l], ev, stream)
             if rc:
                 _lib.check(rc, "moe_layer_forward_nf4")
 
@@ -142,11 +144,14 @@ def main() -> int:
     # Routed experts per layer (inputs are fixed, so routing is the same every step).
     u_per_layer = [int(torch.unique(idxs[l]).numel()) for l in range(L)]
 
-    evs = ([[hip.array4() for _ in range(L)] for _ in range(args_ns.steps)] if hip else None)
+    evs = [hip.array4() for _ in range(args_ns.steps)] if hip else None
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for s_ in range(args_ns.steps):
-        step(evs[s_] if hip else None)
+        if hip:
+            step(evs[s_], s_ % L)
+        else:
+            step()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     ms_per_step = elapsed * 1e3 / args_ns.steps
@@ -154,11 +159,12 @@ def main() -> int:
     # ------------------------------------------------------------------ kernel times
     gu_us = down_us = route_us = None
     if hip:
-        route_us = hip.mean_us([(e[0], e[1]) for st in evs for e in st])
-        gu_us = hip.mean_us([(e[1], e[2]) for st in evs for e in st])
-        down_us = hip.mean_us([(e[2], e[3]) for st in evs for e in st])
+        route_us = hip.mean_us([(e[0], e[1]) for e in evs])
+        gu_us = hip.mean_us([(e[1], e[2]) for e in evs])
+        down_us = hip.mean_us([(e[2], e[3]) for e in evs])
     u_mean = sum(u_per_layer) / L
-    gu_bytes = sum(gateup_bytes(u, H, F, T, K) for u in u_per_layer) / L
+    prof_layers = [s_ % L for s_ in range(args_ns.steps)]
+    gu_bytes = sum(gateup_bytes(u_per_layer[l], H, F, T, K) for l in prof_layers) / len(prof_layers)
     ly_bytes = sum(layer_bytes(u, H, F, T, E) for u in u_per_layer) / L
     layer_us = ms_per_step * 1e3 / L
     layer_gbps = ly_bytes / (layer_us * 1e-6) / 1e9
@@ -213,7 +219,11 @@ def main() -> int:
 
 
 class _HipEvents:
-    """Raw hipEvent_t handles (libamdhip64) for the profiled layer entry point."""
+    """Raw hipEvent_t handles (libamdhip64) for the profiled layer entry point, created with
+    hipEventDisableSystemFence: timing-only events whose record skips the system-scope
+    cache write-back, so they perturb the launches they bracket as little as possible."""
+
+    DISABLE_SYSTEM_FENCE = 0x20000000
 
     def __init__(self):
         import ctypes
@@ -230,7 +240,7 @@ class _HipEvents:
         arr = (self.ct.c_void_p * 4)()
         for i in range(4):
             h = self.ct.c_void_p()
-            if self.hip.hipEventCreateWithFlags(self.ct.byref(h), 0) != 0:
+            if self.hip.hipEventCreateWithFlags(self.ct.byref(h), self.DISABLE_SYSTEM_FENCE) != 0:
                 raise RuntimeError("hipEventCreateWithFlags failed")
             arr[i] = h
             self.all.append(h)

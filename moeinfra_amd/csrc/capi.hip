@@ -28,6 +28,12 @@ int launch_identity_route(int64_t T, int32_t *counts, int32_t *offsets, int32_t 
                           int32_t *active, hipStream_t stream);
 int launch_reduce_splits(const float *ypart, int nsplit, int64_t numel, uint16_t *y,
                          hipStream_t stream);
+bool decode_layer_supported(int64_t T, int32_t k, int32_t E, int32_t H, int32_t F);
+int64_t decode_route_bytes();
+int launch_decode_layer(const moe_nf4_expert_t *experts, int32_t E, const void *gate,
+                        const void *bias, const void *x, int64_t T, int32_t H, int32_t F,
+                        int32_t k, void *out, void *logits, void *weights, void *idx64,
+                        void *route_ws, void *h_ws, hipStream_t s, hipEvent_t *ev);
 
 namespace {
 thread_local char g_last_error[512] = "";
@@ -41,7 +47,7 @@ int64_t align_up(int64_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
 // Byte offsets of the layer workspace regions.
 struct LayerWs {
-  int64_t idx32, counts, offsets, perm_tok, slot_pos, active, counter, h, ypart, total;
+  int64_t idx32, counts, offsets, perm_tok, slot_pos, active, counter, droute, h, ypart, total;
   int nsplit;
 };
 
@@ -57,6 +63,7 @@ LayerWs layer_ws(int64_t T, int32_t k, int32_t E, int32_t H, int32_t F) {
   w.slot_pos = o; o = align_up(o + rows * 4);
   w.active = o;   o = align_up(o + (int64_t)(E + 1) * 4);
   w.counter = o;  o = align_up(o + 4);
+  w.droute = o;   o = align_up(o + decode_route_bytes());
   w.h = o;        o = align_up(o + rows * (int64_t)F * 2);
   w.ypart = o;    o = align_up(o + (int64_t)w.nsplit * rows * H * 4);
   w.total = o;
@@ -125,8 +132,9 @@ extern "C" int64_t moe_layer_workspace_bytes(int64_t T, int32_t k, int32_t E, in
 
 namespace moe {
 namespace {
-// Router -> grouping -> gate/up -> down -> combine.  Small batches use the fused routing
-// kernel and fold the combine into the down projection (three launches per layer).
+// Decode batches (T <= 4, T*k <= 8, E <= 16) run the two-launch decode layer (routing in
+// the gate/up kernel, combine in the down kernel).  Otherwise: router -> grouping ->
+// gate/up -> down -> combine, with the fused routing + grouping kernel for T <= 16.
 // `ev`, when given, receives hipEventRecord marks before the routing and after each of
 // the three phases (route, gate/up, down + combine).
 int layer_forward(const moe_nf4_expert_t *experts, int32_t E, const void *gate_bf16,
@@ -148,6 +156,10 @@ int layer_forward(const moe_nf4_expert_t *experts, int32_t E, const void *gate_b
   int32_t *slot_pos = at<int32_t>(workspace, w.slot_pos);
   int32_t *active = at<int32_t>(workspace, w.active);
   uint32_t *counter = at<uint32_t>(workspace, w.counter);
+  if (decode_layer_supported(T, k, E, H, F))
+    return launch_decode_layer(experts, E, gate_bf16, bias_f32, x_bf16, T, H, F, k, out_bf16,
+                               logits_bf16, weights_f32, idx_i64, at<void>(workspace, w.droute),
+                               at<void>(workspace, w.h), s, ev);
   if (ev) MOE_HIP_CHECK(hipEventRecord(ev[0], s));
   const bool small = route_small_supported(T, k);
   int rc;

@@ -1,0 +1,739 @@
+// Decode MoE layer in two launches: routing fused into the NF4 gate/up GEMV, and the
+// weighted combine fused into the NF4 down GEMV.  For T <= 4 tokens with T*k <= 8 routed
+// slots and E <= 16 experts (Mixtral decode: T = 1, k = 2, E = 8).
+//
+// Why: at batch 1 a Mixtral layer streams ~198 MB of NF4 weights; every extra kernel
+// boundary costs a few microseconds (cache write-back/invalidate, ramp-up), and any
+// chain of dependent global loads before a workgroup's first weight load delays the
+// whole stream by one memory round trip per link.  So:
+//
+//  decode_gateup_kernel  every workgroup recomputes the routing of the <= 4 tokens (the
+//    gate is 64 KB and stays in L2): logits = bf16(x . gate^T) with fp32 accumulation,
+//    fp32 softmax (+ optional per-expert bias), top-k (descending, ties keep the lower
+//    index), renormalised weights, then the grouping of the T*k slots by expert
+//    (engine/router.py:50-94, model/moe_layer.py:142-191).  The workgroup then streams
+//    its share of the (active expert, 4-row tile) list of w1/w3 and writes
+//    h = bf16(silu(bf16(w1 x)) * bf16(w3 x)) per routed row.  Workgroup 0 publishes the
+//    routing outputs and a compact descriptor (DecodeRoute) for the down kernel.
+//
+//  decode_down_kernel  one descriptor load, then each workgroup owns whole 4-row tiles
+//    of the output and runs them for every active expert, its four waves splitting K
+//    into quarters; the quarters meet in LDS, each expert's row value is rounded to bf16
+//    (the expert's output dtype) and the slots of each token are combined in ascending
+//    expert order, o = bf16(o + bf16(y_e) * w_e) (model/moe_layer.py:147,187-191).
+//
+// Both kernels stream 4-row tiles through the D-stage register pipeline of the
+// 4x4x4 MFMA GEMV (gemv4_core.h), with the NF4 codebook table in LDS.
+#include "gemv4_core.h"
+
+namespace moe {
+
+constexpr int kDecMaxTokens = 4;
+constexpr int kDecMaxSlots = 8;
+constexpr int kDecMaxExperts = 16;
+constexpr int kDecMaxTilesPerWg = 4;
+
+// Routing of one decode step, written by workgroup 0 of the gate/up kernel and read by
+// the down kernel.  "Active" experts are those with at least one routed slot, in
+// ascending expert order; slot s = t*k + j is the j-th choice of token t.
+struct DecodeRoute {
+  int32_t n_active;
+  int32_t bc;     // every active expert has exactly one token
+  int32_t slow1;  // an active expert's w1/w3 codebook differs from the first one's
+  int32_t slow2;  // same for w2
+  int32_t active[kDecMaxSlots];    // expert id of each active index
+  int32_t counts[kDecMaxSlots];    // tokens of each active expert
+  int32_t offsets[kDecMaxSlots];   // first h row of each active expert
+  int32_t perm_tok[kDecMaxSlots];  // token of each h row
+  int32_t slot_a[kDecMaxSlots];    // active index of each slot's expert
+  int32_t slot_m[kDecMaxSlots];    // position of the slot's token within its expert's rows
+  float slot_w[kDecMaxSlots];      // renormalised routing weight of each slot
+  float code2[kDecMaxSlots][16];   // w2 codebook of each active expert
+};
+static_assert(sizeof(DecodeRoute) % 16 == 0, "descriptor is copied in 16-byte words");
+constexpr int kRouteWords = (int)(sizeof(DecodeRoute) / 4);
+static_assert(kRouteWords <= kFfnThreads, "one descriptor word per thread");
+
+namespace {
+
+// Global-memory pointer types.  Pointers read back from LDS are generic to the compiler,
+// and generic (flat) loads count against the LDS wait counter too, which would serialise
+// the table lookups behind the weight stream; these casts keep the loads global.
+#define MOE_GLOBAL __attribute__((address_space(1)))
+typedef const MOE_GLOBAL uint8_t *gq_t;
+typedef const MOE_GLOBAL float *ga_t;
+typedef const MOE_GLOBAL uint16_t *gx_t;
+
+typedef __attribute__((ext_vector_type(4))) unsigned int u32x4_t;
+__device__ __forceinline__ uint4 ld_u4(const MOE_GLOBAL void *p) {
+  const u32x4_t v = *static_cast<const MOE_GLOBAL u32x4_t *>(p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// A pointer read from a wave-uniform address, kept in scalar registers (so that lanes can
+// select among several such pointers without turning the reads into per-lane loads).
+__device__ __forceinline__ const void *uniform_ptr(const void *const &field) {
+  const uint64_t v = reinterpret_cast<uint64_t>(field);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return reinterpret_cast<const void *>(((uint64_t)hi << 32) | lo);
+}
+
+// Pointers of one pipeline item: NP weight streams (packed bytes and absmax of the lane's
+// row, already offset to the item's first stage) and the lane's activation chunk.
+template <int NP>
+struct ItemPtr {
+  gq_t wq[NP];
+  ga_t wa[NP];
+  gx_t ap;
+};
+
+// Streams n_items items of nsq stages each (stage = 4 rows x 256 packed bytes per weight
+// stream) through a D-stage register pipeline.  next_item(P) is called once per item, in
+// order, and sets P to that item's pointers; finish(acc) receives each item's per-lane
+// partial sums (before the cross-lane reduction), again in order; hook() runs once after
+// the prologue loads are in flight (every wave calls it exactly once, also without work:
+// it may contain workgroup barriers); slow_code() gives the private codebook of the item
+// being consumed on the SLOW path and is called in order, once per item.
+template <int NP, int D, bool SLOW, bool BC, typename ItemFn, typename FinishFn, typename Hook,
+          typename SlowFn>
+__device__ __forceinline__ void stream_items(int n_items, int nsq, ItemFn &&next_item,
+                                             FinishFn &&finish, Hook &&hook, SlowFn &&slow_code,
+                                             const uint32_t *tbl, const uint32_t (&lane_const)[NP]) {
+  const int total = n_items * nsq;
+  if (total <= 0) {
+    hook();
+    return;
+  }
+  ItemPtr<NP> P;
+  next_item(P);
+  int lt = 0, ls = 0;  // next stage to load (item, stage)
+  auto load = [&](Stage4<NP, BC> &st) {
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      st.q[p] = ld_u4(P.wq[p] + ls * 256);
+      st.s[p] = P.wa[p][ls * 8];
+    }
+    const gx_t px = P.ap + ls * kStageVals;
+#pragma unroll
+    for (int i = 0; i < (BC ? 1 : 4); ++i) st.xa[i] = ld_u4(px + 8 * i);
+  };
+  // Past the last stage the load position saturates and re-reads that stage (unused), so
+  // the prefetches need no branch.
+  auto advance = [&]() {
+    if (++ls == nsq) {
+      if (lt + 1 < n_items) {
+        ++lt;
+        ls = 0;
+        next_item(P);
+      } else {
+        ls = nsq - 1;
+      }
+    }
+  };
+
+  f32x4 acc[NP];
+#pragma unroll
+  for (int p = 0; p < NP; ++p) acc[p] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  const float *sc = SLOW ? slow_code() : nullptr;
+  auto compute = [&](const Stage4<NP, BC> &st) {
+    f32x4 t[NP];
+#pragma unroll
+    for (int p = 0; p < NP; ++p) t[p] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const s16x4 a = a_operand<BC>(st.xa, i);
+#pragma unroll
+      for (int p = 0; p < NP; ++p)
+        t[p] = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(
+            a, b_operand<SLOW>(st.q[p], i, tbl, lane_const[p], sc + 16 * p), t[p], 0, 0, 0);
+    }
+#pragma unroll
+    for (int p = 0; p < NP; ++p) scale_acc(acc[p], t[p], st.s[p]);
+  };
+
+  Stage4<NP, BC> st[D];
+  // Scheduling barriers keep the prologue loads in stage order (the loop's wait counts
+  // must also hold on entry; see expert_gemv4.hip).
+#pragma unroll
+  for (int d = 0; d < D - 1; ++d) {
+    load(st[d]);
+    advance();
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  hook();
+  int ct = 0, cs = 0;  // item / stage being consumed
+  for (int s0 = 0; s0 < total; s0 += D) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      load(st[(d + D - 1) % D]);
+      advance();
+      if (s0 + d < total) {
+        compute(st[d]);
+        if (++cs == nsq) {
+          finish(acc);
+#pragma unroll
+          for (int p = 0; p < NP; ++p) acc[p] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+          cs = 0;
+          ++ct;
+          if (SLOW && ct < n_items) sc = slow_code();
+        }
+      }
+    }
+  }
+}
+
+// 64 KB lookup table: replicas 0-31 from code_a, 32-63 from code_b (16 floats each).
+// Thread (wave w, replica r) writes the words i = 64*w + r + 256*n, n = 0..63, i.e.
+// packed byte v = w + 4n, whose nibbles are v >> 4 = n >> 2 and v & 15 = w + 4*(n & 3):
+// 20 codebook reads into registers, then 64 stores and no further LDS reads.
+__device__ __forceinline__ void build_table(uint32_t *tbl, const float *code_a,
+                                            const float *code_b) {
+  const int r = threadIdx.x & (kWave - 1);
+  const int w = threadIdx.x >> 6;
+  const float *c = (r & 32) ? code_b : code_a;
+  float hi[16], lo[4];
+#pragma unroll
+  for (int q = 0; q < 16; ++q) hi[q] = c[q];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) lo[q] = c[w + 4 * q];
+#pragma unroll
+  for (int n = 0; n < 64; ++n) tbl[(w + 4 * n) * kWave + r] = pack_bf16x2(hi[n >> 2], lo[n & 3]);
+}
+
+// Sum over the 64 lanes, every lane gets the result: DPP within each row of 16 lanes
+// (xor 1, xor 2, rotate 4, rotate 8), then two cross-row exchanges.  Fixed order, so all
+// workgroups obtain bit-identical sums.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xf,
+                                                            0xf, false));
+}
+__device__ __forceinline__ float wave_sum_fast(float v) {
+  v += dpp_mov<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_mov<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_mov<0x124>(v);  // row_ror:4
+  v += dpp_mov<0x128>(v);  // row_ror:8
+  v += __shfl_xor(v, 16, kWave);
+  v += __shfl_xor(v, 32, kWave);
+  return v;
+}
+
+template <int EMAX>
+__global__ void __launch_bounds__(kFfnThreads, 2)
+decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
+                     const uint16_t *__restrict__ gate, const float *__restrict__ bias, int T,
+                     int H, int F, int E, int k, uint16_t *__restrict__ logits_out,
+                     float *__restrict__ w_out, int64_t *__restrict__ idx_out,
+                     DecodeRoute *__restrict__ route_out, uint16_t *__restrict__ h_out) {
+  __shared__ __attribute__((aligned(16))) uint32_t s_tbl[kTableWords];
+  __shared__ float s_part[kFfnWaves][kDecMaxTokens][EMAX];
+  // Codebooks of every expert: [0,16) w1, [16,32) w3, [32,48) w2 ([48,64) repeats w2).
+  __shared__ float s_code[EMAX][kWave];
+  __shared__ __attribute__((aligned(16))) DecodeRoute s_rt;
+  __shared__ int32_t s_idx[kDecMaxSlots];
+  __shared__ float s_w[kDecMaxSlots];
+  __shared__ const void *s_eptr[EMAX][4];  // w1_packed, w1_absmax, w3_packed, w3_absmax
+
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool wg0 = blockIdx.x == 0;
+
+  // ---- gate products: each thread sums NCH 8-value chunks per round (all of a round's
+  // loads issued before any product), then wave and workgroup sums.  The first round's
+  // loads go out first; the per-expert metadata loads follow them.
+  constexpr int NCH = EMAX <= 8 ? 2 : 1;
+  constexpr int EPW = EMAX / kFfnWaves;  // experts per wave for the metadata loads
+  float acc[kDecMaxTokens][EMAX];
+#pragma unroll
+  for (int t = 0; t < kDecMaxTokens; ++t)
+#pragma unroll
+    for (int e = 0; e < EMAX; ++e) acc[t][e] = 0.0f;
+  uint4 xv[NCH][kDecMaxTokens];
+  uint4 gv[NCH][EMAX];
+  auto load_round = [&](int cb) {
+#pragma unroll
+    for (int h = 0; h < NCH; ++h) {
+      int c = cb + (h * kFfnThreads + tid) * 8;
+      c = c < H ? c : 0;
+#pragma unroll
+      for (int t = 0; t < kDecMaxTokens; ++t)
+        xv[h][t] = *reinterpret_cast<const uint4 *>(x + (int64_t)(t < T ? t : 0) * H + c);
+#pragma unroll
+      for (int e = 0; e < EMAX; ++e)
+        gv[h][e] = *reinterpret_cast<const uint4 *>(gate + (int64_t)(e < E ? e : E - 1) * H + c);
+    }
+  };
+  auto fma_round = [&](int cb) {
+#pragma unroll
+    for (int h = 0; h < NCH; ++h) {
+      if (cb + (h * kFfnThreads + tid) * 8 >= H) continue;
+#pragma unroll
+      for (int t = 0; t < kDecMaxTokens; ++t) {
+        if (t >= T) continue;
+        const uint32_t xw[4] = {xv[h][t].x, xv[h][t].y, xv[h][t].z, xv[h][t].w};
+#pragma unroll
+        for (int e = 0; e < EMAX; ++e) {
+          const uint32_t gw[4] = {gv[h][e].x, gv[h][e].y, gv[h][e].z, gv[h][e].w};
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            acc[t][e] = fmaf(bf16lo_to_f32(xw[q]), bf16lo_to_f32(gw[q]), acc[t][e]);
+            acc[t][e] = fmaf(bf16hi_to_f32(xw[q]), bf16hi_to_f32(gw[q]), acc[t][e]);
+          }
+        }
+      }
+    }
+  };
+  load_round(0);
+  // Metadata of experts wave + 4q (wave-uniform, so the table entries are scalar loads):
+  // lane l < 16 reads w1 code[l], 16..31 w3 code[l-16], 32..63 w2 code[l & 15]; lane f < 4
+  // keeps stream pointer f (w1_packed, w1_absmax, w3_packed, w3_absmax).
+  float cvw[EPW];
+  const void *pvw[EPW];
+#pragma unroll
+  for (int q = 0; q < EPW; ++q) {
+    const int e = wave + kFfnWaves * q;
+    const moe_nf4_expert_t &ex = tab.e[e < E ? e : E - 1];
+    const void *c1 = uniform_ptr(ex.w1_code), *c3 = uniform_ptr(ex.w3_code);
+    const void *c2 = uniform_ptr(ex.w2_code);
+    const void *p1 = uniform_ptr(ex.w1_packed), *a1 = uniform_ptr(ex.w1_absmax);
+    const void *p3 = uniform_ptr(ex.w3_packed), *a3 = uniform_ptr(ex.w3_absmax);
+    const void *cp = lane < 16 ? c1 : lane < 32 ? c3 : c2;
+    cvw[q] = ((ga_t)cp)[lane & 15];
+    const int f = lane & 3;
+    pvw[q] = f == 0 ? p1 : f == 1 ? a1 : f == 2 ? p3 : a3;
+  }
+  // Unconditional stores (clamped experts rewrite identical values), so the metadata
+  // loads stay ahead of the products instead of sinking to a later conditional use.
+#pragma unroll
+  for (int q = 0; q < EPW; ++q) {
+    const int e = wave + kFfnWaves * q;
+    const int ee = e < E ? e : E - 1;
+    s_code[ee][lane] = cvw[q];
+    s_eptr[ee][lane & 3] = pvw[q];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  fma_round(0);
+  for (int cb = NCH * kFfnThreads * 8; cb < H; cb += NCH * kFfnThreads * 8) {
+    load_round(cb);
+    __builtin_amdgcn_sched_barrier(0);
+    fma_round(cb);
+  }
+#pragma unroll
+  for (int t = 0; t < kDecMaxTokens; ++t) {
+    if (t < T) {
+#pragma unroll
+      for (int e = 0; e < EMAX; ++e) {
+        if (e < E) {
+          const float v = wave_sum_fast(acc[t][e]);
+          if (lane == 0) s_part[wave][t][e] = v;
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- softmax / top-k: one lane per token
+  if (tid < T) {
+    const int t = tid;
+    float p[EMAX];
+    float m = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < EMAX; ++e) {
+      if (e < E) {
+        const float v = s_part[0][t][e] + s_part[1][t][e] + s_part[2][t][e] + s_part[3][t][e];
+        const uint16_t lb = f32_to_bf16(v);
+        if (wg0 && logits_out != nullptr) logits_out[t * E + e] = lb;
+        float l = bf16_to_f32(lb);
+        if (bias != nullptr) l = l + bias[e];
+        p[e] = l;
+        m = fmaxf(m, l);
+      }
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int e = 0; e < EMAX; ++e) {
+      if (e < E) {
+        p[e] = expf(p[e] - m);
+        s += p[e];
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < EMAX; ++e)
+      if (e < E) p[e] = p[e] / s;
+    float topw[kDecMaxSlots];
+    int topi[kDecMaxSlots];
+    uint32_t taken = 0;
+    float wsum = 0.0f;
+    for (int j = 0; j < k; ++j) {
+      float best = -INFINITY;
+      int bi = -1;
+#pragma unroll
+      for (int e = 0; e < EMAX; ++e) {
+        if (e < E && !((taken >> e) & 1u) && (bi < 0 || p[e] > best)) {
+          best = p[e];
+          bi = e;
+        }
+      }
+      taken |= 1u << bi;
+      topw[j] = best;
+      topi[j] = bi;
+      wsum += best;
+    }
+    for (int j = 0; j < k; ++j) {
+      const float wv = topw[j] / wsum;
+      s_idx[t * k + j] = topi[j];
+      s_w[t * k + j] = wv;
+      if (wg0) {
+        w_out[t * k + j] = wv;
+        idx_out[t * k + j] = topi[j];
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- grouping (wave 0): expert `lane` has cnt slots; slot `lane` goes to row off_e+rank
+  const int ns = T * k;
+  if (wave == 0) {
+    int cnt = 0, off = 0;
+    if (lane < E) {
+      for (int s = 0; s < ns; ++s) {
+        const int e = s_idx[s];
+        cnt += e == lane;
+        off += e < lane;
+      }
+    }
+    const uint64_t amask = __ballot(lane < E && cnt > 0);
+    const int a_of = __popcll(amask & ((1ull << lane) - 1ull));
+    const int e_s = lane < ns ? s_idx[lane] : 0;
+    const int off_e = __shfl(off, e_s, kWave);
+    const int a_e = __shfl(a_of, e_s, kWave);
+    if (lane < E && cnt > 0) {
+      s_rt.active[a_of] = lane;
+      s_rt.counts[a_of] = cnt;
+      s_rt.offsets[a_of] = off;
+    }
+    if (lane < ns) {
+      int rank = 0;
+      for (int s = 0; s < lane; ++s) rank += s_idx[s] == e_s;
+      s_rt.perm_tok[off_e + rank] = lane / k;
+      s_rt.slot_a[lane] = a_e;
+      s_rt.slot_m[lane] = rank;
+      s_rt.slot_w[lane] = s_w[lane];
+    }
+    const bool multi = __ballot(lane < E && cnt > 1) != 0;
+    if (lane == 0) {
+      s_rt.n_active = __popcll(amask);
+      s_rt.bc = multi ? 0 : 1;
+    }
+  }
+  __syncthreads();
+
+  // ---- codebook flags, expert pointers, descriptor
+  const int u = s_rt.n_active;
+  if (wave == 0) {
+    const int e0 = s_rt.active[0];
+    bool d1 = false, d2 = false;
+    for (int a = 1; a < u; ++a) {
+      const int e = s_rt.active[a];
+      if (lane < 32)
+        d1 |= __builtin_bit_cast(uint32_t, s_code[e][lane]) !=
+              __builtin_bit_cast(uint32_t, s_code[e0][lane]);
+      if (wg0 && lane < 16)
+        d2 |= __builtin_bit_cast(uint32_t, s_code[e][32 + lane]) !=
+              __builtin_bit_cast(uint32_t, s_code[e0][32 + lane]);
+    }
+    const bool slow1 = __ballot(d1) != 0;
+    const bool slow2 = __ballot(d2) != 0;
+    if (lane == 0) {
+      s_rt.slow1 = slow1 ? 1 : 0;
+      s_rt.slow2 = slow2 ? 1 : 0;
+    }
+  } else if (wave == 2 && wg0) {
+    for (int i = lane; i < u * 16; i += kWave)
+      s_rt.code2[i >> 4][i & 15] = s_code[s_rt.active[i >> 4]][32 + (i & 15)];
+  }
+  __syncthreads();
+  if (wg0 && tid < kRouteWords)
+    reinterpret_cast<uint32_t *>(route_out)[tid] = reinterpret_cast<const uint32_t *>(&s_rt)[tid];
+
+  // ---- w1/w3 stream over this wave's range of the (active expert, tile) list
+  const int lanej = lane & 3;
+  const int blk = lane >> 2;
+  const int tiles_e = F >> 2;
+  const int N = u * tiles_e;
+  const int W = (int)gridDim.x * kFfnWaves;
+  const int wid = (int)blockIdx.x * kFfnWaves + wave;
+  const int i0 = (int)((int64_t)wid * N / W);
+  const int n_items = (int)((int64_t)(wid + 1) * N / W) - i0;
+  const int nsq = H / kStageVals;
+  const size_t row_bytes = (size_t)(H >> 1);
+  const size_t row_blocks = (size_t)(H >> 6);
+  const uint32_t lane_const[2] = {(uint32_t)(lane & 31) << 2, ((uint32_t)(lane & 31) << 2) | 128u};
+  const float *code0 = s_code[s_rt.active[0]];
+  const bool bc = s_rt.bc != 0;
+  const int a_start = i0 / tiles_e;
+  const int tile_start = i0 - a_start * tiles_e;
+
+  // Load side: (la, ltile) walks the items in order; within an expert the pointers step
+  // by one 4-row tile, at an expert change they are rebuilt from the LDS tables.
+  int la = a_start, ltile = tile_start - 1;
+  auto next_item = [&](ItemPtr<2> &P) {
+    if (++ltile < tiles_e && ltile != tile_start) {
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        P.wq[p] += 4 * row_bytes;
+        P.wa[p] += 4 * row_blocks;
+      }
+      return;
+    }
+    if (ltile == tiles_e) {
+      ltile = 0;
+      ++la;
+    }
+    const size_t row = (size_t)ltile * 4 + lanej;
+    const int e = s_rt.active[la];
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      P.wq[p] = (gq_t)s_eptr[e][2 * p] + row * row_bytes + blk * 16;
+      P.wa[p] = (ga_t)s_eptr[e][2 * p + 1] + row * row_blocks + (blk >> 1);
+    }
+    const int jj = (!bc && lanej < s_rt.counts[la]) ? lanej : 0;
+    const int tok = s_rt.perm_tok[s_rt.offsets[la] + jj];
+    P.ap = (gx_t)x + (size_t)tok * H + blk * 32 + (bc ? lanej * 8 : 0);
+  };
+  // Consume side: (ca, ctile) walks the same items for the h stores.
+  int ca = a_start, ctile = tile_start;
+  auto finish = [&](f32x4 (&ac)[2]) {
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) ac[p][q] = lanes_sum16(ac[p][q]);
+    if (blk == 0) {
+      const int row = ctile * 4 + lanej;
+      const int cnt = s_rt.counts[ca];
+      const int off = s_rt.offsets[ca];
+#pragma unroll
+      for (int m = 0; m < 4; ++m)
+        if (m < cnt) h_out[(size_t)(off + m) * F + row] = swiglu_bf16(ac[0][m], ac[1][m]);
+    }
+    if (++ctile == tiles_e) {
+      ctile = 0;
+      ++ca;
+    }
+  };
+  auto hook = [&]() {
+    build_table(s_tbl, code0, code0 + 16);
+    __syncthreads();
+  };
+  auto slow_code = [&]() -> const float * { return s_code[s_rt.active[ca]]; };
+  const bool slow = s_rt.slow1 != 0;
+  if (!slow && bc)
+    stream_items<2, 6, false, true>(n_items, nsq, next_item, finish, hook, slow_code, s_tbl, lane_const);
+  else if (!slow)
+    stream_items<2, 4, false, false>(n_items, nsq, next_item, finish, hook, slow_code, s_tbl, lane_const);
+  else if (bc)
+    stream_items<2, 6, true, true>(n_items, nsq, next_item, finish, hook, slow_code, s_tbl, lane_const);
+  else
+    stream_items<2, 4, true, false>(n_items, nsq, next_item, finish, hook, slow_code, s_tbl, lane_const);
+}
+
+__global__ void __launch_bounds__(kFfnThreads, 2)
+decode_down_kernel(const ExpertTable tab, const DecodeRoute *__restrict__ route,
+                   const uint16_t *__restrict__ h, int T, int H, int F, int E, int k,
+                   int tiles_per_wg, uint16_t *__restrict__ out) {
+  __shared__ __attribute__((aligned(16))) uint32_t s_tbl[kTableWords];
+  __shared__ __attribute__((aligned(16))) DecodeRoute s_rt;
+  __shared__ float s_part[kDecMaxTilesPerWg][kDecMaxSlots][kFfnWaves][16];
+  __shared__ const void *s_eptr[kDecMaxExperts][2];  // w2_packed, w2_absmax of every expert
+
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // The descriptor and every expert's w2 pointers in one round trip.
+  uint32_t rw = 0;
+  if (tid < kRouteWords) rw = reinterpret_cast<const uint32_t *>(route)[tid];
+  for (int i = tid; i < (int)(sizeof(s_part) / 4); i += kFfnThreads)
+    reinterpret_cast<float *>(s_part)[i] = 0.0f;
+  // Experts wave + 4q: wave-uniform table entries (scalar loads), lanes 0/1 keep
+  // w2_packed / w2_absmax.
+  constexpr int EPW = kDecMaxExperts / kFfnWaves;
+  const void *pk[EPW], *pa[EPW];
+#pragma unroll
+  for (int q = 0; q < EPW; ++q) {
+    const int e = wave + kFfnWaves * q;
+    const moe_nf4_expert_t &ex = tab.e[e < E ? e : E - 1];
+    pk[q] = uniform_ptr(ex.w2_packed);
+    pa[q] = uniform_ptr(ex.w2_absmax);
+  }
+#pragma unroll
+  for (int q = 0; q < EPW; ++q) {
+    const int e = wave + kFfnWaves * q;
+    if (e < E && lane < 2) s_eptr[e][lane] = lane ? pa[q] : pk[q];
+  }
+  if (tid < kRouteWords) reinterpret_cast<uint32_t *>(&s_rt)[tid] = rw;
+  __syncthreads();
+  const int u = s_rt.n_active;
+
+  const int lanej = lane & 3;
+  const int blk = lane >> 2;
+  const int r0 = blockIdx.x * tiles_per_wg;
+  const int r_end = min(r0 + tiles_per_wg, H >> 2);
+  const int ntl = r_end > r0 ? r_end - r0 : 0;
+  const int NS = F / kStageVals;
+  const int s_lo = wave * NS / kFfnWaves;
+  const int nsq = (wave + 1) * NS / kFfnWaves - s_lo;
+  const int n_items = ntl * u;
+  const size_t row_bytes = (size_t)(F >> 1);
+  const size_t row_blocks = (size_t)(F >> 6);
+  const uint32_t lane_const[1] = {(uint32_t)lane << 2};
+  const bool bc = s_rt.bc != 0;
+
+  // Items in expert-major order (item i: active expert i / ntl, tile i % ntl); the
+  // partial sums meet in LDS, so the order does not affect the result.
+  int la = 0, ltl = -1;
+  auto next_item = [&](ItemPtr<1> &P) {
+    if (++ltl < ntl && ltl != 0) {
+      P.wq[0] += 4 * row_bytes;
+      P.wa[0] += 4 * row_blocks;
+      return;
+    }
+    if (ltl == ntl) {
+      ltl = 0;
+      ++la;
+    }
+    const size_t row = (size_t)(r0 + ltl) * 4 + lanej;
+    const int e = s_rt.active[la];
+    P.wq[0] = (gq_t)s_eptr[e][0] + row * row_bytes + s_lo * 256 + blk * 16;
+    P.wa[0] = (ga_t)s_eptr[e][1] + row * row_blocks + s_lo * 8 + (blk >> 1);
+    const int jj = (!bc && lanej < s_rt.counts[la]) ? lanej : 0;
+    P.ap = (gx_t)h + (size_t)(s_rt.offsets[la] + jj) * F + (size_t)s_lo * kStageVals + blk * 32 +
+           (bc ? lanej * 8 : 0);
+  };
+  int ca = 0, ctl = 0;
+  auto finish = [&](f32x4 (&ac)[1]) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) ac[0][q] = lanes_sum16(ac[0][q]);
+    if (blk == 0) {
+#pragma unroll
+      for (int m = 0; m < 4; ++m) s_part[ctl][ca][wave][lanej * 4 + m] = ac[0][m];
+    }
+    if (++ctl == ntl) {
+      ctl = 0;
+      ++ca;
+    }
+  };
+  auto hook = [&]() {
+    build_table(s_tbl, s_rt.code2[0], s_rt.code2[0]);
+    __syncthreads();
+  };
+  auto slow_code = [&]() -> const float * { return s_rt.code2[ca]; };
+  const bool slow = s_rt.slow2 != 0;
+  if (!slow && bc)
+    stream_items<1, 8, false, true>(n_items, nsq, next_item, finish, hook, slow_code, s_tbl, lane_const);
+  else if (!slow)
+    stream_items<1, 8, false, false>(n_items, nsq, next_item, finish, hook, slow_code, s_tbl, lane_const);
+  else if (bc)
+    stream_items<1, 8, true, true>(n_items, nsq, next_item, finish, hook, slow_code, s_tbl, lane_const);
+  else
+    stream_items<1, 8, true, false>(n_items, nsq, next_item, finish, hook, slow_code, s_tbl, lane_const);
+  __syncthreads();
+
+  // ---- combine: one thread per (tile, token, row); slots in ascending expert order
+  if (tid < ntl * T * 4) {
+    const int tl = tid / (T * 4);
+    const int rem = tid - tl * T * 4;
+    const int t = rem >> 2;
+    const int jr = rem & 3;
+    int ord[kDecMaxSlots];
+    for (int j = 0; j < k; ++j) {
+      const int key = s_rt.slot_a[t * k + j];
+      int p = j;
+      while (p > 0 && s_rt.slot_a[t * k + ord[p - 1]] > key) {
+        ord[p] = ord[p - 1];
+        --p;
+      }
+      ord[p] = j;
+    }
+    float o = 0.0f;
+    for (int jj = 0; jj < k; ++jj) {
+      const int s = t * k + ord[jj];
+      const int a = s_rt.slot_a[s];
+      const int m = s_rt.slot_m[s];
+      const float y = s_part[tl][a][0][jr * 4 + m] + s_part[tl][a][1][jr * 4 + m] +
+                      s_part[tl][a][2][jr * 4 + m] + s_part[tl][a][3][jr * 4 + m];
+      const float pr = bf16_to_f32(f32_to_bf16(y)) * s_rt.slot_w[s];
+      o = bf16_to_f32(f32_to_bf16(o + pr));
+    }
+    out[(size_t)t * H + (size_t)(r0 + tl) * 4 + jr] = f32_to_bf16(o);
+  }
+}
+
+}  // namespace
+
+int decode_tiles_per_wg(int32_t H) {
+  const int rt = H / 4;
+  const int cap = 2 * device_cu_count();
+  return (rt + cap - 1) / cap;
+}
+
+bool decode_layer_supported(int64_t T, int32_t k, int32_t E, int32_t H, int32_t F) {
+  return T >= 1 && T <= kDecMaxTokens && T * k <= kDecMaxSlots && E >= 1 &&
+         E <= kDecMaxExperts && k >= 1 && k <= E && H % kStageVals == 0 &&
+         F % kStageVals == 0 && H >= kStageVals && F >= kStageVals &&
+         decode_tiles_per_wg(H) <= kDecMaxTilesPerWg;
+}
+
+int64_t decode_route_bytes() { return (int64_t)sizeof(DecodeRoute); }
+
+// Gate/up (with routing) then down (with combine).  `ev`, when given, receives marks
+// before the first kernel (twice: the routing has no launch of its own), between the two
+// kernels and after the second.
+int launch_decode_layer(const moe_nf4_expert_t *experts, int32_t E, const void *gate,
+                        const void *bias, const void *x, int64_t T, int32_t H, int32_t F,
+                        int32_t k, void *out, void *logits, void *weights, void *idx64,
+                        void *route_ws, void *h_ws, hipStream_t s, hipEvent_t *ev) {
+  MOE_REQUIRE(decode_layer_supported(T, k, E, H, F), "shape not supported by the decode layer");
+  MOE_REQUIRE(((uintptr_t)x % 16) == 0 && ((uintptr_t)gate % 16) == 0,
+              "x and gate must be 16-byte aligned");
+  MOE_REQUIRE(((uintptr_t)route_ws % 16) == 0 && ((uintptr_t)h_ws % 16) == 0,
+              "workspace regions must be 16-byte aligned");
+  ExpertTable tab{};
+  for (int e = 0; e < E; ++e) {
+    const moe_nf4_expert_t &ex = experts[e];
+    MOE_REQUIRE(ex.w1_packed && ex.w1_absmax && ex.w1_code && ex.w3_packed && ex.w3_absmax &&
+                    ex.w3_code && ex.w2_packed && ex.w2_absmax && ex.w2_code,
+                "expert %d is not resident (null pointer in its table entry)", e);
+    tab.e[e] = ex;
+  }
+  const int cap = 2 * device_cu_count();
+  const int64_t u_max = T * k < E ? T * k : E;
+  int64_t g1 = (u_max * (F / 4) + kFfnWaves - 1) / kFfnWaves;
+  if (g1 > cap) g1 = cap;
+  const int tpw = decode_tiles_per_wg(H);
+  const int64_t g2 = (H / 4 + tpw - 1) / tpw;
+
+  if (ev) MOE_HIP_CHECK(hipEventRecord(ev[0], s));
+  if (ev) MOE_HIP_CHECK(hipEventRecord(ev[1], s));
+  auto gateup = [&](auto kern) {
+    hipLaunchKernelGGL(kern, dim3((unsigned)g1), dim3(kFfnThreads), 0, s, tab,
+                       (const uint16_t *)x, (const uint16_t *)gate, (const float *)bias, (int)T, H,
+                       F, E, k, (uint16_t *)logits, (float *)weights, (int64_t *)idx64,
+                       (DecodeRoute *)route_ws, (uint16_t *)h_ws);
+  };
+  if (E <= 8)
+    gateup(decode_gateup_kernel<8>);
+  else
+    gateup(decode_gateup_kernel<16>);
+  MOE_LAUNCH_CHECK();
+  if (ev) MOE_HIP_CHECK(hipEventRecord(ev[2], s));
+  hipLaunchKernelGGL(decode_down_kernel, dim3((unsigned)g2), dim3(kFfnThreads), 0, s, tab,
+                     (const DecodeRoute *)route_ws, (const uint16_t *)h_ws, (int)T, H, F, E, k,
+                     tpw, (uint16_t *)out);
+  MOE_LAUNCH_CHECK();
+  if (ev) MOE_HIP_CHECK(hipEventRecord(ev[3], s));
+  return MOE_STATUS_OK;
+}
+
+}  // namespace moe

@@ -1,0 +1,277 @@
+"""The reference-compatible Python API on the GPU: expert containers, the staged H2D
+transfer path, and MoELayer in all-resident and offload modes, each checked against the
+oracle; plus a full Mixtral-8x7B-shape layer (hidden 4096, FFN 14336, 8 experts, top-2)."""
+from __future__ import annotations
+
+import time
+import types
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import bits, build_layer, near_tie_rows, oracle_layer
+from oracle import moe_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-2   # rel-L2 bound on expert / layer outputs
+
+
+def _layer_err(got_bits, want_bits, logits_bits):
+    """rel-L2 over the tokens whose top-k is not decided by a 1-ulp logit tie (the device
+    and the oracle round the gate logits independently)."""
+    ok = ~near_tie_rows(logits_bits)
+    assert ok.sum() >= max(1, ok.size // 2)
+    return orc.rel_l2(orc.bf16_to_f32(got_bits[ok]), orc.bf16_to_f32(want_bits[ok]))
+
+
+def _bf16(shape, seed, std=0.02):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(shape, generator=g) * std).to(torch.bfloat16)
+
+
+def _serialized(packed, absmax, shape):
+    from moeinfra_amd.model.expert import NF4QuantState
+
+    code = torch.from_numpy(orc.NF4_CODE.copy())
+    qs = NF4QuantState(absmax=torch.from_numpy(absmax.copy()), code=code, shape=torch.Size(shape))
+    return {"weight": torch.from_numpy(packed.copy()).reshape(-1, 1),
+            "weight.absmax": qs.absmax, "weight.quant_map": code,
+            "weight.quant_state.bitsandbytes__nf4": qs.blob()}
+
+
+def _prequantized(ex):
+    """helpers.NF4Expert (oracle-quantised) -> the CPU-authoritative serialized expert."""
+    from moeinfra_amd.model.expert import PrequantizedNF4Expert
+
+    shapes = {"w1": (ex.inter, ex.hidden), "w3": (ex.inter, ex.hidden),
+              "w2": (ex.hidden, ex.inter)}
+    s = {n: _serialized(*ex.np[n], shapes[n]) for n in ("w1", "w2", "w3")}
+    return PrequantizedNF4Expert.from_serialized(s["w1"], s["w2"], s["w3"], ex.hidden, ex.inter)
+
+
+def _resident(ex, device):
+    """helpers.NF4Expert -> ReconstructedNF4Expert over device copies of its tensors."""
+    from moeinfra_amd.transfer.nf4_reconstruct import ReconstructedNF4Expert
+
+    code = torch.from_numpy(orc.NF4_CODE.copy()).to(device)
+    state = {n: {"weight": torch.from_numpy(p.copy()).reshape(-1, 1).to(device),
+                 "absmax": torch.from_numpy(a.copy()).to(device), "code": code, "offset": None}
+             for n, (p, a) in ex.np.items()}
+    meta = types.SimpleNamespace(hidden_size=ex.hidden, intermediate_size=ex.inter)
+    return ReconstructedNF4Expert(meta, state)
+
+
+def test_quantized_expert_cuda_matches_oracle(cuda_device):
+    from moeinfra_amd.model.expert import QuantizedMixtralExpert
+
+    H, F = 256, 512
+    w1, w2, w3 = _bf16((F, H), 1), _bf16((H, F), 2), _bf16((F, H), 3)
+    ex = QuantizedMixtralExpert(w1, w2, w3)
+    assert ex.device.type == "cpu" and ex.size_bytes == 3 * H * F * 2
+    ex.cuda()
+    assert ex.device.type == "cuda" and ex.size_bytes == 3 * H * F // 2
+    state = {}
+    for name, w in (("w1", w1), ("w2", w2), ("w3", w3)):
+        lin = getattr(ex, name)
+        p, a = orc.nf4_quantize(bits(w).reshape(-1))
+        np.testing.assert_array_equal(lin.weight.cpu().numpy().reshape(-1), p)
+        np.testing.assert_array_equal(lin.quant_state.absmax.cpu().numpy(), a)
+        np.testing.assert_array_equal(bits(lin.dequantize()).reshape(-1), orc.nf4_dequant(p, a))
+        state[name] = (p, a)
+    sd = ex.state_dict()
+    assert {"w1.weight", "w1.weight.absmax", "w1.weight.quant_map",
+            "w1.weight.quant_state.bitsandbytes__nf4"} <= set(sd)
+    x = _bf16((3, H), 4, 1.0)
+    want = orc.swiglu(bits(x), *orc.dequant_expert(state, H, F))
+    got = ex(x.to(cuda_device))
+    assert got.dtype == torch.bfloat16
+    assert orc.rel_l2(orc.bf16_to_f32(bits(got)), orc.bf16_to_f32(want)) < TOL
+    got32 = ex(x.float().to(cuda_device))
+    assert got32.dtype == torch.float32
+    np.testing.assert_array_equal(bits(got32.to(torch.bfloat16)), bits(got))
+
+
+def _transfer_rig(cm, budget_slots, slot_bytes):
+    from moeinfra_amd.transfer.pinned_memory import PinnedMemoryBudget
+    from moeinfra_amd.transfer.reusable_staging import ReusablePinnedStagingPool
+    from moeinfra_amd.transfer.scheduler import TransferScheduler
+
+    pool = ReusablePinnedStagingPool(PinnedMemoryBudget(budget_slots * slot_bytes), slot_bytes)
+    stream = torch.cuda.Stream()
+    return TransferScheduler(cm, 24.0, 4, staging_pool=pool, transfer_stream=stream), pool
+
+
+def _req(layer, e):
+    from moeinfra_amd.transfer.types import TransferDirection, TransferPriority, TransferRequest
+
+    return TransferRequest(f"t-{layer}-{e}-{time.monotonic_ns()}", layer, e,
+                           TransferDirection.CPU_TO_GPU, TransferPriority.HIGH, time.monotonic())
+
+
+def test_staged_transfer_reconstructs_the_expert(cuda_device):
+    from moeinfra_amd.cache.manager import CacheManager
+    from moeinfra_amd.cache.types import EvictionPolicy
+    from moeinfra_amd.transfer.nf4_reconstruct import ReconstructedNF4Expert
+
+    H, F = 512, 1024
+    gate, experts, x = build_layer(H, F, 2, 4, seed=5)
+    cm = CacheManager(gpu_slots=1, cpu_slots=4, policy=EvictionPolicy.LRU)
+    cpu = [_prequantized(e) for e in experts]
+    for e, ex in enumerate(cpu):
+        cm.put(0, e, ex, "cpu")
+    sch, pool = _transfer_rig(cm, 1, cpu[0].size_bytes)
+    for e in range(2):
+        assert sch.submit(_req(0, e))
+        r = sch.execute_next()
+        assert r.success, r.error
+        assert r.bytes_transferred == cpu[e].size_bytes
+        g = cm.peek_gpu(0, e)
+        assert isinstance(g, ReconstructedNF4Expert) and g.device.type == "cuda"
+        assert torch.equal(g.w2.weight.cpu(), cpu[e].w2["weight"])
+        assert cm.peek_cpu(0, e) is cpu[e]                     # CPU copy stays authoritative
+        want = orc.swiglu(bits(x), *experts[e].dequant_np())
+        assert orc.rel_l2(orc.bf16_to_f32(bits(g(x.to(cuda_device)))),
+                          orc.bf16_to_f32(want)) < TOL
+    assert pool.slot_count == 1 and pool.active_slots == 0     # one slot, reused
+    slot = next(iter(pool._slots.values()))
+    assert all(t.is_pinned() for proj in slot.tensors.values() for t in proj.values()
+               if t is not None)
+    assert not cpu[0].w1["weight"].is_pinned()                 # the source stays pageable
+    assert cm.stats().gpu_slots_used == 1                      # gpu_slots=1: expert 0 evicted
+    assert not cm.is_gpu_resident(0, 0) and cm.is_gpu_resident(0, 1)
+
+
+def test_async_transfer_then_layer(cuda_device):
+    from moeinfra_amd.cache.manager import CacheManager
+    from moeinfra_amd.cache.types import EvictionPolicy
+    from moeinfra_amd.transfer.types import TransferStatus
+
+    H, F = 256, 512
+    _, experts, _ = build_layer(H, F, 3, 1, seed=6)
+    cm = CacheManager(gpu_slots=4, cpu_slots=4, policy=EvictionPolicy.LRU)
+    for e, ex in enumerate(experts):
+        cm.put(0, e, _prequantized(ex), "cpu")
+    sch, pool = _transfer_rig(cm, 2, cm.get_size_bytes(0, 0))
+    handles = [sch.submit_async(_req(0, e)) for e in range(3)]
+    assert [h.status for h in handles] == [TransferStatus.IN_FLIGHT] * 2 + [TransferStatus.REJECTED]
+    assert sch.submit_async(_req(0, 0)) is handles[0]          # the in-flight handle again
+    torch.cuda.synchronize()
+    assert sch.poll_async(0, 0) == TransferStatus.READY
+    assert sch.poll_async(0, 1) == TransferStatus.READY
+    assert cm.is_gpu_resident(0, 0) and cm.is_gpu_resident(0, 1)
+    assert sch.submit_async(_req(0, 0)).status == TransferStatus.READY
+    assert pool.active_slots == 0
+    torch.cuda.synchronize()                                   # the slots' reuse events
+    h = sch.submit_async(_req(0, 2))                           # a slot is free again
+    assert h.status == TransferStatus.IN_FLIGHT and sch.cancel(h.request_id)
+    torch.cuda.synchronize()
+    assert sch.poll_async(0, 2) == TransferStatus.CANCELLED and not cm.is_gpu_resident(0, 2)
+    assert pool.active_slots == 0
+
+
+def _layer(cm, gate, device, layer_id=0, scheduler=None):
+    from moeinfra_amd.engine.router import ExpertRouter
+    from moeinfra_amd.model.moe_layer import MoELayer
+
+    return MoELayer(layer_id, ExpertRouter(gate.to(device), 2), cm, model_loader=None,
+                    transfer_scheduler=scheduler)
+
+
+@pytest.mark.parametrize("T", [1, 5, 40])
+def test_moe_layer_all_resident(cuda_device, T):
+    from moeinfra_amd.cache.manager import CacheManager
+    from moeinfra_amd.cache.types import EvictionPolicy
+
+    H, F, E = 512, 1024, 8
+    gate, experts, x = build_layer(H, F, E, T, seed=10 + T)
+    cm = CacheManager(gpu_slots=E, cpu_slots=E, policy=EvictionPolicy.LRU)
+    for e, ex in enumerate(experts):
+        cm.put(0, e, _resident(ex.to(cuda_device), cuda_device), "cuda:0")
+    layer = _layer(cm, gate, cuda_device)
+    want, (lg, _, _) = oracle_layer(gate, experts, x)
+    out1 = layer.forward(x.to(cuda_device))
+    out2 = layer.forward(x.to(cuda_device).reshape(1, T, H))   # cached table + workspace
+    assert _layer_err(bits(out1), want, lg) < TOL
+    np.testing.assert_array_equal(bits(out2).reshape(T, H), bits(out1))
+
+
+def test_moe_layer_offload(cuda_device):
+    from moeinfra_amd.cache.manager import CacheManager
+    from moeinfra_amd.cache.types import EvictionPolicy
+
+    H, F, E, T = 512, 1024, 8, 12
+    gate, experts, x = build_layer(H, F, E, T, seed=21)
+    cm = CacheManager(gpu_slots=E, cpu_slots=E, policy=EvictionPolicy.LRU)
+    for e, ex in enumerate(experts):
+        cm.put(0, e, _prequantized(ex), "cpu")
+    for e in (0, 3):                                           # two experts already resident
+        cm.put(0, e, _resident(experts[e].to(cuda_device), cuda_device), "cuda:0")
+    sch, pool = _transfer_rig(cm, 1, cm.get_size_bytes(0, 1))
+    layer = _layer(cm, gate, cuda_device, scheduler=sch)
+    want, (lg, _, idx) = oracle_layer(gate, experts, x)
+    out = layer.forward(x.to(cuda_device))
+    assert _layer_err(bits(out), want, lg) < TOL
+    routed = set(np.unique(idx).tolist())
+    assert routed - {0, 3}, "routing should need at least one transfer"
+    assert cm.is_gpu_resident(0, 0) and cm.is_gpu_resident(0, 3)
+    assert not any(cm.is_gpu_resident(0, e) for e in routed - {0, 3})
+    assert pool.active_slots == 0 and sch.pending_count() == 0
+
+
+# --------------------------------------------------------------------------- full size
+_FULL = {}
+
+
+def _full_layer(device):
+    """Mixtral-8x7B MoE layer shape, weights drawn and NF4-quantised on the GPU."""
+    if "layer" not in _FULL:
+        from moeinfra_amd import ops
+
+        H, F, E = 4096, 14336, 8
+        g = torch.Generator(device=device).manual_seed(1234)
+        experts, keep = [], []
+        for e in range(E):
+            st = {}
+            for name, shape in (("w1", (F, H)), ("w3", (F, H)), ("w2", (H, F))):
+                w = (torch.randn(shape, generator=g, device=device) * 0.02).to(torch.bfloat16)
+                p, a, code = ops.nf4_quantize(w)
+                st[name] = (p, a, code)
+                del w
+            keep.append(st)
+        gate = (torch.randn((E, H), generator=g, device=device) * 0.02).to(torch.bfloat16)
+        from moeinfra_amd._lib import MoeNf4Expert
+
+        structs = [MoeNf4Expert(*(t.data_ptr() for n in ("w1", "w3", "w2") for t in st[n]))
+                   for st in keep]
+        _FULL["layer"] = (H, F, E, gate, keep, ops.expert_table(structs))
+    return _FULL["layer"]
+
+
+@pytest.mark.parametrize("T", [1, 4, 32])
+def test_full_size_layer_matches_oracle(cuda_device, T):
+    from moeinfra_amd import ops
+
+    H, F, E, gate, keep, table = _full_layer(cuda_device)
+    gen = torch.Generator(device=cuda_device).manual_seed(T)
+    x = torch.randn((T, H), generator=gen, device=cuda_device).to(torch.bfloat16)
+    out, _, w, idx = ops.layer_forward(table, E, gate, x, 2, F)
+    torch.cuda.synchronize()
+    xb, gb = bits(x), bits(gate)
+    cache = {}
+
+    def expert_fn(e, rows):
+        if e not in cache:
+            st = {n: (keep[e][n][0].cpu().numpy().reshape(-1), keep[e][n][1].cpu().numpy())
+                  for n in ("w1", "w3", "w2")}
+            cache[e] = orc.dequant_expert(st, H, F, threads=8)
+        return orc.swiglu(rows, *cache[e])
+
+    want, (lg_o, w_o, idx_o) = orc.moe_layer(xb, gb, expert_fn)
+    ok = ~near_tie_rows(lg_o)
+    np.testing.assert_array_equal(idx.cpu().numpy()[ok], idx_o[ok])
+    np.testing.assert_allclose(w.cpu().numpy()[ok], w_o[ok], rtol=1e-5, atol=1e-6)
+    err = _layer_err(bits(out), want, lg_o)
+    print(f"full-size layer T={T}: rel-L2 {err:.2e}", flush=True)
+    assert err < TOL
