@@ -86,6 +86,7 @@ struct ItemPtr {
   gq_t wq[NP];
   ga_t wa[NP];
   gx_t ap;
+  ga_t ab[NP];  // absmax of the item's first tile row at its first stage (aligned stream)
 };
 
 // Streams n_items items of nsq stages each (stage = 4 rows x 256 packed bytes per weight
@@ -183,6 +184,120 @@ __device__ __forceinline__ void stream_items(int n_items, int nsq, ItemFn &&next
   }
 }
 
+// Aligned stream: every item has exactly NSQ stages (2 <= NSQ <= 8) and the register
+// pipeline is NSQ deep, so unrolled step d always handles stage d of an item.  That allows
+//  * the item's absmax block (4 rows x 8*NSQ floats) to be fetched with one 16-byte load
+//    per lane when the load side enters the item, and staged in the wave's LDS slot at
+//    the item boundary, instead of one 4-byte load per lane and stage;
+//  * with XREG (one token for the whole stream, single-token broadcast form), the
+//    activation chunks of all NSQ stages to stay in registers, loaded once.
+// Step d of item it issues the load of stage NSQ-1 of item it (d = 0) or of stage d-1 of
+// item it+1 (d >= 1; past the last item the last item's stages are re-read, unused).
+// next_item / finish / hook / slow_code as for stream_items; `arow` is the absmax row
+// stride (floats), `aslot` the wave's LDS slot (NP x 256 floats), `xbase` the lane's
+// activation chunk of stage 0 (XREG only).
+template <int NP, int NX>
+struct StageQ {
+  uint4 q[NP];
+  uint4 xa[NX];
+};
+
+template <int NP, int NSQ, bool SLOW, bool BC, bool XREG, typename ItemFn, typename FinishFn,
+          typename Hook, typename SlowFn>
+__device__ __forceinline__ void stream_aligned(int n_items, ItemFn &&next_item, FinishFn &&finish,
+                                               Hook &&hook, SlowFn &&slow_code,
+                                               const uint32_t *tbl,
+                                               const uint32_t (&lane_const)[NP], size_t arow,
+                                               float *aslot, gx_t xbase) {
+  static_assert(NSQ >= 2 && NSQ <= 8, "an item's absmax block must fit one load per lane");
+  constexpr int NX = XREG ? 1 : (BC ? 1 : 4);
+  const int lane = threadIdx.x & (kWave - 1);
+  const int blk = lane >> 2;
+  const int j = lane & 3;
+  if (n_items <= 0) {
+    hook();
+    return;
+  }
+  // This lane's absmax chunk: row a_row, floats a_col .. a_col+3 (lanes >= 8*NSQ idle).
+  const bool a_act = lane < 8 * NSQ;
+  const int a_row = a_act ? lane / (2 * NSQ) : 0;
+  const int a_col = a_act ? 4 * (lane % (2 * NSQ)) : 0;
+
+  ItemPtr<NP> P;
+  next_item(P);
+  uint4 abuf[NP];
+  auto load_abs = [&]() {
+#pragma unroll
+    for (int p = 0; p < NP; ++p) abuf[p] = ld_u4(P.ab[p] + a_row * arow + a_col);
+  };
+  auto store_abs = [&]() {
+    if (a_act) {
+#pragma unroll
+      for (int p = 0; p < NP; ++p)
+        *reinterpret_cast<uint4 *>(aslot + p * 256 + a_row * 64 + a_col) = abuf[p];
+    }
+  };
+  uint4 xr[XREG ? NSQ : 1];
+  if (XREG) {
+#pragma unroll
+    for (int sg = 0; sg < NSQ; ++sg) xr[sg] = ld_u4(xbase + sg * kStageVals);
+  }
+  load_abs();
+  auto load = [&](StageQ<NP, NX> &st, int sg) {
+#pragma unroll
+    for (int p = 0; p < NP; ++p) st.q[p] = ld_u4(P.wq[p] + sg * 256);
+    if (!XREG) {
+      const gx_t px = P.ap + sg * kStageVals;
+#pragma unroll
+      for (int i = 0; i < NX; ++i) st.xa[i] = ld_u4(px + 8 * i);
+    }
+  };
+  StageQ<NP, NX> st[NSQ];
+#pragma unroll
+  for (int d = 0; d < NSQ - 1; ++d) {
+    load(st[d], d);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  store_abs();
+  hook();
+
+  f32x4 acc[NP];
+#pragma unroll
+  for (int p = 0; p < NP; ++p) acc[p] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  const float *sc = SLOW ? slow_code() : nullptr;
+  for (int it = 0; it < n_items; ++it) {
+#pragma unroll
+    for (int d = 0; d < NSQ; ++d) {
+      if (d == 1 && it + 1 < n_items) {
+        next_item(P);
+        load_abs();
+      }
+      load(st[(d + NSQ - 1) % NSQ], d == 0 ? NSQ - 1 : d - 1);
+      __builtin_amdgcn_sched_barrier(0);  // this step's loads before its products
+      const uint4 *xa = XREG ? &xr[d] : st[d].xa;
+      f32x4 t[NP];
+#pragma unroll
+      for (int p = 0; p < NP; ++p) t[p] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const s16x4 a = a_operand<BC>(xa, i);
+#pragma unroll
+        for (int p = 0; p < NP; ++p)
+          t[p] = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(
+              a, b_operand<SLOW>(st[d].q[p], i, tbl, lane_const[p], sc + 16 * p), t[p], 0, 0, 0);
+      }
+#pragma unroll
+      for (int p = 0; p < NP; ++p)
+        scale_acc(acc[p], t[p], aslot[p * 256 + j * 64 + 8 * d + (blk >> 1)]);
+    }
+    finish(acc);
+#pragma unroll
+    for (int p = 0; p < NP; ++p) acc[p] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    if (SLOW && it + 1 < n_items) sc = slow_code();
+    store_abs();
+  }
+}
+
 // 64 KB lookup table: replicas 0-31 from code_a, 32-63 from code_b (16 floats each).
 // Thread (wave w, replica r) writes the words i = 64*w + r + 256*n, n = 0..63, i.e.
 // packed byte v = w + 4n, whose nibbles are v >> 4 = n >> 2 and v & 15 = w + 4*(n & 3):
@@ -234,6 +349,7 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
   __shared__ int32_t s_idx[kDecMaxSlots];
   __shared__ float s_w[kDecMaxSlots];
   __shared__ const void *s_eptr[EMAX][4];  // w1_packed, w1_absmax, w3_packed, w3_absmax
+  __shared__ __attribute__((aligned(16))) float s_aslot[kFfnWaves][2 * 256];
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
@@ -485,6 +601,7 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
       for (int p = 0; p < 2; ++p) {
         P.wq[p] += 4 * row_bytes;
         P.wa[p] += 4 * row_blocks;
+        P.ab[p] += 4 * row_blocks;
       }
       return;
     }
@@ -498,6 +615,7 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
     for (int p = 0; p < 2; ++p) {
       P.wq[p] = (gq_t)s_eptr[e][2 * p] + row * row_bytes + blk * 16;
       P.wa[p] = (ga_t)s_eptr[e][2 * p + 1] + row * row_blocks + (blk >> 1);
+      P.ab[p] = (ga_t)s_eptr[e][2 * p + 1] + (size_t)ltile * 4 * row_blocks;
     }
     const int jj = (!bc && lanej < s_rt.counts[la]) ? lanej : 0;
     const int tok = s_rt.perm_tok[s_rt.offsets[la] + jj];
@@ -529,7 +647,11 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
   };
   auto slow_code = [&]() -> const float * { return s_code[s_rt.active[ca]]; };
   const bool slow = s_rt.slow1 != 0;
-  if (!slow && bc)
+  if (!slow && bc && nsq == 8 && T == 1)
+    stream_aligned<2, 8, false, true, true>(n_items, next_item, finish, hook, slow_code, s_tbl,
+                                            lane_const, row_blocks, s_aslot[wave],
+                                            (gx_t)x + blk * 32 + lanej * 8);
+  else if (!slow && bc)
     stream_items<2, 6, false, true>(n_items, nsq, next_item, finish, hook, slow_code, s_tbl, lane_const);
   else if (!slow)
     stream_items<2, 4, false, false>(n_items, nsq, next_item, finish, hook, slow_code, s_tbl, lane_const);
@@ -547,6 +669,7 @@ decode_down_kernel(const ExpertTable tab, const DecodeRoute *__restrict__ route,
   __shared__ __attribute__((aligned(16))) DecodeRoute s_rt;
   __shared__ float s_part[kDecMaxTilesPerWg][kDecMaxSlots][kFfnWaves][16];
   __shared__ const void *s_eptr[kDecMaxExperts][2];  // w2_packed, w2_absmax of every expert
+  __shared__ __attribute__((aligned(16))) float s_aslot[kFfnWaves][256];
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
@@ -597,6 +720,7 @@ decode_down_kernel(const ExpertTable tab, const DecodeRoute *__restrict__ route,
     if (++ltl < ntl && ltl != 0) {
       P.wq[0] += 4 * row_bytes;
       P.wa[0] += 4 * row_blocks;
+      P.ab[0] += 4 * row_blocks;
       return;
     }
     if (ltl == ntl) {
@@ -607,6 +731,7 @@ decode_down_kernel(const ExpertTable tab, const DecodeRoute *__restrict__ route,
     const int e = s_rt.active[la];
     P.wq[0] = (gq_t)s_eptr[e][0] + row * row_bytes + s_lo * 256 + blk * 16;
     P.wa[0] = (ga_t)s_eptr[e][1] + row * row_blocks + s_lo * 8 + (blk >> 1);
+    P.ab[0] = (ga_t)s_eptr[e][1] + (size_t)(r0 + ltl) * 4 * row_blocks + s_lo * 8;
     const int jj = (!bc && lanej < s_rt.counts[la]) ? lanej : 0;
     P.ap = (gx_t)h + (size_t)(s_rt.offsets[la] + jj) * F + (size_t)s_lo * kStageVals + blk * 32 +
            (bc ? lanej * 8 : 0);
@@ -630,7 +755,13 @@ decode_down_kernel(const ExpertTable tab, const DecodeRoute *__restrict__ route,
   };
   auto slow_code = [&]() -> const float * { return s_rt.code2[ca]; };
   const bool slow = s_rt.slow2 != 0;
-  if (!slow && bc)
+  if (!slow && bc && nsq == 7)
+    stream_aligned<1, 7, false, true, false>(n_items, next_item, finish, hook, slow_code, s_tbl,
+                                             lane_const, row_blocks, s_aslot[wave], nullptr);
+  else if (!slow && bc && nsq == 8)
+    stream_aligned<1, 8, false, true, false>(n_items, next_item, finish, hook, slow_code, s_tbl,
+                                             lane_const, row_blocks, s_aslot[wave], nullptr);
+  else if (!slow && bc)
     stream_items<1, 8, false, true>(n_items, nsq, next_item, finish, hook, slow_code, s_tbl, lane_const);
   else if (!slow)
     stream_items<1, 8, false, false>(n_items, nsq, next_item, finish, hook, slow_code, s_tbl, lane_const);
