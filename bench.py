@@ -42,6 +42,9 @@ def parse_args():
     p.add_argument("--cpu-seconds", type=float, default=15.0,
                    help="approximate CPU time budget of the oracle baseline sample")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                   help="only run 10 plain device copies of MIB MiB (the known-size kernel that "
+                        "scales the FETCH_SIZE / WRITE_SIZE counters) and exit")
     p.add_argument("--no-kernel-events", action="store_true",
                    help="do not bracket kernels with HIP events (headline timing only)")
     return p.parse_args()
@@ -78,6 +81,9 @@ def main() -> int:
         return 2
 
     import torch
+
+    if args.copy_calibration > 0:
+        return _copy_calibration(args.copy_calibration)
 
     from moeinfra_amd import _lib, ops, synth
 
@@ -254,6 +260,23 @@ class _HipEvents:
                 raise RuntimeError("hipEventElapsedTime failed")
             tot += ms.value
         return 1e3 * tot / len(pairs)
+
+
+def _copy_calibration(mib: int) -> int:
+    """Ten device-to-device copies of `mib` MiB (reads and writes exactly that many bytes
+    each): the reference kernel for converting FETCH_SIZE / WRITE_SIZE counter readings to
+    bytes."""
+    import torch
+
+    n = mib << 20
+    src = torch.empty(n, dtype=torch.uint8, device="cuda:0").fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(10):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": n, "copies": 10}), flush=True)
+    return 0
 
 
 def _traffic(name: str):

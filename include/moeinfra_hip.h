@@ -154,11 +154,14 @@ int moe_expert_swiglu_nf4(const moe_nf4_expert_t *expert, const void *x_bf16, in
 /* ---------------------------------------------------------------- whole layer
  * Router (K2) -> permute (K3) -> expert FFN (K4) -> combine (K5) in one call: the
  * device-resident form of MoELayer._forward_tokens (model/moe_layer.py:117-211) with
- * every routed expert resident.  Batches of up to 16 tokens route and group in one
- * kernel; with up to 4 tokens the combine runs inside the down projection, so a layer is
- * three kernel launches.  experts[e] must be valid for every e < E that the
- * router can select.  logits_bf16 may be NULL; weights_f32 [T,k] and idx_i64 [T,k]
- * receive the routing.  workspace >= moe_layer_workspace_bytes(T, k, E, H, F). */
+ * every routed expert resident.  Decode batches (T <= 4, T*k <= 8, E <= 16, H and F
+ * multiples of 512) run as two launches: routing and grouping inside the gate/up kernel,
+ * the weighted combine inside the down kernel; all E table entries must then be non-null.
+ * Larger batches: one routing + grouping kernel (T <= 16) or router + permute, then
+ * gate/up, down and combine.  Otherwise experts[e] must be valid for every e < E that
+ * the router can select.  logits_bf16 may be NULL; weights_f32 [T,k] and idx_i64 [T,k]
+ * receive the routing.  workspace >= moe_layer_workspace_bytes(T, k, E, H, F), 256-byte
+ * aligned. */
 int64_t moe_layer_workspace_bytes(int64_t T, int32_t k, int32_t E, int32_t H, int32_t F);
 int moe_layer_forward_nf4(const moe_nf4_expert_t *experts, int32_t E, const void *gate_bf16,
                           const void *bias_f32, const void *x_bf16, int64_t T, int32_t H,
@@ -168,7 +171,9 @@ int moe_layer_forward_nf4(const moe_nf4_expert_t *experts, int32_t E, const void
 
 /* moe_layer_forward_nf4 with hipEventRecord marks on the stream: events[0] before the
  * routing, events[1] after routing + grouping, events[2] after gate/up, events[3] after
- * down + combine.  The kernels are those of moe_layer_forward_nf4; for profiling. */
+ * down + combine.  In the two-launch decode form events[0] and events[1] are recorded
+ * back to back (the routing runs inside the gate/up kernel).  The kernels are those of
+ * moe_layer_forward_nf4; for profiling. */
 int moe_layer_forward_nf4_profiled(const moe_nf4_expert_t *experts, int32_t E,
                                    const void *gate_bf16, const void *bias_f32,
                                    const void *x_bf16, int64_t T, int32_t H, int32_t F,
