@@ -51,6 +51,16 @@ struct DecodeRoute {
   float code2[kDecMaxSlots][16];   // w2 codebook of each active expert
 };
 static_assert(sizeof(DecodeRoute) % 16 == 0, "descriptor is copied in 16-byte words");
+
+// The fields of DecodeRoute before code2 (a wave's private copy in the gate/up kernel).
+struct RouteHead {
+  int32_t n_active, bc, slow1, slow2;
+  int32_t active[kDecMaxSlots], counts[kDecMaxSlots], offsets[kDecMaxSlots];
+  int32_t perm_tok[kDecMaxSlots], slot_a[kDecMaxSlots], slot_m[kDecMaxSlots];
+  float slot_w[kDecMaxSlots];
+};
+static_assert(offsetof(DecodeRoute, code2) == sizeof(RouteHead), "DecodeRoute starts with RouteHead");
+constexpr int kRouteHeadWords = (int)(sizeof(RouteHead) / 4);
 constexpr int kRouteWords = (int)(sizeof(DecodeRoute) / 4);
 static_assert(kRouteWords <= kFfnThreads, "one descriptor word per thread");
 
@@ -194,8 +204,13 @@ __device__ __forceinline__ void stream_items(int n_items, int nsq, ItemFn &&next
 // Step d of item it issues the load of stage NSQ-1 of item it (d = 0) or of stage d-1 of
 // item it+1 (d >= 1; past the last item the last item's stages are re-read, unused).
 // next_item / finish / hook / slow_code as for stream_items; `arow` is the absmax row
-// stride (floats), `aslot` the wave's LDS slot (NP x 256 floats), `xbase` the lane's
+// stride (floats), `aslot` the wave's LDS slot (NP x kASlotFloats), `xbase` the lane's
 // activation chunk of stage 0 (XREG only).
+// Per-wave absmax slot of one item: 4 rows of up to 64 floats, rows padded to 72 floats so
+// that the four rows read in one instruction fall into different LDS banks.
+constexpr int kASlotRow = 72;
+constexpr int kASlotFloats = 4 * kASlotRow;
+
 template <int NP, int NX>
 struct StageQ {
   uint4 q[NP];
@@ -234,8 +249,9 @@ __device__ __forceinline__ void stream_aligned(int n_items, ItemFn &&next_item, 
     if (a_act) {
 #pragma unroll
       for (int p = 0; p < NP; ++p)
-        *reinterpret_cast<uint4 *>(aslot + p * 256 + a_row * 64 + a_col) = abuf[p];
+        *reinterpret_cast<uint4 *>(aslot + p * kASlotFloats + a_row * kASlotRow + a_col) = abuf[p];
     }
+    wave_lds_sync();  // every lane reads chunks other lanes stored
   };
   uint4 xr[XREG ? NSQ : 1];
   if (XREG) {
@@ -288,7 +304,7 @@ __device__ __forceinline__ void stream_aligned(int n_items, ItemFn &&next_item, 
       }
 #pragma unroll
       for (int p = 0; p < NP; ++p)
-        scale_acc(acc[p], t[p], aslot[p * 256 + j * 64 + 8 * d + (blk >> 1)]);
+        scale_acc(acc[p], t[p], aslot[p * kASlotFloats + j * kASlotRow + 8 * d + (blk >> 1)]);
     }
     finish(acc);
 #pragma unroll
@@ -298,20 +314,29 @@ __device__ __forceinline__ void stream_aligned(int n_items, ItemFn &&next_item, 
   }
 }
 
-// 64 KB lookup table: replicas 0-31 from code_a, 32-63 from code_b (16 floats each).
-// Thread (wave w, replica r) writes the words i = 64*w + r + 256*n, n = 0..63, i.e.
-// packed byte v = w + 4n, whose nibbles are v >> 4 = n >> 2 and v & 15 = w + 4*(n & 3):
-// 20 codebook reads into registers, then 64 stores and no further LDS reads.
-__device__ __forceinline__ void build_table(uint32_t *tbl, const float *code_a,
-                                            const float *code_b) {
+// 64 KB lookup table (see nf4_tile.h) from codebooks held in registers: thread (wave w,
+// replica r) writes the words i = 64*(w + 4n) + r, n = 0..63, i.e. packed byte v = w + 4n,
+// whose nibbles are v >> 4 = n >> 2 and v & 15 = w + 4*(n & 3); replicas r < 32 take c_a,
+// r >= 32 take c_b.  No LDS reads.
+__device__ __forceinline__ void build_table_regs(uint32_t *tbl, const float (&c_a)[16],
+                                                 const float (&c_b)[16]) {
   const int r = threadIdx.x & (kWave - 1);
   const int w = threadIdx.x >> 6;
-  const float *c = (r & 32) ? code_b : code_a;
+  const bool second = (r & 32) != 0;
   float hi[16], lo[4];
 #pragma unroll
-  for (int q = 0; q < 16; ++q) hi[q] = c[q];
+  for (int q = 0; q < 16; ++q) hi[q] = second ? c_b[q] : c_a[q];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) lo[q] = c[w + 4 * q];
+  for (int q = 0; q < 4; ++q) {
+    float va = c_a[0], vb = c_b[0];
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      if (i == w + 4 * q) {
+        va = c_a[i];
+        vb = c_b[i];
+      }
+    lo[q] = second ? vb : va;
+  }
 #pragma unroll
   for (int n = 0; n < 64; ++n) tbl[(w + 4 * n) * kWave + r] = pack_bf16x2(hi[n >> 2], lo[n & 3]);
 }
@@ -334,6 +359,116 @@ __device__ __forceinline__ float wave_sum_fast(float v) {
   return v;
 }
 
+// Reductions over the 16 lanes of a DPP row (every lane of the row gets the result).
+__device__ __forceinline__ float row_max16(float v) {
+  v = fmaxf(v, dpp_mov<0xB1>(v));   // quad_perm [1,0,3,2]
+  v = fmaxf(v, dpp_mov<0x4E>(v));   // quad_perm [2,3,0,1]
+  v = fmaxf(v, dpp_mov<0x124>(v));  // row_ror:4
+  v = fmaxf(v, dpp_mov<0x128>(v));  // row_ror:8
+  return v;
+}
+__device__ __forceinline__ float row_sum16(float v) {
+  v += dpp_mov<0xB1>(v);
+  v += dpp_mov<0x4E>(v);
+  v += dpp_mov<0x124>(v);
+  v += dpp_mov<0x128>(v);
+  return v;
+}
+
+// Routing of the T <= 4 tokens by one wave, lane (t = lane/16, e = lane%16) holding
+// expert e of token t: fp32 sum of the four waves' gate partials in fixed order -> bf16
+// logit (+ bias) -> fp32 softmax over the row -> top-k by k rounds of row arg-max (ties:
+// the lowest expert index) -> weights renormalised by their sum in rank order.  Then the
+// grouping of the T*k slots (s = t*k + j) by expert, ascending expert and ascending slot,
+// written to the wave's RouteHead.  Every wave runs this on its own copy: no barrier.
+struct RouteSummary {
+  int n_active;  // wave-uniform
+  bool bc;
+};
+
+template <int EMAX>
+__device__ __forceinline__ RouteSummary route_wave(RouteHead &rh, int32_t (&sl_e)[kDecMaxSlots],
+                                           float (&sl_w)[kDecMaxSlots],
+                                           const float (*s_part)[kDecMaxTokens][EMAX],
+                                           const float *bias, int T, int E, int k,
+                                           uint16_t *logits_out) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int t = lane >> 4;
+  const int e = lane & 15;
+  const bool valid = t < T && e < E;
+  float l = -INFINITY;
+  if (valid) {
+    const float v = s_part[0][t][e] + s_part[1][t][e] + s_part[2][t][e] + s_part[3][t][e];
+    const uint16_t lb = f32_to_bf16(v);
+    if (logits_out != nullptr) logits_out[t * E + e] = lb;
+    l = bf16_to_f32(lb);
+    if (bias != nullptr) l = l + bias[e];
+  }
+  const float m = row_max16(l);
+  const float pe = valid ? expf(l - m) : 0.0f;
+  const float p = pe / row_sum16(pe);
+  bool taken = false;
+  float wsum = 0.0f;
+  for (int j = 0; j < k; ++j) {
+    const bool cand = valid && !taken;
+    const float best = row_max16(cand ? p : -1.0f);
+    const uint64_t hit = __ballot(cand && p == best);
+    const uint64_t any = __ballot(cand);
+    int win = __builtin_ctzll(((hit >> (16 * t)) & 0xffffull) | 0x10000ull);  // row's lowest
+    // No lane equal to the maximum (NaN weights): the lowest untaken expert, as a strict
+    // '>' scan starting from "no choice yet" picks.
+    if (win > 15) win = __builtin_ctzll(((any >> (16 * t)) & 0xffffull) | 0x10000ull);
+    if (win > 15) win = 0;
+    taken |= e == win;
+    wsum += best;
+    if (e == 0 && t < T) {
+      sl_e[t * k + j] = win;
+      sl_w[t * k + j] = best;
+    }
+  }
+  if (e == 0 && t < T) {
+    for (int j = 0; j < k; ++j) sl_w[t * k + j] = sl_w[t * k + j] / wsum;
+  }
+  wave_lds_sync();  // the row leaders' slot entries are read by other lanes below
+  // Grouping: lane s < ns is slot s; expert counts by ballot, ascending expert order.
+  const int ns = T * k;
+  const int my_e = lane < ns ? sl_e[lane] : -1;
+  const uint64_t below = (1ull << lane) - 1ull;
+  int n_active = 0, run = 0, my_row = 0, my_a = 0, my_rank = 0;
+  bool multi = false;
+  for (int x = 0; x < E; ++x) {
+    const uint64_t mx = __ballot(my_e == x);
+    const int c = __popcll(mx);
+    if (c > 0) {
+      if (lane == 0) {
+        rh.active[n_active] = x;
+        rh.counts[n_active] = c;
+        rh.offsets[n_active] = run;
+      }
+      if (my_e == x) {
+        my_rank = __popcll(mx & below);
+        my_row = run + my_rank;
+        my_a = n_active;
+      }
+      multi |= c > 1;
+      ++n_active;
+      run += c;
+    }
+  }
+  if (lane < ns) {
+    rh.perm_tok[my_row] = lane / k;
+    rh.slot_a[lane] = my_a;
+    rh.slot_m[lane] = my_rank;
+    rh.slot_w[lane] = sl_w[lane];
+  }
+  if (lane == 0) {
+    rh.n_active = n_active;
+    rh.bc = multi ? 0 : 1;
+  }
+  wave_lds_sync();  // rh is read by every lane of the wave afterwards
+  return RouteSummary{n_active, !multi};
+}
+
 template <int EMAX>
 __global__ void __launch_bounds__(kFfnThreads, 2)
 decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
@@ -345,11 +480,11 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
   __shared__ float s_part[kFfnWaves][kDecMaxTokens][EMAX];
   // Codebooks of every expert: [0,16) w1, [16,32) w3, [32,48) w2 ([48,64) repeats w2).
   __shared__ float s_code[EMAX][kWave];
-  __shared__ __attribute__((aligned(16))) DecodeRoute s_rt;
-  __shared__ int32_t s_idx[kDecMaxSlots];
-  __shared__ float s_w[kDecMaxSlots];
   __shared__ const void *s_eptr[EMAX][4];  // w1_packed, w1_absmax, w3_packed, w3_absmax
-  __shared__ __attribute__((aligned(16))) float s_aslot[kFfnWaves][2 * 256];
+  __shared__ __attribute__((aligned(16))) RouteHead s_rtw[kFfnWaves];  // one copy per wave
+  __shared__ int32_t s_sle[kFfnWaves][kDecMaxSlots];                       // per wave: slot experts
+  __shared__ float s_slw[kFfnWaves][kDecMaxSlots];                         // per wave: slot weights
+  __shared__ __attribute__((aligned(16))) float s_aslot[kFfnWaves][2 * kASlotFloats];
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
@@ -420,6 +555,19 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
     const int f = lane & 3;
     pvw[q] = f == 0 ? p1 : f == 1 ? a1 : f == 2 ? p3 : a3;
   }
+  // Expert 0's w1 / w3 codebooks (scalar loads) for the lookup table, built now so the
+  // weight stream does not wait for it; experts whose codebooks differ take the
+  // per-nibble path.
+  float c1v[16], c3v[16];
+  {
+    const ga_t c1 = (ga_t)uniform_ptr(tab.e[0].w1_code);
+    const ga_t c3 = (ga_t)uniform_ptr(tab.e[0].w3_code);
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      c1v[q] = c1[q];
+      c3v[q] = c3[q];
+    }
+  }
   // Unconditional stores (clamped experts rewrite identical values), so the metadata
   // loads stay ahead of the products instead of sinking to a later conditional use.
 #pragma unroll
@@ -429,6 +577,7 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
     s_code[ee][lane] = cvw[q];
     s_eptr[ee][lane & 3] = pvw[q];
   }
+  build_table_regs(s_tbl, c1v, c3v);
   __builtin_amdgcn_sched_barrier(0);
   fma_round(0);
   for (int cb = NCH * kFfnThreads * 8; cb < H; cb += NCH * kFfnThreads * 8) {
@@ -448,131 +597,46 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
       }
     }
   }
+  // The only barrier of the routing phase: gate sums, codebooks, stream pointers and the
+  // lookup table are visible to every wave after it.
   __syncthreads();
 
-  // ---- softmax / top-k: one lane per token
-  if (tid < T) {
-    const int t = tid;
-    float p[EMAX];
-    float m = -INFINITY;
-#pragma unroll
-    for (int e = 0; e < EMAX; ++e) {
-      if (e < E) {
-        const float v = s_part[0][t][e] + s_part[1][t][e] + s_part[2][t][e] + s_part[3][t][e];
-        const uint16_t lb = f32_to_bf16(v);
-        if (wg0 && logits_out != nullptr) logits_out[t * E + e] = lb;
-        float l = bf16_to_f32(lb);
-        if (bias != nullptr) l = l + bias[e];
-        p[e] = l;
-        m = fmaxf(m, l);
-      }
-    }
-    float s = 0.0f;
-#pragma unroll
-    for (int e = 0; e < EMAX; ++e) {
-      if (e < E) {
-        p[e] = expf(p[e] - m);
-        s += p[e];
-      }
-    }
-#pragma unroll
-    for (int e = 0; e < EMAX; ++e)
-      if (e < E) p[e] = p[e] / s;
-    float topw[kDecMaxSlots];
-    int topi[kDecMaxSlots];
-    uint32_t taken = 0;
-    float wsum = 0.0f;
-    for (int j = 0; j < k; ++j) {
-      float best = -INFINITY;
-      int bi = -1;
-#pragma unroll
-      for (int e = 0; e < EMAX; ++e) {
-        if (e < E && !((taken >> e) & 1u) && (bi < 0 || p[e] > best)) {
-          best = p[e];
-          bi = e;
-        }
-      }
-      taken |= 1u << bi;
-      topw[j] = best;
-      topi[j] = bi;
-      wsum += best;
-    }
-    for (int j = 0; j < k; ++j) {
-      const float wv = topw[j] / wsum;
-      s_idx[t * k + j] = topi[j];
-      s_w[t * k + j] = wv;
-      if (wg0) {
-        w_out[t * k + j] = wv;
-        idx_out[t * k + j] = topi[j];
-      }
-    }
-  }
-  __syncthreads();
-
-  // ---- grouping (wave 0): expert `lane` has cnt slots; slot `lane` goes to row off_e+rank
+  // ---- routing and grouping, by every wave on its own copy
+  RouteHead &rt = s_rtw[wave];
+  const RouteSummary rs = route_wave<EMAX>(rt, s_sle[wave], s_slw[wave], s_part, bias, T, E, k,
+                                           (wg0 && wave == 0) ? logits_out : nullptr);
+  const int u = rs.n_active;
   const int ns = T * k;
-  if (wave == 0) {
-    int cnt = 0, off = 0;
-    if (lane < E) {
-      for (int s = 0; s < ns; ++s) {
-        const int e = s_idx[s];
-        cnt += e == lane;
-        off += e < lane;
-      }
-    }
-    const uint64_t amask = __ballot(lane < E && cnt > 0);
-    const int a_of = __popcll(amask & ((1ull << lane) - 1ull));
-    const int e_s = lane < ns ? s_idx[lane] : 0;
-    const int off_e = __shfl(off, e_s, kWave);
-    const int a_e = __shfl(a_of, e_s, kWave);
-    if (lane < E && cnt > 0) {
-      s_rt.active[a_of] = lane;
-      s_rt.counts[a_of] = cnt;
-      s_rt.offsets[a_of] = off;
+  // Codebook checks against expert 0 (the table's): lane c < 32 checks w1|w3 word c,
+  // lanes 32..47 the w2 words.
+  bool d1 = false, d2 = false;
+  for (int a = 0; a < u; ++a) {
+    const uint32_t mine = __builtin_bit_cast(uint32_t, s_code[rt.active[a]][lane]);
+    const uint32_t ref = __builtin_bit_cast(uint32_t, s_code[0][lane]);
+    if (lane < 32) d1 |= mine != ref;
+    else if (lane < 48) d2 |= mine != ref;
+  }
+  const bool slow1 = __ballot(d1) != 0;
+  const bool slow2 = __ballot(d2) != 0;
+  if (lane == 0) {
+    rt.slow1 = slow1 ? 1 : 0;
+    rt.slow2 = slow2 ? 1 : 0;
+  }
+  wave_lds_sync();
+  if (wg0 && wave == 0) {
+    const uint32_t *src = reinterpret_cast<const uint32_t *>(&rt);
+    uint32_t *dst = reinterpret_cast<uint32_t *>(route_out);
+    if (lane < kRouteHeadWords) dst[lane] = src[lane];
+    for (int i = lane; i < kDecMaxSlots * 16; i += kWave) {
+      const int a = i >> 4;
+      route_out->code2[a][i & 15] = a < u ? s_code[rt.active[a]][32 + (i & 15)] : 0.0f;
     }
     if (lane < ns) {
-      int rank = 0;
-      for (int s = 0; s < lane; ++s) rank += s_idx[s] == e_s;
-      s_rt.perm_tok[off_e + rank] = lane / k;
-      s_rt.slot_a[lane] = a_e;
-      s_rt.slot_m[lane] = rank;
-      s_rt.slot_w[lane] = s_w[lane];
-    }
-    const bool multi = __ballot(lane < E && cnt > 1) != 0;
-    if (lane == 0) {
-      s_rt.n_active = __popcll(amask);
-      s_rt.bc = multi ? 0 : 1;
+      w_out[lane] = s_slw[wave][lane];
+      idx_out[lane] = s_sle[wave][lane];
     }
   }
-  __syncthreads();
-
-  // ---- codebook flags, expert pointers, descriptor
-  const int u = s_rt.n_active;
-  if (wave == 0) {
-    const int e0 = s_rt.active[0];
-    bool d1 = false, d2 = false;
-    for (int a = 1; a < u; ++a) {
-      const int e = s_rt.active[a];
-      if (lane < 32)
-        d1 |= __builtin_bit_cast(uint32_t, s_code[e][lane]) !=
-              __builtin_bit_cast(uint32_t, s_code[e0][lane]);
-      if (wg0 && lane < 16)
-        d2 |= __builtin_bit_cast(uint32_t, s_code[e][32 + lane]) !=
-              __builtin_bit_cast(uint32_t, s_code[e0][32 + lane]);
-    }
-    const bool slow1 = __ballot(d1) != 0;
-    const bool slow2 = __ballot(d2) != 0;
-    if (lane == 0) {
-      s_rt.slow1 = slow1 ? 1 : 0;
-      s_rt.slow2 = slow2 ? 1 : 0;
-    }
-  } else if (wave == 2 && wg0) {
-    for (int i = lane; i < u * 16; i += kWave)
-      s_rt.code2[i >> 4][i & 15] = s_code[s_rt.active[i >> 4]][32 + (i & 15)];
-  }
-  __syncthreads();
-  if (wg0 && tid < kRouteWords)
-    reinterpret_cast<uint32_t *>(route_out)[tid] = reinterpret_cast<const uint32_t *>(&s_rt)[tid];
+  const RouteHead &s_rt = rt;
 
   // ---- w1/w3 stream over this wave's range of the (active expert, tile) list
   const int lanej = lane & 3;
@@ -587,8 +651,7 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
   const size_t row_bytes = (size_t)(H >> 1);
   const size_t row_blocks = (size_t)(H >> 6);
   const uint32_t lane_const[2] = {(uint32_t)(lane & 31) << 2, ((uint32_t)(lane & 31) << 2) | 128u};
-  const float *code0 = s_code[s_rt.active[0]];
-  const bool bc = s_rt.bc != 0;
+  const bool bc = rs.bc;
   const int a_start = i0 / tiles_e;
   const int tile_start = i0 - a_start * tiles_e;
 
@@ -641,12 +704,9 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
       ++ca;
     }
   };
-  auto hook = [&]() {
-    build_table(s_tbl, code0, code0 + 16);
-    __syncthreads();
-  };
+  auto hook = [&]() {};
   auto slow_code = [&]() -> const float * { return s_code[s_rt.active[ca]]; };
-  const bool slow = s_rt.slow1 != 0;
+  const bool slow = slow1;
   if (!slow && bc && nsq == 8 && T == 1)
     stream_aligned<2, 8, false, true, true>(n_items, next_item, finish, hook, slow_code, s_tbl,
                                             lane_const, row_blocks, s_aslot[wave],
@@ -669,7 +729,7 @@ decode_down_kernel(const ExpertTable tab, const DecodeRoute *__restrict__ route,
   __shared__ __attribute__((aligned(16))) DecodeRoute s_rt;
   __shared__ float s_part[kDecMaxTilesPerWg][kDecMaxSlots][kFfnWaves][16];
   __shared__ const void *s_eptr[kDecMaxExperts][2];  // w2_packed, w2_absmax of every expert
-  __shared__ __attribute__((aligned(16))) float s_aslot[kFfnWaves][256];
+  __shared__ __attribute__((aligned(16))) float s_aslot[kFfnWaves][kASlotFloats];
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
@@ -696,6 +756,15 @@ decode_down_kernel(const ExpertTable tab, const DecodeRoute *__restrict__ route,
     if (e < E && lane < 2) s_eptr[e][lane] = lane ? pa[q] : pk[q];
   }
   if (tid < kRouteWords) reinterpret_cast<uint32_t *>(&s_rt)[tid] = rw;
+  // Lookup table from expert 0's w2 codebook (scalar loads), built before the barrier;
+  // the gate/up kernel flagged (slow2) active experts whose codebook differs from it.
+  {
+    float c2v[16];
+    const ga_t c2 = (ga_t)uniform_ptr(tab.e[0].w2_code);
+#pragma unroll
+    for (int q = 0; q < 16; ++q) c2v[q] = c2[q];
+    build_table_regs(s_tbl, c2v, c2v);
+  }
   __syncthreads();
   const int u = s_rt.n_active;
 
@@ -749,10 +818,7 @@ decode_down_kernel(const ExpertTable tab, const DecodeRoute *__restrict__ route,
       ++ca;
     }
   };
-  auto hook = [&]() {
-    build_table(s_tbl, s_rt.code2[0], s_rt.code2[0]);
-    __syncthreads();
-  };
+  auto hook = [&]() {};
   auto slow_code = [&]() -> const float * { return s_rt.code2[ca]; };
   const bool slow = s_rt.slow2 != 0;
   if (!slow && bc && nsq == 7)

@@ -290,6 +290,7 @@ gemv4_kernel(const ExpertTable tab, const uint16_t *__restrict__ act, int H, int
     }
     const bool slow = __any(diff);
     if (slow && lane < 32) s_slow[wave][lane] = mine;
+    wave_lds_sync();  // the whole wave reads s_slow[wave] below
     const bool bc = rt.counts[e] == 1;
     const float *sc = s_slow[wave];
     if (!slow && bc)

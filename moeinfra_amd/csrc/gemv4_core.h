@@ -84,6 +84,17 @@ __device__ __forceinline__ s16x4 b_operand(const uint4 &q, int i, const uint32_t
   return as_s16x4(b0, b1);
 }
 
+// Orders LDS writes of some lanes of a wave before LDS reads of other lanes of the same
+// wave.  Lanes are separate threads to the compiler: without this, a store by one lane and
+// a load of the same location by another are a race that the compiler may reorder (for
+// example by forwarding the stored value to the storing lane and reading LDS early for the
+// others).  Wavefront-scope release/acquire fences around a wave barrier; no s_barrier.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 __device__ __forceinline__ float lanes_sum16(float v) {
   // Sum over the 16 lanes that share l % 4 (the block index occupies lane bits 2..5).
   v += __shfl_xor(v, 4, kWave);
