@@ -195,20 +195,47 @@ __device__ __forceinline__ void stream_items(int n_items, int nsq, ItemFn &&next
 }
 
 // Aligned stream: every item has exactly NSQ stages (2 <= NSQ <= 8) and the register
-// pipeline is NSQ deep, so unrolled step d always handles stage d of an item.  That allows
+// pipeline is DEPTH stages deep with DEPTH dividing NSQ, so unrolled step d always handles
+// stage d of an item and buffer d % DEPTH.  That allows
 //  * the item's absmax block (4 rows x 8*NSQ floats) to be fetched with one 16-byte load
 //    per lane when the load side enters the item, and staged in the wave's LDS slot at
 //    the item boundary, instead of one 4-byte load per lane and stage;
 //  * with XREG (one token for the whole stream, single-token broadcast form), the
 //    activation chunks of all NSQ stages to stay in registers, loaded once.
-// Step d of item it issues the load of stage NSQ-1 of item it (d = 0) or of stage d-1 of
-// item it+1 (d >= 1; past the last item the last item's stages are re-read, unused).
+// Step d of item it issues the load of stage d + DEPTH - 1 of the stage sequence: stage
+// d + DEPTH - 1 of item it, or stage d + DEPTH - 1 - NSQ of item it+1 (past the last item
+// the last item's stages are re-read, unused).  At most DEPTH stages per projection are in
+// flight per wave: the depth sets the bytes a wave keeps outstanding.
 // next_item / finish / hook / slow_code as for stream_items; `arow` is the absmax row
 // stride (floats), `aslot` the wave's LDS slot (NP x kASlotFloats), `xbase` the lane's
-// activation chunk of stage 0 (XREG only).
+// activation chunk of stage 0 (XREG only).  With BC the four MFMA result rows are the same
+// token, and only row 0 of `acc` is accumulated (finish must read row 0 only).
 // Per-wave absmax slot of one item: 4 rows of up to 64 floats, rows padded to 72 floats so
 // that the four rows read in one instruction fall into different LDS banks.
+// The 16-level NF4 codebook (QLoRA; bitsandbytes' NF4 table, the `code` tensor of the quant
+// state, transfer/nf4_reconstruct.py:48) as fp32: the decode kernels build their lookup
+// table from these values and route experts whose codebooks differ to the per-nibble path.
+constexpr float kNf4Code[16] = {
+    -1.0f, -0.6961928009986877f, -0.5250730514526367f, -0.39491748809814453f,
+    -0.28444138169288635f, -0.18477343022823334f, -0.09105003625154495f, 0.0f,
+    0.07958029955625534f, 0.16093020141124725f, 0.24611230194568634f, 0.33791524242401123f,
+    0.44070982933044434f, 0.5626170039176941f, 0.7229568362236023f, 1.0f};
+
 constexpr int kASlotRow = 72;
+#ifndef MOE_GATEUP_DEPTH
+#define MOE_GATEUP_DEPTH 4
+#endif
+// Pipeline depth of the single-token gate/up stream (stages of both projections).
+constexpr int kGateUpDepth = MOE_GATEUP_DEPTH;
+#ifndef MOE_LOOKAHEAD
+#define MOE_LOOKAHEAD 1
+#endif
+// Table lookups one stage ahead of the products in the aligned stream.
+constexpr bool kLookahead = MOE_LOOKAHEAD != 0;
+#ifndef MOE_SPLIT_CHAINS
+#define MOE_SPLIT_CHAINS 1
+#endif
+constexpr bool kSplitChains = MOE_SPLIT_CHAINS != 0;
 constexpr int kASlotFloats = 4 * kASlotRow;
 
 template <int NP, int NX>
@@ -217,15 +244,19 @@ struct StageQ {
   uint4 xa[NX];
 };
 
-template <int NP, int NSQ, bool SLOW, bool BC, bool XREG, typename ItemFn, typename FinishFn,
-          typename Hook, typename SlowFn>
+template <int NP, int NSQ, int DEPTH, bool SLOW, bool BC, bool XREG, bool LA, typename ItemFn,
+          typename FinishFn, typename Hook, typename SlowFn>
 __device__ __forceinline__ void stream_aligned(int n_items, ItemFn &&next_item, FinishFn &&finish,
                                                Hook &&hook, SlowFn &&slow_code,
                                                const uint32_t *tbl,
                                                const uint32_t (&lane_const)[NP], size_t arow,
                                                float *aslot, gx_t xbase) {
   static_assert(NSQ >= 2 && NSQ <= 8, "an item's absmax block must fit one load per lane");
+  static_assert(DEPTH >= 2 && DEPTH <= NSQ && NSQ % DEPTH == 0, "depth must divide NSQ");
+  static_assert(!LA || (!SLOW && DEPTH >= 3), "lookahead needs the table path and depth >= 3");
   constexpr int NX = XREG ? 1 : (BC ? 1 : 4);
+  // First step that loads a stage of the next item.
+  constexpr int kNext = NSQ - DEPTH + 1;
   const int lane = threadIdx.x & (kWave - 1);
   const int blk = lane >> 2;
   const int j = lane & 3;
@@ -268,9 +299,9 @@ __device__ __forceinline__ void stream_aligned(int n_items, ItemFn &&next_item, 
       for (int i = 0; i < NX; ++i) st.xa[i] = ld_u4(px + 8 * i);
     }
   };
-  StageQ<NP, NX> st[NSQ];
+  StageQ<NP, NX> st[DEPTH];
 #pragma unroll
-  for (int d = 0; d < NSQ - 1; ++d) {
+  for (int d = 0; d < DEPTH - 1; ++d) {
     load(st[d], d);
     __builtin_amdgcn_sched_barrier(0);
   }
@@ -281,30 +312,85 @@ __device__ __forceinline__ void stream_aligned(int n_items, ItemFn &&next_item, 
 #pragma unroll
   for (int p = 0; p < NP; ++p) acc[p] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   const float *sc = SLOW ? slow_code() : nullptr;
+  // LA: the table lookups of a stage are issued one step ahead, interleaved with the
+  // products of the stage before, so that their LDS latency overlaps the MFMAs.
+  s16x4 bq[LA ? NP : 1][8];
+  if (LA) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int p = 0; p < NP; ++p) bq[p][i] = b_operand<false>(st[0].q[p], i, tbl, lane_const[p], nullptr);
+  }
   for (int it = 0; it < n_items; ++it) {
 #pragma unroll
     for (int d = 0; d < NSQ; ++d) {
-      if (d == 1 && it + 1 < n_items) {
+      if (d == kNext && it + 1 < n_items) {
         next_item(P);
         load_abs();
       }
-      load(st[(d + NSQ - 1) % NSQ], d == 0 ? NSQ - 1 : d - 1);
+      const int g = d + DEPTH - 1;  // stage sequence index of this step's load
+      load(st[g % DEPTH], g < NSQ ? g : g - NSQ);
       __builtin_amdgcn_sched_barrier(0);  // this step's loads before its products
-      const uint4 *xa = XREG ? &xr[d] : st[d].xa;
+      const StageQ<NP, NX> &cur = st[d % DEPTH];
+      const uint4 *xa = XREG ? &xr[d] : cur.xa;
+      float scl[NP];
+#pragma unroll
+      for (int p = 0; p < NP; ++p) scl[p] = aslot[p * kASlotFloats + j * kASlotRow + 8 * d + (blk >> 1)];
       f32x4 t[NP];
 #pragma unroll
       for (int p = 0; p < NP; ++p) t[p] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      if (LA) {
+        // Stage d+1 is in buffer (d+1) % DEPTH (for d = NSQ-1: the next item's stage 0, or
+        // a re-read of this item's when it is the last one).
+        const StageQ<NP, NX> &nxt = st[(d + 1) % DEPTH];
+        s16x4 bn[LA ? NP : 1][8];
+        f32x4 t2[NP];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const s16x4 a = a_operand<BC>(xa, i);
+        for (int p = 0; p < NP; ++p) t2[p] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int p = 0; p < NP; ++p)
-          t[p] = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(
-              a, b_operand<SLOW>(st[d].q[p], i, tbl, lane_const[p], sc + 16 * p), t[p], 0, 0, 0);
+        for (int i = 0; i < 8; ++i) {
+#pragma unroll
+          for (int p = 0; p < NP; ++p) bn[p][i] = b_operand<false>(nxt.q[p], i, tbl, lane_const[p], nullptr);
+          const s16x4 a = a_operand<BC>(xa, i);
+#pragma unroll
+          for (int p = 0; p < NP; ++p) {
+            // Two accumulators per projection (even / odd i) halve the dependent chain.
+            if (kSplitChains && (i & 1))
+              t2[p] = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(a, bq[p][i], t2[p], 0, 0, 0);
+            else
+              t[p] = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(a, bq[p][i], t[p], 0, 0, 0);
+          }
+        }
+        if (kSplitChains) {
+#pragma unroll
+          for (int p = 0; p < NP; ++p) {
+            if (BC)
+              t[p][0] += t2[p][0];
+            else
+              t[p] += t2[p];
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+#pragma unroll
+          for (int p = 0; p < NP; ++p) bq[p][i] = bn[p][i];
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const s16x4 a = a_operand<BC>(xa, i);
+#pragma unroll
+          for (int p = 0; p < NP; ++p)
+            t[p] = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(
+                a, b_operand<SLOW>(cur.q[p], i, tbl, lane_const[p], sc + 16 * p), t[p], 0, 0, 0);
+        }
       }
 #pragma unroll
-      for (int p = 0; p < NP; ++p)
-        scale_acc(acc[p], t[p], aslot[p * kASlotFloats + j * kASlotRow + 8 * d + (blk >> 1)]);
+      for (int p = 0; p < NP; ++p) {
+        if (BC)  // one token in every row: only row 0 is accumulated
+          acc[p][0] = fmaf(scl[p], t[p][0], acc[p][0]);
+        else
+          scale_acc(acc[p], t[p], scl[p]);
+      }
     }
     finish(acc);
 #pragma unroll
@@ -314,31 +400,25 @@ __device__ __forceinline__ void stream_aligned(int n_items, ItemFn &&next_item, 
   }
 }
 
-// 64 KB lookup table (see nf4_tile.h) from codebooks held in registers: thread (wave w,
-// replica r) writes the words i = 64*(w + 4n) + r, n = 0..63, i.e. packed byte v = w + 4n,
-// whose nibbles are v >> 4 = n >> 2 and v & 15 = w + 4*(n & 3); replicas r < 32 take c_a,
-// r >= 32 take c_b.  No LDS reads.
+// 64 KB lookup table (see nf4_tile.h) from codebooks held in registers.  Word
+// 64*v + r holds the bf16 pair of packed byte v for replica r; replicas 0-31 use c_a,
+// 32-63 use c_b, so four consecutive replicas hold the same word.  Thread tid writes
+// words 4*tid + 1024*q .. +3 (q = 0..15) with one 16-byte store each: byte
+// v = tid/16 + 16q, i.e. high nibble q and low nibble tid/16, replicas 4*(tid%16) .. +3.
 __device__ __forceinline__ void build_table_regs(uint32_t *tbl, const float (&c_a)[16],
                                                  const float (&c_b)[16]) {
-  const int r = threadIdx.x & (kWave - 1);
-  const int w = threadIdx.x >> 6;
-  const bool second = (r & 32) != 0;
-  float hi[16], lo[4];
+  const int tid = threadIdx.x;
+  const bool second = (tid & 8) != 0;  // replica 4*(tid%16) >= 32
+  const int lo_nib = tid >> 4;
+  float lo = c_a[0];
 #pragma unroll
-  for (int q = 0; q < 16; ++q) hi[q] = second ? c_b[q] : c_a[q];
+  for (int i = 0; i < 16; ++i)
+    if (i == lo_nib) lo = second ? c_b[i] : c_a[i];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    float va = c_a[0], vb = c_b[0];
-#pragma unroll
-    for (int i = 0; i < 16; ++i)
-      if (i == w + 4 * q) {
-        va = c_a[i];
-        vb = c_b[i];
-      }
-    lo[q] = second ? vb : va;
+  for (int q = 0; q < 16; ++q) {
+    const uint32_t w = pack_bf16x2(second ? c_b[q] : c_a[q], lo);
+    *reinterpret_cast<uint4 *>(tbl + 4 * tid + 1024 * q) = make_uint4(w, w, w, w);
   }
-#pragma unroll
-  for (int n = 0; n < 64; ++n) tbl[(w + 4 * n) * kWave + r] = pack_bf16x2(hi[n >> 2], lo[n & 3]);
 }
 
 // Sum over the 64 lanes, every lane gets the result: DPP within each row of 16 lanes
@@ -491,55 +571,52 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const bool wg0 = blockIdx.x == 0;
 
-  // ---- gate products: each thread sums NCH 8-value chunks per round (all of a round's
-  // loads issued before any product), then wave and workgroup sums.  The first round's
-  // loads go out first; the per-expert metadata loads follow them.
-  constexpr int NCH = EMAX <= 8 ? 2 : 1;
-  constexpr int EPW = EMAX / kFfnWaves;  // experts per wave for the metadata loads
-  float acc[kDecMaxTokens][EMAX];
+  // ---- lookup table from the NF4 codebook constants: no load in front of it, so it is
+  // written while the gate loads below are in flight.  Experts whose codebooks differ from
+  // these values take the per-nibble path (checked after the routing).
+  {
+    float cst[16];
 #pragma unroll
-  for (int t = 0; t < kDecMaxTokens; ++t)
+    for (int q = 0; q < 16; ++q) cst[q] = kNf4Code[q];
+    build_table_regs(s_tbl, cst, cst);
+  }
+
+  // ---- gate products on the 4x4x4 MFMA: wave w takes H range [w*H/4, (w+1)*H/4) in
+  // chunks of 128 values; lane (b = lane/4, j = lane%4) holds values 8b .. 8b+7 of the
+  // chunk of token j (A rows, tokens >= T repeat a valid row and are ignored) and of
+  // expert 4g + j (B columns).  D[b][m][n] sums block b's slice for token m and expert
+  // 4g + n; a butterfly over the 16 blocks completes the wave's partial sums.
+  constexpr int G = EMAX / 4;                 // expert groups of four
+  constexpr int CPR = EMAX <= 8 ? 8 : 4;      // chunks per load round
+  const int lj = lane & 3;
+  const int lb = lane >> 2;
+  const int hq = H / kFfnWaves;               // multiple of 128
+  const int n_chunks = hq / 128;
+  const gx_t xrow = (gx_t)x + (size_t)(lj < T ? lj : T - 1) * H + (size_t)wave * hq + 8 * lb;
+  gx_t grow[G];
 #pragma unroll
-    for (int e = 0; e < EMAX; ++e) acc[t][e] = 0.0f;
-  uint4 xv[NCH][kDecMaxTokens];
-  uint4 gv[NCH][EMAX];
-  auto load_round = [&](int cb) {
+  for (int g = 0; g < G; ++g) {
+    const int e = 4 * g + lj;
+    grow[g] = (gx_t)gate + (size_t)(e < E ? e : E - 1) * H + (size_t)wave * hq + 8 * lb;
+  }
+  f32x4 gacc[G];
 #pragma unroll
-    for (int h = 0; h < NCH; ++h) {
-      int c = cb + (h * kFfnThreads + tid) * 8;
-      c = c < H ? c : 0;
+  for (int g = 0; g < G; ++g) gacc[g] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  uint4 xv[CPR], gv[CPR][G];
+  auto load_round = [&](int c0) {
 #pragma unroll
-      for (int t = 0; t < kDecMaxTokens; ++t)
-        xv[h][t] = *reinterpret_cast<const uint4 *>(x + (int64_t)(t < T ? t : 0) * H + c);
+    for (int c = 0; c < CPR; ++c) {
+      const int cc = c0 + c < n_chunks ? c0 + c : n_chunks - 1;  // clamped re-read, unused
+      xv[c] = ld_u4(xrow + cc * 128);
 #pragma unroll
-      for (int e = 0; e < EMAX; ++e)
-        gv[h][e] = *reinterpret_cast<const uint4 *>(gate + (int64_t)(e < E ? e : E - 1) * H + c);
-    }
-  };
-  auto fma_round = [&](int cb) {
-#pragma unroll
-    for (int h = 0; h < NCH; ++h) {
-      if (cb + (h * kFfnThreads + tid) * 8 >= H) continue;
-#pragma unroll
-      for (int t = 0; t < kDecMaxTokens; ++t) {
-        if (t >= T) continue;
-        const uint32_t xw[4] = {xv[h][t].x, xv[h][t].y, xv[h][t].z, xv[h][t].w};
-#pragma unroll
-        for (int e = 0; e < EMAX; ++e) {
-          const uint32_t gw[4] = {gv[h][e].x, gv[h][e].y, gv[h][e].z, gv[h][e].w};
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            acc[t][e] = fmaf(bf16lo_to_f32(xw[q]), bf16lo_to_f32(gw[q]), acc[t][e]);
-            acc[t][e] = fmaf(bf16hi_to_f32(xw[q]), bf16hi_to_f32(gw[q]), acc[t][e]);
-          }
-        }
-      }
+      for (int g = 0; g < G; ++g) gv[c][g] = ld_u4(grow[g] + cc * 128);
     }
   };
   load_round(0);
   // Metadata of experts wave + 4q (wave-uniform, so the table entries are scalar loads):
   // lane l < 16 reads w1 code[l], 16..31 w3 code[l-16], 32..63 w2 code[l & 15]; lane f < 4
   // keeps stream pointer f (w1_packed, w1_absmax, w3_packed, w3_absmax).
+  constexpr int EPW = EMAX / kFfnWaves;
   float cvw[EPW];
   const void *pvw[EPW];
 #pragma unroll
@@ -555,47 +632,45 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
     const int f = lane & 3;
     pvw[q] = f == 0 ? p1 : f == 1 ? a1 : f == 2 ? p3 : a3;
   }
-  // Expert 0's w1 / w3 codebooks (scalar loads) for the lookup table, built now so the
-  // weight stream does not wait for it; experts whose codebooks differ take the
-  // per-nibble path.
-  float c1v[16], c3v[16];
-  {
-    const ga_t c1 = (ga_t)uniform_ptr(tab.e[0].w1_code);
-    const ga_t c3 = (ga_t)uniform_ptr(tab.e[0].w3_code);
+  __builtin_amdgcn_sched_barrier(0);
+  for (int c0 = 0; c0 < n_chunks; c0 += CPR) {
+    if (c0 > 0) {
+      load_round(c0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
 #pragma unroll
-    for (int q = 0; q < 16; ++q) {
-      c1v[q] = c1[q];
-      c3v[q] = c3[q];
+    for (int c = 0; c < CPR; ++c) {
+      if (c0 + c >= n_chunks) break;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const s16x4 av = h ? as_s16x4(xv[c].z, xv[c].w) : as_s16x4(xv[c].x, xv[c].y);
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          const s16x4 bv = h ? as_s16x4(gv[c][g].z, gv[c][g].w) : as_s16x4(gv[c][g].x, gv[c][g].y);
+          gacc[g] = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(av, bv, gacc[g], 0, 0, 0);
+        }
+      }
     }
   }
-  // Unconditional stores (clamped experts rewrite identical values), so the metadata
-  // loads stay ahead of the products instead of sinking to a later conditional use.
+  // Butterfly over the blocks for the T token rows; lane j of block 0 writes the wave's
+  // partial sums of experts 4g + j.
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int m = 0; m < kDecMaxTokens; ++m) {
+      if (m < T) {
+        const float v = lanes_sum16(gacc[g][m]);
+        const int e = 4 * g + lj;
+        if (lb == 0 && e < E) s_part[wave][m][e] = v;
+      }
+    }
+  // Unconditional stores (clamped experts rewrite identical values).
 #pragma unroll
   for (int q = 0; q < EPW; ++q) {
     const int e = wave + kFfnWaves * q;
     const int ee = e < E ? e : E - 1;
     s_code[ee][lane] = cvw[q];
     s_eptr[ee][lane & 3] = pvw[q];
-  }
-  build_table_regs(s_tbl, c1v, c3v);
-  __builtin_amdgcn_sched_barrier(0);
-  fma_round(0);
-  for (int cb = NCH * kFfnThreads * 8; cb < H; cb += NCH * kFfnThreads * 8) {
-    load_round(cb);
-    __builtin_amdgcn_sched_barrier(0);
-    fma_round(cb);
-  }
-#pragma unroll
-  for (int t = 0; t < kDecMaxTokens; ++t) {
-    if (t < T) {
-#pragma unroll
-      for (int e = 0; e < EMAX; ++e) {
-        if (e < E) {
-          const float v = wave_sum_fast(acc[t][e]);
-          if (lane == 0) s_part[wave][t][e] = v;
-        }
-      }
-    }
   }
   // The only barrier of the routing phase: gate sums, codebooks, stream pointers and the
   // lookup table are visible to every wave after it.
@@ -607,12 +682,16 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
                                            (wg0 && wave == 0) ? logits_out : nullptr);
   const int u = rs.n_active;
   const int ns = T * k;
-  // Codebook checks against expert 0 (the table's): lane c < 32 checks w1|w3 word c,
+  // Codebook checks against the table's NF4 values: lane c < 32 checks w1|w3 word c,
   // lanes 32..47 the w2 words.
+  float ref_f = kNf4Code[0];
+#pragma unroll
+  for (int q = 1; q < 16; ++q)
+    if ((lane & 15) == q) ref_f = kNf4Code[q];
+  const uint32_t ref = __builtin_bit_cast(uint32_t, ref_f);
   bool d1 = false, d2 = false;
   for (int a = 0; a < u; ++a) {
     const uint32_t mine = __builtin_bit_cast(uint32_t, s_code[rt.active[a]][lane]);
-    const uint32_t ref = __builtin_bit_cast(uint32_t, s_code[0][lane]);
     if (lane < 32) d1 |= mine != ref;
     else if (lane < 48) d2 |= mine != ref;
   }
@@ -686,11 +765,14 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
   };
   // Consume side: (ca, ctile) walks the same items for the h stores.
   int ca = a_start, ctile = tile_start;
-  auto finish = [&](f32x4 (&ac)[2]) {
+  // nrows: MFMA result rows that hold tokens (1 on the single-token path, whose other rows
+  // are never accumulated).
+  auto finish_rows = [&](f32x4 (&ac)[2], int nrows) {
 #pragma unroll
     for (int p = 0; p < 2; ++p)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) ac[p][q] = lanes_sum16(ac[p][q]);
+      for (int q = 0; q < 4; ++q)
+        if (q < nrows) ac[p][q] = lanes_sum16(ac[p][q]);
     if (blk == 0) {
       const int row = ctile * 4 + lanej;
       const int cnt = s_rt.counts[ca];
@@ -704,11 +786,13 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
       ++ca;
     }
   };
+  auto finish = [&](f32x4 (&ac)[2]) { finish_rows(ac, 4); };
+  auto finish1 = [&](f32x4 (&ac)[2]) { finish_rows(ac, 1); };
   auto hook = [&]() {};
   auto slow_code = [&]() -> const float * { return s_code[s_rt.active[ca]]; };
   const bool slow = slow1;
   if (!slow && bc && nsq == 8 && T == 1)
-    stream_aligned<2, 8, false, true, true>(n_items, next_item, finish, hook, slow_code, s_tbl,
+    stream_aligned<2, 8, kGateUpDepth, false, true, true, kLookahead>(n_items, next_item, finish1, hook, slow_code, s_tbl,
                                             lane_const, row_blocks, s_aslot[wave],
                                             (gx_t)x + blk * 32 + lanej * 8);
   else if (!slow && bc)
@@ -756,14 +840,13 @@ decode_down_kernel(const ExpertTable tab, const DecodeRoute *__restrict__ route,
     if (e < E && lane < 2) s_eptr[e][lane] = lane ? pa[q] : pk[q];
   }
   if (tid < kRouteWords) reinterpret_cast<uint32_t *>(&s_rt)[tid] = rw;
-  // Lookup table from expert 0's w2 codebook (scalar loads), built before the barrier;
-  // the gate/up kernel flagged (slow2) active experts whose codebook differs from it.
+  // Lookup table from the NF4 codebook constants, built before the barrier; the gate/up
+  // kernel flagged (slow2) active experts whose w2 codebook differs from them.
   {
-    float c2v[16];
-    const ga_t c2 = (ga_t)uniform_ptr(tab.e[0].w2_code);
+    float cst[16];
 #pragma unroll
-    for (int q = 0; q < 16; ++q) c2v[q] = c2[q];
-    build_table_regs(s_tbl, c2v, c2v);
+    for (int q = 0; q < 16; ++q) cst[q] = kNf4Code[q];
+    build_table_regs(s_tbl, cst, cst);
   }
   __syncthreads();
   const int u = s_rt.n_active;
@@ -806,26 +889,32 @@ decode_down_kernel(const ExpertTable tab, const DecodeRoute *__restrict__ route,
            (bc ? lanej * 8 : 0);
   };
   int ca = 0, ctl = 0;
-  auto finish = [&](f32x4 (&ac)[1]) {
+  // nrows: result rows to keep (1 when the stream accumulated row 0 only; the combine then
+  // reads row 0, slot_m being 0 for every slot).
+  auto finish_rows = [&](f32x4 (&ac)[1], int nrows) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) ac[0][q] = lanes_sum16(ac[0][q]);
+    for (int q = 0; q < 4; ++q)
+      if (q < nrows) ac[0][q] = lanes_sum16(ac[0][q]);
     if (blk == 0) {
 #pragma unroll
-      for (int m = 0; m < 4; ++m) s_part[ctl][ca][wave][lanej * 4 + m] = ac[0][m];
+      for (int m = 0; m < 4; ++m)
+        if (m < nrows) s_part[ctl][ca][wave][lanej * 4 + m] = ac[0][m];
     }
     if (++ctl == ntl) {
       ctl = 0;
       ++ca;
     }
   };
+  auto finish = [&](f32x4 (&ac)[1]) { finish_rows(ac, 4); };
+  auto finish1 = [&](f32x4 (&ac)[1]) { finish_rows(ac, 1); };
   auto hook = [&]() {};
   auto slow_code = [&]() -> const float * { return s_rt.code2[ca]; };
   const bool slow = s_rt.slow2 != 0;
   if (!slow && bc && nsq == 7)
-    stream_aligned<1, 7, false, true, false>(n_items, next_item, finish, hook, slow_code, s_tbl,
+    stream_aligned<1, 7, 7, false, true, false, kLookahead>(n_items, next_item, finish1, hook, slow_code, s_tbl,
                                              lane_const, row_blocks, s_aslot[wave], nullptr);
   else if (!slow && bc && nsq == 8)
-    stream_aligned<1, 8, false, true, false>(n_items, next_item, finish, hook, slow_code, s_tbl,
+    stream_aligned<1, 8, 8, false, true, false, kLookahead>(n_items, next_item, finish1, hook, slow_code, s_tbl,
                                              lane_const, row_blocks, s_aslot[wave], nullptr);
   else if (!slow && bc)
     stream_items<1, 8, false, true>(n_items, nsq, next_item, finish, hook, slow_code, s_tbl, lane_const);
@@ -884,6 +973,29 @@ bool decode_layer_supported(int64_t T, int32_t k, int32_t E, int32_t H, int32_t 
 
 int64_t decode_route_bytes() { return (int64_t)sizeof(DecodeRoute); }
 
+// Workgroups of the gate/up kernel.  Its waves split the (routed expert, 4-row tile) items
+// evenly, in order; the item count is u * F/4 for the u routed experts, known only inside
+// the kernel.  With more items than wave slots (two workgroups per CU), the wave count is
+// the largest divisor of F/4 (a multiple of the workgroup's wave count) that fills at least
+// 3/4 of the slots: every wave then gets exactly u * (F/4) / waves items whatever u is,
+// instead of some waves one item more than others.
+int64_t decode_gateup_groups(int64_t T, int32_t k, int32_t E, int32_t F) {
+  const int64_t slots = 2 * (int64_t)device_cu_count() * kFfnWaves;
+  const int64_t u_max = T * k < E ? T * k : E;
+  const int64_t te = F / 4;
+  int64_t waves = u_max * te;
+  if (waves > slots) {
+    waves = slots;
+    for (int64_t d = 1; d <= te; ++d) {
+      const int64_t w = te / d;
+      if (te % d != 0 || w % kFfnWaves != 0 || w > slots) continue;
+      if (4 * w >= 3 * slots) waves = w;
+      break;
+    }
+  }
+  return (waves + kFfnWaves - 1) / kFfnWaves;
+}
+
 // Gate/up (with routing) then down (with combine).  `ev`, when given, receives marks
 // before the first kernel (twice: the routing has no launch of its own), between the two
 // kernels and after the second.
@@ -904,10 +1016,7 @@ int launch_decode_layer(const moe_nf4_expert_t *experts, int32_t E, const void *
                 "expert %d is not resident (null pointer in its table entry)", e);
     tab.e[e] = ex;
   }
-  const int cap = 2 * device_cu_count();
-  const int64_t u_max = T * k < E ? T * k : E;
-  int64_t g1 = (u_max * (F / 4) + kFfnWaves - 1) / kFfnWaves;
-  if (g1 > cap) g1 = cap;
+  const int64_t g1 = decode_gateup_groups(T, k, E, F);
   const int tpw = decode_tiles_per_wg(H);
   const int64_t g2 = (H / 4 + tpw - 1) / tpw;
 
