@@ -31,7 +31,13 @@ namespace moe {
 constexpr int kDecMaxTokens = 4;
 constexpr int kDecMaxSlots = 8;
 constexpr int kDecMaxExperts = 16;
-constexpr int kDecMaxTilesPerWg = 4;
+constexpr int kDecMaxTilesPerWg = 8;
+// Both decode kernels run one 8-wave workgroup per CU: one copy of the 64 KB lookup table
+// per CU, and the CU's waves share their items through an LDS counter.
+constexpr int kDecWaves = 8;
+constexpr int kDecThreads = kDecWaves * kWave;
+// The down kernel splits K (= F) of every (tile, expert) into at most this many parts.
+constexpr int kDecMaxKParts = 8;
 
 // Routing of one decode step, written by workgroup 0 of the gate/up kernel and read by
 // the down kernel.  "Active" experts are those with at least one routed slot, in
@@ -62,7 +68,7 @@ struct RouteHead {
 static_assert(offsetof(DecodeRoute, code2) == sizeof(RouteHead), "DecodeRoute starts with RouteHead");
 constexpr int kRouteHeadWords = (int)(sizeof(RouteHead) / 4);
 constexpr int kRouteWords = (int)(sizeof(DecodeRoute) / 4);
-static_assert(kRouteWords <= kFfnThreads, "one descriptor word per thread");
+static_assert(kRouteWords <= kDecThreads, "one descriptor word per thread");
 
 namespace {
 
@@ -202,16 +208,24 @@ __device__ __forceinline__ void stream_items(int n_items, int nsq, ItemFn &&next
 //    the item boundary, instead of one 4-byte load per lane and stage;
 //  * with XREG (one token for the whole stream, single-token broadcast form), the
 //    activation chunks of all NSQ stages to stay in registers, loaded once.
-// Step d of item it issues the load of stage d + DEPTH - 1 of the stage sequence: stage
-// d + DEPTH - 1 of item it, or stage d + DEPTH - 1 - NSQ of item it+1 (past the last item
-// the last item's stages are re-read, unused).  At most DEPTH stages per projection are in
-// flight per wave: the depth sets the bytes a wave keeps outstanding.
-// next_item / finish / hook / slow_code as for stream_items; `arow` is the absmax row
+// Items come from grab() (wave-uniform item index, negative when none is left), taken one
+// item ahead, so the waves of a workgroup can share a work counter; set_ptrs(P, item) sets
+// the pointers of an item and finish(acc, item) receives its per-lane partial sums (before
+// the cross-lane reduction).  Step d of an item issues the load of stage d + DEPTH - 1 of
+// the stage sequence: stage d + DEPTH - 1 of this item, or stage d + DEPTH - 1 - NSQ of the
+// next one (after the last item, a re-read of this item's stages, unused).  At most DEPTH
+// stages per projection are in flight per wave: the depth sets the bytes a wave keeps
+// outstanding.  With LA the table lookups of a stage are issued one step ahead of its
+// products, so that their LDS latency overlaps the MFMAs.  hook() runs once after the
+// prologue (every wave calls it exactly once, also without work).  `arow` is the absmax row
 // stride (floats), `aslot` the wave's LDS slot (NP x kASlotFloats), `xbase` the lane's
 // activation chunk of stage 0 (XREG only).  With BC the four MFMA result rows are the same
 // token, and only row 0 of `acc` is accumulated (finish must read row 0 only).
 // Per-wave absmax slot of one item: 4 rows of up to 64 floats, rows padded to 72 floats so
 // that the four rows read in one instruction fall into different LDS banks.
+constexpr int kASlotRow = 72;
+constexpr int kASlotFloats = 4 * kASlotRow;
+
 // The 16-level NF4 codebook (QLoRA; bitsandbytes' NF4 table, the `code` tensor of the quant
 // state, transfer/nf4_reconstruct.py:48) as fp32: the decode kernels build their lookup
 // table from these values and route experts whose codebooks differ to the per-nibble path.
@@ -221,7 +235,6 @@ constexpr float kNf4Code[16] = {
     0.07958029955625534f, 0.16093020141124725f, 0.24611230194568634f, 0.33791524242401123f,
     0.44070982933044434f, 0.5626170039176941f, 0.7229568362236023f, 1.0f};
 
-constexpr int kASlotRow = 72;
 #ifndef MOE_GATEUP_DEPTH
 #define MOE_GATEUP_DEPTH 4
 #endif
@@ -232,11 +245,6 @@ constexpr int kGateUpDepth = MOE_GATEUP_DEPTH;
 #endif
 // Table lookups one stage ahead of the products in the aligned stream.
 constexpr bool kLookahead = MOE_LOOKAHEAD != 0;
-#ifndef MOE_SPLIT_CHAINS
-#define MOE_SPLIT_CHAINS 1
-#endif
-constexpr bool kSplitChains = MOE_SPLIT_CHAINS != 0;
-constexpr int kASlotFloats = 4 * kASlotRow;
 
 template <int NP, int NX>
 struct StageQ {
@@ -244,23 +252,24 @@ struct StageQ {
   uint4 xa[NX];
 };
 
-template <int NP, int NSQ, int DEPTH, bool SLOW, bool BC, bool XREG, bool LA, typename ItemFn,
-          typename FinishFn, typename Hook, typename SlowFn>
-__device__ __forceinline__ void stream_aligned(int n_items, ItemFn &&next_item, FinishFn &&finish,
-                                               Hook &&hook, SlowFn &&slow_code,
+template <int NP, int NSQ, int DEPTH, bool BC, bool XREG, bool LA, typename GrabFn,
+          typename PtrFn, typename FinishFn, typename Hook>
+__device__ __forceinline__ void stream_aligned(GrabFn &&grab, PtrFn &&set_ptrs,
+                                               FinishFn &&finish, Hook &&hook,
                                                const uint32_t *tbl,
                                                const uint32_t (&lane_const)[NP], size_t arow,
                                                float *aslot, gx_t xbase) {
   static_assert(NSQ >= 2 && NSQ <= 8, "an item's absmax block must fit one load per lane");
   static_assert(DEPTH >= 2 && DEPTH <= NSQ && NSQ % DEPTH == 0, "depth must divide NSQ");
-  static_assert(!LA || (!SLOW && DEPTH >= 3), "lookahead needs the table path and depth >= 3");
+  static_assert(!LA || DEPTH >= 3, "lookahead needs depth >= 3");
   constexpr int NX = XREG ? 1 : (BC ? 1 : 4);
   // First step that loads a stage of the next item.
   constexpr int kNext = NSQ - DEPTH + 1;
   const int lane = threadIdx.x & (kWave - 1);
   const int blk = lane >> 2;
   const int j = lane & 3;
-  if (n_items <= 0) {
+  int cur = grab();
+  if (cur < 0) {
     hook();
     return;
   }
@@ -270,7 +279,7 @@ __device__ __forceinline__ void stream_aligned(int n_items, ItemFn &&next_item, 
   const int a_col = a_act ? 4 * (lane % (2 * NSQ)) : 0;
 
   ItemPtr<NP> P;
-  next_item(P);
+  set_ptrs(P, cur);
   uint4 abuf[NP];
   auto load_abs = [&]() {
 #pragma unroll
@@ -307,13 +316,11 @@ __device__ __forceinline__ void stream_aligned(int n_items, ItemFn &&next_item, 
   }
   store_abs();
   hook();
+  int nxt = grab();
 
   f32x4 acc[NP];
 #pragma unroll
   for (int p = 0; p < NP; ++p) acc[p] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  const float *sc = SLOW ? slow_code() : nullptr;
-  // LA: the table lookups of a stage are issued one step ahead, interleaved with the
-  // products of the stage before, so that their LDS latency overlaps the MFMAs.
   s16x4 bq[LA ? NP : 1][8];
   if (LA) {
 #pragma unroll
@@ -321,18 +328,18 @@ __device__ __forceinline__ void stream_aligned(int n_items, ItemFn &&next_item, 
 #pragma unroll
       for (int p = 0; p < NP; ++p) bq[p][i] = b_operand<false>(st[0].q[p], i, tbl, lane_const[p], nullptr);
   }
-  for (int it = 0; it < n_items; ++it) {
+  for (;;) {
 #pragma unroll
     for (int d = 0; d < NSQ; ++d) {
-      if (d == kNext && it + 1 < n_items) {
-        next_item(P);
+      if (d == kNext && nxt >= 0) {
+        set_ptrs(P, nxt);
         load_abs();
       }
       const int g = d + DEPTH - 1;  // stage sequence index of this step's load
       load(st[g % DEPTH], g < NSQ ? g : g - NSQ);
       __builtin_amdgcn_sched_barrier(0);  // this step's loads before its products
-      const StageQ<NP, NX> &cur = st[d % DEPTH];
-      const uint4 *xa = XREG ? &xr[d] : cur.xa;
+      const StageQ<NP, NX> &cs = st[d % DEPTH];
+      const uint4 *xa = XREG ? &xr[d] : cs.xa;
       float scl[NP];
 #pragma unroll
       for (int p = 0; p < NP; ++p) scl[p] = aslot[p * kASlotFloats + j * kASlotRow + 8 * d + (blk >> 1)];
@@ -342,33 +349,16 @@ __device__ __forceinline__ void stream_aligned(int n_items, ItemFn &&next_item, 
       if (LA) {
         // Stage d+1 is in buffer (d+1) % DEPTH (for d = NSQ-1: the next item's stage 0, or
         // a re-read of this item's when it is the last one).
-        const StageQ<NP, NX> &nxt = st[(d + 1) % DEPTH];
+        const StageQ<NP, NX> &ns = st[(d + 1) % DEPTH];
         s16x4 bn[LA ? NP : 1][8];
-        f32x4 t2[NP];
-#pragma unroll
-        for (int p = 0; p < NP; ++p) t2[p] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
 #pragma unroll
-          for (int p = 0; p < NP; ++p) bn[p][i] = b_operand<false>(nxt.q[p], i, tbl, lane_const[p], nullptr);
+          for (int p = 0; p < NP; ++p) bn[p][i] = b_operand<false>(ns.q[p], i, tbl, lane_const[p], nullptr);
           const s16x4 a = a_operand<BC>(xa, i);
 #pragma unroll
-          for (int p = 0; p < NP; ++p) {
-            // Two accumulators per projection (even / odd i) halve the dependent chain.
-            if (kSplitChains && (i & 1))
-              t2[p] = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(a, bq[p][i], t2[p], 0, 0, 0);
-            else
-              t[p] = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(a, bq[p][i], t[p], 0, 0, 0);
-          }
-        }
-        if (kSplitChains) {
-#pragma unroll
-          for (int p = 0; p < NP; ++p) {
-            if (BC)
-              t[p][0] += t2[p][0];
-            else
-              t[p] += t2[p];
-          }
+          for (int p = 0; p < NP; ++p)
+            t[p] = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(a, bq[p][i], t[p], 0, 0, 0);
         }
 #pragma unroll
         for (int i = 0; i < 8; ++i)
@@ -381,7 +371,7 @@ __device__ __forceinline__ void stream_aligned(int n_items, ItemFn &&next_item, 
 #pragma unroll
           for (int p = 0; p < NP; ++p)
             t[p] = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(
-                a, b_operand<SLOW>(cur.q[p], i, tbl, lane_const[p], sc + 16 * p), t[p], 0, 0, 0);
+                a, b_operand<false>(cs.q[p], i, tbl, lane_const[p], nullptr), t[p], 0, 0, 0);
         }
       }
 #pragma unroll
@@ -392,32 +382,44 @@ __device__ __forceinline__ void stream_aligned(int n_items, ItemFn &&next_item, 
           scale_acc(acc[p], t[p], scl[p]);
       }
     }
-    finish(acc);
+    finish(acc, cur);
 #pragma unroll
     for (int p = 0; p < NP; ++p) acc[p] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    if (SLOW && it + 1 < n_items) sc = slow_code();
+    if (nxt < 0) break;
     store_abs();
+    cur = nxt;
+    nxt = grab();
   }
 }
 
-// 64 KB lookup table (see nf4_tile.h) from codebooks held in registers.  Word
-// 64*v + r holds the bf16 pair of packed byte v for replica r; replicas 0-31 use c_a,
-// 32-63 use c_b, so four consecutive replicas hold the same word.  Thread tid writes
-// words 4*tid + 1024*q .. +3 (q = 0..15) with one 16-byte store each: byte
-// v = tid/16 + 16q, i.e. high nibble q and low nibble tid/16, replicas 4*(tid%16) .. +3.
+// 64 KB lookup table (see nf4_tile.h) from codebooks held in registers, by NT threads.
+// Word 64*v + r holds the bf16 pair of packed byte v for replica r; replicas 0-31 use c_a,
+// 32-63 use c_b, so four consecutive replicas hold the same word.  Store s (words 4s ..
+// 4s+3, one 16-byte store) covers byte v = s/16 (high nibble v >> 4, low nibble v & 15)
+// and replicas 4*(s%16) .. +3; thread tid makes stores s = tid + NT*r, r < 4096/NT, so its
+// low nibble and replica half are fixed and its high nibble is tid/256 + (NT/256)*r.
+template <int NT>
 __device__ __forceinline__ void build_table_regs(uint32_t *tbl, const float (&c_a)[16],
                                                  const float (&c_b)[16]) {
+  static_assert(NT % 256 == 0 && 4096 % NT == 0, "NT must be 256, 512, 1024, ...");
+  constexpr int R = 4096 / NT;
+  constexpr int HS = NT / 256;
   const int tid = threadIdx.x;
   const bool second = (tid & 8) != 0;  // replica 4*(tid%16) >= 32
-  const int lo_nib = tid >> 4;
+  const int lo_nib = (tid >> 4) & 15;
+  const int hi0 = tid >> 8;  // < HS
   float lo = c_a[0];
 #pragma unroll
   for (int i = 0; i < 16; ++i)
     if (i == lo_nib) lo = second ? c_b[i] : c_a[i];
 #pragma unroll
-  for (int q = 0; q < 16; ++q) {
-    const uint32_t w = pack_bf16x2(second ? c_b[q] : c_a[q], lo);
-    *reinterpret_cast<uint4 *>(tbl + 4 * tid + 1024 * q) = make_uint4(w, w, w, w);
+  for (int r = 0; r < R; ++r) {
+    float hi = second ? c_b[HS * r] : c_a[HS * r];
+#pragma unroll
+    for (int h = 1; h < HS; ++h)
+      if (hi0 == h) hi = second ? c_b[HS * r + h] : c_a[HS * r + h];
+    const uint32_t w = pack_bf16x2(hi, lo);
+    *reinterpret_cast<uint4 *>(tbl + 4 * (tid + NT * r)) = make_uint4(w, w, w, w);
   }
 }
 
@@ -456,7 +458,7 @@ __device__ __forceinline__ float row_sum16(float v) {
 }
 
 // Routing of the T <= 4 tokens by one wave, lane (t = lane/16, e = lane%16) holding
-// expert e of token t: fp32 sum of the four waves' gate partials in fixed order -> bf16
+// expert e of token t: fp32 sum of the NW waves' gate partials in wave order -> bf16
 // logit (+ bias) -> fp32 softmax over the row -> top-k by k rounds of row arg-max (ties:
 // the lowest expert index) -> weights renormalised by their sum in rank order.  Then the
 // grouping of the T*k slots (s = t*k + j) by expert, ascending expert and ascending slot,
@@ -466,7 +468,7 @@ struct RouteSummary {
   bool bc;
 };
 
-template <int EMAX>
+template <int EMAX, int NW>
 __device__ __forceinline__ RouteSummary route_wave(RouteHead &rh, int32_t (&sl_e)[kDecMaxSlots],
                                            float (&sl_w)[kDecMaxSlots],
                                            const float (*s_part)[kDecMaxTokens][EMAX],
@@ -478,7 +480,9 @@ __device__ __forceinline__ RouteSummary route_wave(RouteHead &rh, int32_t (&sl_e
   const bool valid = t < T && e < E;
   float l = -INFINITY;
   if (valid) {
-    const float v = s_part[0][t][e] + s_part[1][t][e] + s_part[2][t][e] + s_part[3][t][e];
+    float v = s_part[0][t][e];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) v += s_part[w][t][e];
     const uint16_t lb = f32_to_bf16(v);
     if (logits_out != nullptr) logits_out[t * E + e] = lb;
     l = bf16_to_f32(lb);
@@ -550,26 +554,28 @@ __device__ __forceinline__ RouteSummary route_wave(RouteHead &rh, int32_t (&sl_e
 }
 
 template <int EMAX>
-__global__ void __launch_bounds__(kFfnThreads, 2)
+__global__ void __launch_bounds__(kDecThreads, 1)
 decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
                      const uint16_t *__restrict__ gate, const float *__restrict__ bias, int T,
                      int H, int F, int E, int k, uint16_t *__restrict__ logits_out,
                      float *__restrict__ w_out, int64_t *__restrict__ idx_out,
                      DecodeRoute *__restrict__ route_out, uint16_t *__restrict__ h_out) {
   __shared__ __attribute__((aligned(16))) uint32_t s_tbl[kTableWords];
-  __shared__ float s_part[kFfnWaves][kDecMaxTokens][EMAX];
+  __shared__ float s_part[kDecWaves][kDecMaxTokens][EMAX];
   // Codebooks of every expert: [0,16) w1, [16,32) w3, [32,48) w2 ([48,64) repeats w2).
   __shared__ float s_code[EMAX][kWave];
   __shared__ const void *s_eptr[EMAX][4];  // w1_packed, w1_absmax, w3_packed, w3_absmax
-  __shared__ __attribute__((aligned(16))) RouteHead s_rtw[kFfnWaves];  // one copy per wave
-  __shared__ int32_t s_sle[kFfnWaves][kDecMaxSlots];                       // per wave: slot experts
-  __shared__ float s_slw[kFfnWaves][kDecMaxSlots];                         // per wave: slot weights
-  __shared__ __attribute__((aligned(16))) float s_aslot[kFfnWaves][2 * kASlotFloats];
+  __shared__ __attribute__((aligned(16))) RouteHead s_rtw[kDecWaves];  // one copy per wave
+  __shared__ int32_t s_sle[kDecWaves][kDecMaxSlots];                       // per wave: slot experts
+  __shared__ float s_slw[kDecWaves][kDecMaxSlots];                         // per wave: slot weights
+  __shared__ __attribute__((aligned(16))) float s_aslot[kDecWaves][2 * kASlotFloats];
+  __shared__ int32_t s_ticket;  // next item of the workgroup's range (single-token path)
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const bool wg0 = blockIdx.x == 0;
+  if (tid == 0) s_ticket = 0;
 
   // ---- lookup table from the NF4 codebook constants: no load in front of it, so it is
   // written while the gate loads below are in flight.  Experts whose codebooks differ from
@@ -578,26 +584,25 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
     float cst[16];
 #pragma unroll
     for (int q = 0; q < 16; ++q) cst[q] = kNf4Code[q];
-    build_table_regs(s_tbl, cst, cst);
+    build_table_regs<kDecThreads>(s_tbl, cst, cst);
   }
 
-  // ---- gate products on the 4x4x4 MFMA: wave w takes H range [w*H/4, (w+1)*H/4) in
-  // chunks of 128 values; lane (b = lane/4, j = lane%4) holds values 8b .. 8b+7 of the
-  // chunk of token j (A rows, tokens >= T repeat a valid row and are ignored) and of
-  // expert 4g + j (B columns).  D[b][m][n] sums block b's slice for token m and expert
-  // 4g + n; a butterfly over the 16 blocks completes the wave's partial sums.
+  // ---- gate products on the 4x4x4 MFMA: wave w takes the 128-value chunks c = w, w + 8,
+  // ... of H; lane (b = lane/4, j = lane%4) holds values 8b .. 8b+7 of a chunk of token j
+  // (A rows; tokens >= T repeat a valid row and are ignored) and of expert 4g + j (B
+  // columns).  D[b][m][n] sums block b's slice for token m and expert 4g + n; a butterfly
+  // over the 16 blocks completes the wave's partial sums.
   constexpr int G = EMAX / 4;                 // expert groups of four
-  constexpr int CPR = EMAX <= 8 ? 8 : 4;      // chunks per load round
+  constexpr int CPR = EMAX <= 8 ? 4 : 2;      // chunks per load round
   const int lj = lane & 3;
   const int lb = lane >> 2;
-  const int hq = H / kFfnWaves;               // multiple of 128
-  const int n_chunks = hq / 128;
-  const gx_t xrow = (gx_t)x + (size_t)(lj < T ? lj : T - 1) * H + (size_t)wave * hq + 8 * lb;
+  const int n_chunks = (H / 128 - wave + kDecWaves - 1) / kDecWaves;  // this wave's chunks
+  const gx_t xrow = (gx_t)x + (size_t)(lj < T ? lj : T - 1) * H + (size_t)wave * 128 + 8 * lb;
   gx_t grow[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     const int e = 4 * g + lj;
-    grow[g] = (gx_t)gate + (size_t)(e < E ? e : E - 1) * H + (size_t)wave * hq + 8 * lb;
+    grow[g] = (gx_t)gate + (size_t)(e < E ? e : E - 1) * H + (size_t)wave * 128 + 8 * lb;
   }
   f32x4 gacc[G];
 #pragma unroll
@@ -606,22 +611,22 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
   auto load_round = [&](int c0) {
 #pragma unroll
     for (int c = 0; c < CPR; ++c) {
-      const int cc = c0 + c < n_chunks ? c0 + c : n_chunks - 1;  // clamped re-read, unused
-      xv[c] = ld_u4(xrow + cc * 128);
+      const int cc = c0 + c < n_chunks ? c0 + c : 0;  // past the end: chunk 0 again, unused
+      xv[c] = ld_u4(xrow + (size_t)cc * (128 * kDecWaves));
 #pragma unroll
-      for (int g = 0; g < G; ++g) gv[c][g] = ld_u4(grow[g] + cc * 128);
+      for (int g = 0; g < G; ++g) gv[c][g] = ld_u4(grow[g] + (size_t)cc * (128 * kDecWaves));
     }
   };
-  load_round(0);
-  // Metadata of experts wave + 4q (wave-uniform, so the table entries are scalar loads):
+  if (n_chunks > 0) load_round(0);
+  // Metadata of experts wave + 8q (wave-uniform, so the table entries are scalar loads):
   // lane l < 16 reads w1 code[l], 16..31 w3 code[l-16], 32..63 w2 code[l & 15]; lane f < 4
   // keeps stream pointer f (w1_packed, w1_absmax, w3_packed, w3_absmax).
-  constexpr int EPW = EMAX / kFfnWaves;
+  constexpr int EPW = (EMAX + kDecWaves - 1) / kDecWaves;
   float cvw[EPW];
   const void *pvw[EPW];
 #pragma unroll
   for (int q = 0; q < EPW; ++q) {
-    const int e = wave + kFfnWaves * q;
+    const int e = wave + kDecWaves * q;
     const moe_nf4_expert_t &ex = tab.e[e < E ? e : E - 1];
     const void *c1 = uniform_ptr(ex.w1_code), *c3 = uniform_ptr(ex.w3_code);
     const void *c2 = uniform_ptr(ex.w2_code);
@@ -667,19 +672,19 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
   // Unconditional stores (clamped experts rewrite identical values).
 #pragma unroll
   for (int q = 0; q < EPW; ++q) {
-    const int e = wave + kFfnWaves * q;
+    const int e = wave + kDecWaves * q;
     const int ee = e < E ? e : E - 1;
     s_code[ee][lane] = cvw[q];
     s_eptr[ee][lane & 3] = pvw[q];
   }
-  // The only barrier of the routing phase: gate sums, codebooks, stream pointers and the
-  // lookup table are visible to every wave after it.
+  // The only barrier of the routing phase: gate sums, codebooks, stream pointers, the
+  // lookup table and the work counter are visible to every wave after it.
   __syncthreads();
 
   // ---- routing and grouping, by every wave on its own copy
   RouteHead &rt = s_rtw[wave];
-  const RouteSummary rs = route_wave<EMAX>(rt, s_sle[wave], s_slw[wave], s_part, bias, T, E, k,
-                                           (wg0 && wave == 0) ? logits_out : nullptr);
+  const RouteSummary rs = route_wave<EMAX, kDecWaves>(rt, s_sle[wave], s_slw[wave], s_part, bias,
+                                                      T, E, k, (wg0 && wave == 0) ? logits_out : nullptr);
   const int u = rs.n_active;
   const int ns = T * k;
   // Codebook checks against the table's NF4 values: lane c < 32 checks w1|w3 word c,
@@ -717,85 +722,92 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
   }
   const RouteHead &s_rt = rt;
 
-  // ---- w1/w3 stream over this wave's range of the (active expert, tile) list
+  // ---- w1/w3 stream over the workgroup's range of the (active expert, 4-row tile) items
   const int lanej = lane & 3;
   const int blk = lane >> 2;
   const int tiles_e = F >> 2;
   const int N = u * tiles_e;
-  const int W = (int)gridDim.x * kFfnWaves;
-  const int wid = (int)blockIdx.x * kFfnWaves + wave;
-  const int i0 = (int)((int64_t)wid * N / W);
-  const int n_items = (int)((int64_t)(wid + 1) * N / W) - i0;
+  const int wlo = (int)((int64_t)blockIdx.x * N / gridDim.x);
+  const int whi = (int)((int64_t)(blockIdx.x + 1) * N / gridDim.x);
   const int nsq = H / kStageVals;
   const size_t row_bytes = (size_t)(H >> 1);
   const size_t row_blocks = (size_t)(H >> 6);
   const uint32_t lane_const[2] = {(uint32_t)(lane & 31) << 2, ((uint32_t)(lane & 31) << 2) | 128u};
   const bool bc = rs.bc;
-  const int a_start = i0 / tiles_e;
-  const int tile_start = i0 - a_start * tiles_e;
 
-  // Load side: (la, ltile) walks the items in order; within an expert the pointers step
-  // by one 4-row tile, at an expert change they are rebuilt from the LDS tables.
-  int la = a_start, ltile = tile_start - 1;
-  auto next_item = [&](ItemPtr<2> &P) {
-    if (++ltile < tiles_e && ltile != tile_start) {
-#pragma unroll
-      for (int p = 0; p < 2; ++p) {
-        P.wq[p] += 4 * row_bytes;
-        P.wa[p] += 4 * row_blocks;
-        P.ab[p] += 4 * row_blocks;
-      }
-      return;
+  // Pointers of item i = (active expert a, tile): rebuilt from the LDS tables.
+  auto item_expert = [&](int i, int &tile) {
+    int a = 0;
+    while (i >= tiles_e) {  // at most u - 1 steps
+      i -= tiles_e;
+      ++a;
     }
-    if (ltile == tiles_e) {
-      ltile = 0;
-      ++la;
-    }
-    const size_t row = (size_t)ltile * 4 + lanej;
-    const int e = s_rt.active[la];
+    tile = i;
+    return a;
+  };
+  auto set_ptrs = [&](ItemPtr<2> &P, int i) {
+    int tile;
+    const int a = item_expert(i, tile);
+    const size_t row = (size_t)tile * 4 + lanej;
+    const int e = s_rt.active[a];
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
       P.wq[p] = (gq_t)s_eptr[e][2 * p] + row * row_bytes + blk * 16;
       P.wa[p] = (ga_t)s_eptr[e][2 * p + 1] + row * row_blocks + (blk >> 1);
-      P.ab[p] = (ga_t)s_eptr[e][2 * p + 1] + (size_t)ltile * 4 * row_blocks;
+      P.ab[p] = (ga_t)s_eptr[e][2 * p + 1] + (size_t)tile * 4 * row_blocks;
     }
-    const int jj = (!bc && lanej < s_rt.counts[la]) ? lanej : 0;
-    const int tok = s_rt.perm_tok[s_rt.offsets[la] + jj];
+    const int jj = (!bc && lanej < s_rt.counts[a]) ? lanej : 0;
+    const int tok = s_rt.perm_tok[s_rt.offsets[a] + jj];
     P.ap = (gx_t)x + (size_t)tok * H + blk * 32 + (bc ? lanej * 8 : 0);
   };
-  // Consume side: (ca, ctile) walks the same items for the h stores.
-  int ca = a_start, ctile = tile_start;
   // nrows: MFMA result rows that hold tokens (1 on the single-token path, whose other rows
   // are never accumulated).
-  auto finish_rows = [&](f32x4 (&ac)[2], int nrows) {
+  auto finish_item = [&](f32x4 (&ac)[2], int i, int nrows) {
 #pragma unroll
     for (int p = 0; p < 2; ++p)
 #pragma unroll
       for (int q = 0; q < 4; ++q)
         if (q < nrows) ac[p][q] = lanes_sum16(ac[p][q]);
     if (blk == 0) {
-      const int row = ctile * 4 + lanej;
-      const int cnt = s_rt.counts[ca];
-      const int off = s_rt.offsets[ca];
+      int tile;
+      const int a = item_expert(i, tile);
+      const int row = tile * 4 + lanej;
+      const int cnt = s_rt.counts[a];
+      const int off = s_rt.offsets[a];
 #pragma unroll
       for (int m = 0; m < 4; ++m)
-        if (m < cnt) h_out[(size_t)(off + m) * F + row] = swiglu_bf16(ac[0][m], ac[1][m]);
-    }
-    if (++ctile == tiles_e) {
-      ctile = 0;
-      ++ca;
+        if (m < cnt && m < nrows) h_out[(size_t)(off + m) * F + row] = swiglu_bf16(ac[0][m], ac[1][m]);
     }
   };
-  auto finish = [&](f32x4 (&ac)[2]) { finish_rows(ac, 4); };
-  auto finish1 = [&](f32x4 (&ac)[2]) { finish_rows(ac, 1); };
   auto hook = [&]() {};
-  auto slow_code = [&]() -> const float * { return s_code[s_rt.active[ca]]; };
   const bool slow = slow1;
-  if (!slow && bc && nsq == 8 && T == 1)
-    stream_aligned<2, 8, kGateUpDepth, false, true, true, kLookahead>(n_items, next_item, finish1, hook, slow_code, s_tbl,
-                                            lane_const, row_blocks, s_aslot[wave],
-                                            (gx_t)x + blk * 32 + lanej * 8);
-  else if (!slow && bc)
+  if (!slow && bc && nsq == 8 && T == 1) {
+    // Single token: the workgroup's items are shared through the work counter.
+    auto grab = [&]() -> int {
+      int t = 0;
+      if (lane == 0) t = __hip_atomic_fetch_add(&s_ticket, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      t = __builtin_amdgcn_readfirstlane(t) + wlo;
+      return t < whi ? t : -1;
+    };
+    auto finish1 = [&](f32x4 (&ac)[2], int i) { finish_item(ac, i, 1); };
+    stream_aligned<2, 8, kGateUpDepth, true, true, kLookahead>(
+        grab, set_ptrs, finish1, hook, s_tbl, lane_const, row_blocks, s_aslot[wave],
+        (gx_t)x + blk * 32 + lanej * 8);
+    return;
+  }
+  // Other shapes: each wave takes a contiguous part of the workgroup's range.
+  const int nw = whi - wlo;
+  const int i0 = wlo + wave * nw / kDecWaves;
+  const int n_items = wlo + (wave + 1) * nw / kDecWaves - i0;
+  int li = i0 - 1;
+  auto next_item = [&](ItemPtr<2> &P) { set_ptrs(P, ++li); };
+  int ci = i0;
+  auto finish = [&](f32x4 (&ac)[2]) { finish_item(ac, ci++, 4); };
+  auto slow_code = [&]() -> const float * {
+    int tile;
+    return s_code[s_rt.active[item_expert(ci, tile)]];
+  };
+  if (!slow && bc)
     stream_items<2, 6, false, true>(n_items, nsq, next_item, finish, hook, slow_code, s_tbl, lane_const);
   else if (!slow)
     stream_items<2, 4, false, false>(n_items, nsq, next_item, finish, hook, slow_code, s_tbl, lane_const);
@@ -805,15 +817,17 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
     stream_items<2, 4, true, false>(n_items, nsq, next_item, finish, hook, slow_code, s_tbl, lane_const);
 }
 
-__global__ void __launch_bounds__(kFfnThreads, 2)
+__global__ void __launch_bounds__(kDecThreads, 1)
 decode_down_kernel(const ExpertTable tab, const DecodeRoute *__restrict__ route,
                    const uint16_t *__restrict__ h, int T, int H, int F, int E, int k,
-                   int tiles_per_wg, uint16_t *__restrict__ out) {
+                   int tiles_per_wg, int kparts, uint16_t *__restrict__ out) {
   __shared__ __attribute__((aligned(16))) uint32_t s_tbl[kTableWords];
   __shared__ __attribute__((aligned(16))) DecodeRoute s_rt;
-  __shared__ float s_part[kDecMaxTilesPerWg][kDecMaxSlots][kFfnWaves][16];
+  // Partial sums of (tile, active expert, K part): 4 rows x 4 token rows.
+  __shared__ float s_part[kDecMaxTilesPerWg][kDecMaxSlots][kDecMaxKParts][16];
   __shared__ const void *s_eptr[kDecMaxExperts][2];  // w2_packed, w2_absmax of every expert
-  __shared__ __attribute__((aligned(16))) float s_aslot[kFfnWaves][kASlotFloats];
+  __shared__ __attribute__((aligned(16))) float s_aslot[kDecWaves][2 * kASlotFloats];
+  __shared__ int32_t s_ticket;  // next unit of the workgroup (single-token path)
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
@@ -821,33 +835,32 @@ decode_down_kernel(const ExpertTable tab, const DecodeRoute *__restrict__ route,
   // The descriptor and every expert's w2 pointers in one round trip.
   uint32_t rw = 0;
   if (tid < kRouteWords) rw = reinterpret_cast<const uint32_t *>(route)[tid];
-  for (int i = tid; i < (int)(sizeof(s_part) / 4); i += kFfnThreads)
-    reinterpret_cast<float *>(s_part)[i] = 0.0f;
-  // Experts wave + 4q: wave-uniform table entries (scalar loads), lanes 0/1 keep
+  // Experts wave + 8q: wave-uniform table entries (scalar loads), lanes 0/1 keep
   // w2_packed / w2_absmax.
-  constexpr int EPW = kDecMaxExperts / kFfnWaves;
+  constexpr int EPW = kDecMaxExperts / kDecWaves;
   const void *pk[EPW], *pa[EPW];
 #pragma unroll
   for (int q = 0; q < EPW; ++q) {
-    const int e = wave + kFfnWaves * q;
+    const int e = wave + kDecWaves * q;
     const moe_nf4_expert_t &ex = tab.e[e < E ? e : E - 1];
     pk[q] = uniform_ptr(ex.w2_packed);
     pa[q] = uniform_ptr(ex.w2_absmax);
   }
-#pragma unroll
-  for (int q = 0; q < EPW; ++q) {
-    const int e = wave + kFfnWaves * q;
-    if (e < E && lane < 2) s_eptr[e][lane] = lane ? pa[q] : pk[q];
-  }
-  if (tid < kRouteWords) reinterpret_cast<uint32_t *>(&s_rt)[tid] = rw;
-  // Lookup table from the NF4 codebook constants, built before the barrier; the gate/up
-  // kernel flagged (slow2) active experts whose w2 codebook differs from them.
+  if (tid == 0) s_ticket = 0;
+  // Lookup table from the NF4 codebook constants, built while the loads are in flight; the
+  // gate/up kernel flagged (slow2) active experts whose w2 codebook differs from them.
   {
     float cst[16];
 #pragma unroll
     for (int q = 0; q < 16; ++q) cst[q] = kNf4Code[q];
-    build_table_regs(s_tbl, cst, cst);
+    build_table_regs<kDecThreads>(s_tbl, cst, cst);
   }
+#pragma unroll
+  for (int q = 0; q < EPW; ++q) {
+    const int e = wave + kDecWaves * q;
+    if (e < E && lane < 2) s_eptr[e][lane] = lane ? pa[q] : pk[q];
+  }
+  if (tid < kRouteWords) reinterpret_cast<uint32_t *>(&s_rt)[tid] = rw;
   __syncthreads();
   const int u = s_rt.n_active;
 
@@ -857,76 +870,120 @@ decode_down_kernel(const ExpertTable tab, const DecodeRoute *__restrict__ route,
   const int r_end = min(r0 + tiles_per_wg, H >> 2);
   const int ntl = r_end > r0 ? r_end - r0 : 0;
   const int NS = F / kStageVals;
-  const int s_lo = wave * NS / kFfnWaves;
-  const int nsq = (wave + 1) * NS / kFfnWaves - s_lo;
-  const int n_items = ntl * u;
+  const int nsq = NS / kparts;  // stages per unit
+  // Units: (active expert a, tile tl, K part kp), kp fastest, so that consecutive units
+  // continue the same rows.
+  const int n_units = u * ntl * kparts;
   const size_t row_bytes = (size_t)(F >> 1);
   const size_t row_blocks = (size_t)(F >> 6);
   const uint32_t lane_const[1] = {(uint32_t)lane << 2};
   const bool bc = s_rt.bc != 0;
 
-  // Items in expert-major order (item i: active expert i / ntl, tile i % ntl); the
-  // partial sums meet in LDS, so the order does not affect the result.
-  int la = 0, ltl = -1;
-  auto next_item = [&](ItemPtr<1> &P) {
-    if (++ltl < ntl && ltl != 0) {
-      P.wq[0] += 4 * row_bytes;
-      P.wa[0] += 4 * row_blocks;
-      P.ab[0] += 4 * row_blocks;
-      return;
-    }
-    if (ltl == ntl) {
-      ltl = 0;
-      ++la;
-    }
-    const size_t row = (size_t)(r0 + ltl) * 4 + lanej;
-    const int e = s_rt.active[la];
+  auto unit_fields = [&](int i, int &tl, int &kp) {
+    kp = i % kparts;
+    const int r = i / kparts;
+    tl = r % ntl;
+    return r / ntl;  // active index
+  };
+  auto set_ptrs = [&](ItemPtr<1> &P, int i) {
+    int tl, kp;
+    const int a = unit_fields(i, tl, kp);
+    const int s_lo = kp * nsq;
+    const size_t row = (size_t)(r0 + tl) * 4 + lanej;
+    const int e = s_rt.active[a];
     P.wq[0] = (gq_t)s_eptr[e][0] + row * row_bytes + s_lo * 256 + blk * 16;
     P.wa[0] = (ga_t)s_eptr[e][1] + row * row_blocks + s_lo * 8 + (blk >> 1);
-    P.ab[0] = (ga_t)s_eptr[e][1] + (size_t)(r0 + ltl) * 4 * row_blocks + s_lo * 8;
-    const int jj = (!bc && lanej < s_rt.counts[la]) ? lanej : 0;
-    P.ap = (gx_t)h + (size_t)(s_rt.offsets[la] + jj) * F + (size_t)s_lo * kStageVals + blk * 32 +
+    P.ab[0] = (ga_t)s_eptr[e][1] + (size_t)(r0 + tl) * 4 * row_blocks + s_lo * 8;
+    const int jj = (!bc && lanej < s_rt.counts[a]) ? lanej : 0;
+    P.ap = (gx_t)h + (size_t)(s_rt.offsets[a] + jj) * F + (size_t)s_lo * kStageVals + blk * 32 +
            (bc ? lanej * 8 : 0);
   };
-  int ca = 0, ctl = 0;
   // nrows: result rows to keep (1 when the stream accumulated row 0 only; the combine then
   // reads row 0, slot_m being 0 for every slot).
-  auto finish_rows = [&](f32x4 (&ac)[1], int nrows) {
+  auto finish_unit = [&](f32x4 (&ac)[1], int i, int nrows) {
 #pragma unroll
     for (int q = 0; q < 4; ++q)
       if (q < nrows) ac[0][q] = lanes_sum16(ac[0][q]);
     if (blk == 0) {
+      int tl, kp;
+      const int a = unit_fields(i, tl, kp);
 #pragma unroll
       for (int m = 0; m < 4; ++m)
-        if (m < nrows) s_part[ctl][ca][wave][lanej * 4 + m] = ac[0][m];
-    }
-    if (++ctl == ntl) {
-      ctl = 0;
-      ++ca;
+        if (m < nrows) s_part[tl][a][kp][lanej * 4 + m] = ac[0][m];
     }
   };
-  auto finish = [&](f32x4 (&ac)[1]) { finish_rows(ac, 4); };
-  auto finish1 = [&](f32x4 (&ac)[1]) { finish_rows(ac, 1); };
   auto hook = [&]() {};
-  auto slow_code = [&]() -> const float * { return s_rt.code2[ca]; };
   const bool slow = s_rt.slow2 != 0;
-  if (!slow && bc && nsq == 7)
-    stream_aligned<1, 7, 7, false, true, false, kLookahead>(n_items, next_item, finish1, hook, slow_code, s_tbl,
-                                             lane_const, row_blocks, s_aslot[wave], nullptr);
-  else if (!slow && bc && nsq == 8)
-    stream_aligned<1, 8, 8, false, true, false, kLookahead>(n_items, next_item, finish1, hook, slow_code, s_tbl,
-                                             lane_const, row_blocks, s_aslot[wave], nullptr);
-  else if (!slow && bc)
-    stream_items<1, 8, false, true>(n_items, nsq, next_item, finish, hook, slow_code, s_tbl, lane_const);
-  else if (!slow)
-    stream_items<1, 8, false, false>(n_items, nsq, next_item, finish, hook, slow_code, s_tbl, lane_const);
-  else if (bc)
-    stream_items<1, 8, true, true>(n_items, nsq, next_item, finish, hook, slow_code, s_tbl, lane_const);
-  else
-    stream_items<1, 8, true, false>(n_items, nsq, next_item, finish, hook, slow_code, s_tbl, lane_const);
+  if (!slow && bc && nsq == 4) {
+    // Single token: units of two tiles (pair tp: tiles 2tp, 2tp+1) share the activation
+    // operand; the workgroup's units are shared through the work counter.
+    const int npairs = (ntl + 1) >> 1;
+    const int n_pu = u * npairs * kparts;
+    auto pair_fields = [&](int i, int &tp, int &kp) {
+      kp = i % kparts;
+      const int r = i / kparts;
+      tp = r % npairs;
+      return r / npairs;  // active index
+    };
+    auto grab = [&]() -> int {
+      int t = 0;
+      if (lane == 0) t = __hip_atomic_fetch_add(&s_ticket, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      t = __builtin_amdgcn_readfirstlane(t);
+      return t < n_pu ? t : -1;
+    };
+    auto set_ptrs2 = [&](ItemPtr<2> &P, int i) {
+      int tp, kp;
+      const int a = pair_fields(i, tp, kp);
+      const int s_lo = kp * nsq;
+      const int e = s_rt.active[a];
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int tl = min(2 * tp + q, ntl - 1);  // an odd last tile is read twice
+        const size_t row = (size_t)(r0 + tl) * 4 + lanej;
+        P.wq[q] = (gq_t)s_eptr[e][0] + row * row_bytes + s_lo * 256 + blk * 16;
+        P.wa[q] = (ga_t)s_eptr[e][1] + row * row_blocks + s_lo * 8 + (blk >> 1);
+        P.ab[q] = (ga_t)s_eptr[e][1] + (size_t)(r0 + tl) * 4 * row_blocks + s_lo * 8;
+      }
+      P.ap = (gx_t)h + (size_t)s_rt.offsets[a] * F + (size_t)s_lo * kStageVals + blk * 32 + lanej * 8;
+    };
+    auto finish2 = [&](f32x4 (&ac)[2], int i) {
+      const float v0 = lanes_sum16(ac[0][0]);
+      const float v1 = lanes_sum16(ac[1][0]);
+      if (blk == 0) {
+        int tp, kp;
+        const int a = pair_fields(i, tp, kp);
+        s_part[2 * tp][a][kp][lanej * 4] = v0;
+        if (2 * tp + 1 < ntl) s_part[2 * tp + 1][a][kp][lanej * 4] = v1;
+      }
+    };
+    const uint32_t lane_const2[2] = {(uint32_t)lane << 2, (uint32_t)lane << 2};
+    stream_aligned<2, 4, 4, true, false, kLookahead>(grab, set_ptrs2, finish2, hook, s_tbl,
+                                                     lane_const2, row_blocks, s_aslot[wave], nullptr);
+  } else {
+    // Each wave takes a contiguous part of the units.
+    const int i0 = wave * n_units / kDecWaves;
+    const int n_items = (wave + 1) * n_units / kDecWaves - i0;
+    int li = i0 - 1;
+    auto next_item = [&](ItemPtr<1> &P) { set_ptrs(P, ++li); };
+    int ci = i0;
+    auto finish = [&](f32x4 (&ac)[1]) { finish_unit(ac, ci++, 4); };
+    auto slow_code = [&]() -> const float * {
+      int tl, kp;
+      return s_rt.code2[unit_fields(ci, tl, kp)];
+    };
+    if (!slow && bc)
+      stream_items<1, 8, false, true>(n_items, nsq, next_item, finish, hook, slow_code, s_tbl, lane_const);
+    else if (!slow)
+      stream_items<1, 8, false, false>(n_items, nsq, next_item, finish, hook, slow_code, s_tbl, lane_const);
+    else if (bc)
+      stream_items<1, 8, true, true>(n_items, nsq, next_item, finish, hook, slow_code, s_tbl, lane_const);
+    else
+      stream_items<1, 8, true, false>(n_items, nsq, next_item, finish, hook, slow_code, s_tbl, lane_const);
+  }
   __syncthreads();
 
-  // ---- combine: one thread per (tile, token, row); slots in ascending expert order
+  // ---- combine: one thread per (tile, token, row); slots in ascending expert order; the
+  // K parts of an expert are summed in part order.
   if (tid < ntl * T * 4) {
     const int tl = tid / (T * 4);
     const int rem = tid - tl * T * 4;
@@ -947,8 +1004,8 @@ decode_down_kernel(const ExpertTable tab, const DecodeRoute *__restrict__ route,
       const int s = t * k + ord[jj];
       const int a = s_rt.slot_a[s];
       const int m = s_rt.slot_m[s];
-      const float y = s_part[tl][a][0][jr * 4 + m] + s_part[tl][a][1][jr * 4 + m] +
-                      s_part[tl][a][2][jr * 4 + m] + s_part[tl][a][3][jr * 4 + m];
+      float y = s_part[tl][a][0][jr * 4 + m];
+      for (int kp = 1; kp < kparts; ++kp) y += s_part[tl][a][kp][jr * 4 + m];
       const float pr = bf16_to_f32(f32_to_bf16(y)) * s_rt.slot_w[s];
       o = bf16_to_f32(f32_to_bf16(o + pr));
     }
@@ -958,10 +1015,22 @@ decode_down_kernel(const ExpertTable tab, const DecodeRoute *__restrict__ route,
 
 }  // namespace
 
+// One workgroup per CU: each owns ceil(tiles / CUs) 4-row output tiles of the down GEMV.
 int decode_tiles_per_wg(int32_t H) {
   const int rt = H / 4;
-  const int cap = 2 * device_cu_count();
+  const int cap = device_cu_count();
   return (rt + cap - 1) / cap;
+}
+
+// K parts of the down GEMV (at most 8): F/512 / 4 when the F/512 stages split into parts of
+// 4 (the single-token path's item), else the smallest divisor d of the stages that leaves
+// at most 8 stages per part, else 1.
+int decode_kparts(int32_t F) {
+  const int ns = F / kStageVals;
+  if (ns % 4 == 0 && ns / 4 <= kDecMaxKParts) return ns / 4;
+  for (int d = 1; d <= kDecMaxKParts; ++d)
+    if (ns % d == 0 && ns / d <= 8) return d;
+  return 1;
 }
 
 bool decode_layer_supported(int64_t T, int32_t k, int32_t E, int32_t H, int32_t F) {
@@ -973,27 +1042,14 @@ bool decode_layer_supported(int64_t T, int32_t k, int32_t E, int32_t H, int32_t 
 
 int64_t decode_route_bytes() { return (int64_t)sizeof(DecodeRoute); }
 
-// Workgroups of the gate/up kernel.  Its waves split the (routed expert, 4-row tile) items
-// evenly, in order; the item count is u * F/4 for the u routed experts, known only inside
-// the kernel.  With more items than wave slots (two workgroups per CU), the wave count is
-// the largest divisor of F/4 (a multiple of the workgroup's wave count) that fills at least
-// 3/4 of the slots: every wave then gets exactly u * (F/4) / waves items whatever u is,
-// instead of some waves one item more than others.
+// Workgroups of the gate/up kernel: one per CU at most; each takes an even share of the
+// (routed expert, 4-row tile) items, which its waves then share through an LDS counter
+// (or split evenly, off the single-token path).
 int64_t decode_gateup_groups(int64_t T, int32_t k, int32_t E, int32_t F) {
-  const int64_t slots = 2 * (int64_t)device_cu_count() * kFfnWaves;
   const int64_t u_max = T * k < E ? T * k : E;
-  const int64_t te = F / 4;
-  int64_t waves = u_max * te;
-  if (waves > slots) {
-    waves = slots;
-    for (int64_t d = 1; d <= te; ++d) {
-      const int64_t w = te / d;
-      if (te % d != 0 || w % kFfnWaves != 0 || w > slots) continue;
-      if (4 * w >= 3 * slots) waves = w;
-      break;
-    }
-  }
-  return (waves + kFfnWaves - 1) / kFfnWaves;
+  const int64_t groups = (u_max * (F / 4) + kDecWaves - 1) / kDecWaves;
+  const int64_t cap = device_cu_count();
+  return groups < cap ? groups : cap;
 }
 
 // Gate/up (with routing) then down (with combine).  `ev`, when given, receives marks
@@ -1023,7 +1079,7 @@ int launch_decode_layer(const moe_nf4_expert_t *experts, int32_t E, const void *
   if (ev) MOE_HIP_CHECK(hipEventRecord(ev[0], s));
   if (ev) MOE_HIP_CHECK(hipEventRecord(ev[1], s));
   auto gateup = [&](auto kern) {
-    hipLaunchKernelGGL(kern, dim3((unsigned)g1), dim3(kFfnThreads), 0, s, tab,
+    hipLaunchKernelGGL(kern, dim3((unsigned)g1), dim3(kDecThreads), 0, s, tab,
                        (const uint16_t *)x, (const uint16_t *)gate, (const float *)bias, (int)T, H,
                        F, E, k, (uint16_t *)logits, (float *)weights, (int64_t *)idx64,
                        (DecodeRoute *)route_ws, (uint16_t *)h_ws);
@@ -1034,9 +1090,9 @@ int launch_decode_layer(const moe_nf4_expert_t *experts, int32_t E, const void *
     gateup(decode_gateup_kernel<16>);
   MOE_LAUNCH_CHECK();
   if (ev) MOE_HIP_CHECK(hipEventRecord(ev[2], s));
-  hipLaunchKernelGGL(decode_down_kernel, dim3((unsigned)g2), dim3(kFfnThreads), 0, s, tab,
+  hipLaunchKernelGGL(decode_down_kernel, dim3((unsigned)g2), dim3(kDecThreads), 0, s, tab,
                      (const DecodeRoute *)route_ws, (const uint16_t *)h_ws, (int)T, H, F, E, k,
-                     tpw, (uint16_t *)out);
+                     tpw, decode_kparts(F), (uint16_t *)out);
   MOE_LAUNCH_CHECK();
   if (ev) MOE_HIP_CHECK(hipEventRecord(ev[3], s));
   return MOE_STATUS_OK;
