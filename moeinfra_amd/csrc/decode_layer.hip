@@ -423,24 +423,6 @@ __device__ __forceinline__ void build_table_regs(uint32_t *tbl, const float (&c_
   }
 }
 
-// Sum over the 64 lanes, every lane gets the result: DPP within each row of 16 lanes
-// (xor 1, xor 2, rotate 4, rotate 8), then two cross-row exchanges.  Fixed order, so all
-// workgroups obtain bit-identical sums.
-template <int CTRL>
-__device__ __forceinline__ float dpp_mov(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xf,
-                                                            0xf, false));
-}
-__device__ __forceinline__ float wave_sum_fast(float v) {
-  v += dpp_mov<0xB1>(v);   // quad_perm [1,0,3,2]
-  v += dpp_mov<0x4E>(v);   // quad_perm [2,3,0,1]
-  v += dpp_mov<0x124>(v);  // row_ror:4
-  v += dpp_mov<0x128>(v);  // row_ror:8
-  v += __shfl_xor(v, 16, kWave);
-  v += __shfl_xor(v, 32, kWave);
-  return v;
-}
-
 // Reductions over the 16 lanes of a DPP row (every lane of the row gets the result).
 __device__ __forceinline__ float row_max16(float v) {
   v = fmaxf(v, dpp_mov<0xB1>(v));   // quad_perm [1,0,3,2]
@@ -462,10 +444,11 @@ __device__ __forceinline__ float row_sum16(float v) {
 // logit (+ bias) -> fp32 softmax over the row -> top-k by k rounds of row arg-max (ties:
 // the lowest expert index) -> weights renormalised by their sum in rank order.  Then the
 // grouping of the T*k slots (s = t*k + j) by expert, ascending expert and ascending slot,
-// written to the wave's RouteHead.  Every wave runs this on its own copy: no barrier.
+// written to `rh` (in LDS; the caller publishes it to the other waves).
 struct RouteSummary {
-  int n_active;  // wave-uniform
+  int n_active;      // wave-uniform
   bool bc;
+  uint32_t present;  // bit x: expert x has a slot
 };
 
 template <int EMAX, int NW>
@@ -492,7 +475,8 @@ __device__ __forceinline__ RouteSummary route_wave(RouteHead &rh, int32_t (&sl_e
   const float pe = valid ? expf(l - m) : 0.0f;
   const float p = pe / row_sum16(pe);
   bool taken = false;
-  float wsum = 0.0f;
+  float wsum = 0.0f, my_w = 0.0f;
+  int my_win = 0;
   for (int j = 0; j < k; ++j) {
     const bool cand = valid && !taken;
     const float best = row_max16(cand ? p : -1.0f);
@@ -505,52 +489,73 @@ __device__ __forceinline__ RouteSummary route_wave(RouteHead &rh, int32_t (&sl_e
     if (win > 15) win = 0;
     taken |= e == win;
     wsum += best;
-    if (e == 0 && t < T) {
-      sl_e[t * k + j] = win;
-      sl_w[t * k + j] = best;
+    if (e == j) {  // lane j of the row keeps choice j
+      my_win = win;
+      my_w = best;
     }
   }
-  if (e == 0 && t < T) {
-    for (int j = 0; j < k; ++j) sl_w[t * k + j] = sl_w[t * k + j] / wsum;
+  const float my_wn = my_w / wsum;
+  if (t < T && e < k) {
+    sl_e[t * k + e] = my_win;
+    sl_w[t * k + e] = my_wn;
   }
-  wave_lds_sync();  // the row leaders' slot entries are read by other lanes below
-  // Grouping: lane s < ns is slot s; expert counts by ballot, ascending expert order.
+  // Grouping of the ns = T*k slots (slot s = t*k + j lives in lane 16*(s/k) + s%k): the
+  // slot experts are gathered into scalars, then lane s < ns places its slot with a few
+  // compares against them -- no loop over the experts, no LDS round trip.
   const int ns = T * k;
-  const int my_e = lane < ns ? sl_e[lane] : -1;
-  const uint64_t below = (1ull << lane) - 1ull;
-  int n_active = 0, run = 0, my_row = 0, my_a = 0, my_rank = 0;
-  bool multi = false;
-  for (int x = 0; x < E; ++x) {
-    const uint64_t mx = __ballot(my_e == x);
-    const int c = __popcll(mx);
-    if (c > 0) {
-      if (lane == 0) {
-        rh.active[n_active] = x;
-        rh.counts[n_active] = c;
-        rh.offsets[n_active] = run;
-      }
-      if (my_e == x) {
-        my_rank = __popcll(mx & below);
-        my_row = run + my_rank;
-        my_a = n_active;
-      }
-      multi |= c > 1;
-      ++n_active;
-      run += c;
+  int se[kDecMaxSlots];
+  float sw[kDecMaxSlots];
+  int stok[kDecMaxSlots];
+  uint32_t present = 0;
+  int tq = 0, jq = 0;  // token and choice of slot q
+#pragma unroll
+  for (int q = 0; q < kDecMaxSlots; ++q) {
+    const int src = q < ns ? 16 * tq + jq : 0;
+    se[q] = q < ns ? __builtin_amdgcn_readlane(my_win, src) : 0x7fff;
+    sw[q] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_wn), src));
+    stok[q] = tq;
+    if (q < ns) present |= 1u << se[q];
+    if (++jq == k) {
+      jq = 0;
+      ++tq;
     }
   }
+  int my_e = se[0], my_tok = stok[0];
+  float my_sw = sw[0];
+#pragma unroll
+  for (int q = 1; q < kDecMaxSlots; ++q)
+    if (lane == q) {
+      my_e = se[q];
+      my_sw = sw[q];
+      my_tok = stok[q];
+    }
+  int before = 0, same = 0, rank = 0;  // slots of smaller experts / of mine / of mine before me
+#pragma unroll
+  for (int q = 0; q < kDecMaxSlots; ++q) {
+    before += se[q] < my_e ? 1 : 0;
+    same += se[q] == my_e ? 1 : 0;
+    rank += (se[q] == my_e && q < lane) ? 1 : 0;
+  }
+  const int my_a = __builtin_popcount(present & ((1u << my_e) - 1u));  // active index
+  const int n_active = __builtin_popcount(present);
+  const bool multi = __ballot(lane < ns && same > 1) != 0;
   if (lane < ns) {
-    rh.perm_tok[my_row] = lane / k;
+    rh.perm_tok[before + rank] = my_tok;
     rh.slot_a[lane] = my_a;
-    rh.slot_m[lane] = my_rank;
-    rh.slot_w[lane] = sl_w[lane];
+    rh.slot_m[lane] = rank;
+    rh.slot_w[lane] = my_sw;
+    if (rank == 0) {  // the first slot of each expert describes it
+      rh.active[my_a] = my_e;
+      rh.counts[my_a] = same;
+      rh.offsets[my_a] = before;
+    }
   }
   if (lane == 0) {
     rh.n_active = n_active;
     rh.bc = multi ? 0 : 1;
   }
   wave_lds_sync();  // rh is read by every lane of the wave afterwards
-  return RouteSummary{n_active, !multi};
+  return RouteSummary{n_active, !multi, present};
 }
 
 template <int EMAX>
@@ -565,9 +570,10 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
   // Codebooks of every expert: [0,16) w1, [16,32) w3, [32,48) w2 ([48,64) repeats w2).
   __shared__ float s_code[EMAX][kWave];
   __shared__ const void *s_eptr[EMAX][4];  // w1_packed, w1_absmax, w3_packed, w3_absmax
-  __shared__ __attribute__((aligned(16))) RouteHead s_rtw[kDecWaves];  // one copy per wave
-  __shared__ int32_t s_sle[kDecWaves][kDecMaxSlots];                       // per wave: slot experts
-  __shared__ float s_slw[kDecWaves][kDecMaxSlots];                         // per wave: slot weights
+  __shared__ __attribute__((aligned(16))) RouteHead s_rt;  // routing of the workgroup
+  __shared__ int32_t s_sle[kDecMaxSlots];                    // slot experts
+  __shared__ float s_slw[kDecMaxSlots];                      // slot weights
+  __shared__ __attribute__((aligned(16))) uint8_t s_slowbits[16];  // per-expert codebook flags
   __shared__ __attribute__((aligned(16))) float s_aslot[kDecWaves][2 * kASlotFloats];
   __shared__ int32_t s_ticket;  // next item of the workgroup's range (single-token path)
 
@@ -576,16 +582,6 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const bool wg0 = blockIdx.x == 0;
   if (tid == 0) s_ticket = 0;
-
-  // ---- lookup table from the NF4 codebook constants: no load in front of it, so it is
-  // written while the gate loads below are in flight.  Experts whose codebooks differ from
-  // these values take the per-nibble path (checked after the routing).
-  {
-    float cst[16];
-#pragma unroll
-    for (int q = 0; q < 16; ++q) cst[q] = kNf4Code[q];
-    build_table_regs<kDecThreads>(s_tbl, cst, cst);
-  }
 
   // ---- gate products on the 4x4x4 MFMA: wave w takes the 128-value chunks c = w, w + 8,
   // ... of H; lane (b = lane/4, j = lane%4) holds values 8b .. 8b+7 of a chunk of token j
@@ -637,6 +633,15 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
     const int f = lane & 3;
     pvw[q] = f == 0 ? p1 : f == 1 ? a1 : f == 2 ? p3 : a3;
   }
+  // ---- lookup table from the NF4 codebook constants, written while the loads above are
+  // in flight.  Experts whose codebooks differ from these values take the per-nibble path.
+  __builtin_amdgcn_sched_barrier(0);
+  {
+    float cst[16];
+#pragma unroll
+    for (int q = 0; q < 16; ++q) cst[q] = kNf4Code[q];
+    build_table_regs<kDecThreads>(s_tbl, cst, cst);
+  }
   __builtin_amdgcn_sched_barrier(0);
   for (int c0 = 0; c0 < n_chunks; c0 += CPR) {
     if (c0 > 0) {
@@ -669,58 +674,67 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
         if (lb == 0 && e < E) s_part[wave][m][e] = v;
       }
     }
-  // Unconditional stores (clamped experts rewrite identical values).
+  // Unconditional stores (clamped experts rewrite identical values), and each expert's
+  // codebook check against the table's NF4 values: bit 0 when its w1 or w3 codebook
+  // differs (lanes 0..31), bit 1 for w2 (lanes 32..47).
+  float ref_f = kNf4Code[0];
+#pragma unroll
+  for (int q = 1; q < 16; ++q)
+    if ((lane & 15) == q) ref_f = kNf4Code[q];
+  const uint32_t ref = __builtin_bit_cast(uint32_t, ref_f);
 #pragma unroll
   for (int q = 0; q < EPW; ++q) {
     const int e = wave + kDecWaves * q;
     const int ee = e < E ? e : E - 1;
     s_code[ee][lane] = cvw[q];
     s_eptr[ee][lane & 3] = pvw[q];
+    const bool diff = __builtin_bit_cast(uint32_t, cvw[q]) != ref;
+    const bool d1 = __ballot(lane < 32 && diff) != 0;
+    const bool d2 = __ballot(lane >= 32 && lane < 48 && diff) != 0;
+    if (lane == 0) s_slowbits[ee] = (uint8_t)((d1 ? 1 : 0) | (d2 ? 2 : 0));
   }
-  // The only barrier of the routing phase: gate sums, codebooks, stream pointers, the
-  // lookup table and the work counter are visible to every wave after it.
+  // Gate sums, codebooks, stream pointers, the lookup table and the work counter are
+  // visible to every wave after this barrier.
   __syncthreads();
 
-  // ---- routing and grouping, by every wave on its own copy
-  RouteHead &rt = s_rtw[wave];
-  const RouteSummary rs = route_wave<EMAX, kDecWaves>(rt, s_sle[wave], s_slw[wave], s_part, bias,
-                                                      T, E, k, (wg0 && wave == 0) ? logits_out : nullptr);
-  const int u = rs.n_active;
+  // ---- routing and grouping by wave 0 (one wave, so that the SIMDs do not run the same
+  // serial code eight times); the other waves wait at the barrier.
   const int ns = T * k;
-  // Codebook checks against the table's NF4 values: lane c < 32 checks w1|w3 word c,
-  // lanes 32..47 the w2 words.
-  float ref_f = kNf4Code[0];
+  if (wave == 0) {
+    // The codebook flags of all experts, as four words of four bytes.
+    const uint4 fb = *reinterpret_cast<const uint4 *>(s_slowbits);
+    const RouteSummary rs = route_wave<EMAX, kDecWaves>(s_rt, s_sle, s_slw, s_part, bias, T, E, k,
+                                                        wg0 ? logits_out : nullptr);
+    const uint32_t fw[4] = {(uint32_t)__builtin_amdgcn_readfirstlane(fb.x),
+                            (uint32_t)__builtin_amdgcn_readfirstlane(fb.y),
+                            (uint32_t)__builtin_amdgcn_readfirstlane(fb.z),
+                            (uint32_t)__builtin_amdgcn_readfirstlane(fb.w)};
+    uint32_t flags = 0;  // OR of the active experts' flags
 #pragma unroll
-  for (int q = 1; q < 16; ++q)
-    if ((lane & 15) == q) ref_f = kNf4Code[q];
-  const uint32_t ref = __builtin_bit_cast(uint32_t, ref_f);
-  bool d1 = false, d2 = false;
-  for (int a = 0; a < u; ++a) {
-    const uint32_t mine = __builtin_bit_cast(uint32_t, s_code[rt.active[a]][lane]);
-    if (lane < 32) d1 |= mine != ref;
-    else if (lane < 48) d2 |= mine != ref;
+    for (int x = 0; x < EMAX; ++x)
+      if ((rs.present >> x) & 1u) flags |= (fw[x >> 2] >> (8 * (x & 3))) & 3u;
+    if (lane == 0) {
+      s_rt.slow1 = (flags & 1u) ? 1 : 0;
+      s_rt.slow2 = (flags & 2u) ? 1 : 0;
+    }
   }
-  const bool slow1 = __ballot(d1) != 0;
-  const bool slow2 = __ballot(d2) != 0;
-  if (lane == 0) {
-    rt.slow1 = slow1 ? 1 : 0;
-    rt.slow2 = slow2 ? 1 : 0;
-  }
-  wave_lds_sync();
+  __syncthreads();
+  const int u = __builtin_amdgcn_readfirstlane(s_rt.n_active);
+  const bool bc = __builtin_amdgcn_readfirstlane(s_rt.bc) != 0;
+  const bool slow1 = __builtin_amdgcn_readfirstlane(s_rt.slow1) != 0;
   if (wg0 && wave == 0) {
-    const uint32_t *src = reinterpret_cast<const uint32_t *>(&rt);
+    const uint32_t *src = reinterpret_cast<const uint32_t *>(&s_rt);
     uint32_t *dst = reinterpret_cast<uint32_t *>(route_out);
     if (lane < kRouteHeadWords) dst[lane] = src[lane];
     for (int i = lane; i < kDecMaxSlots * 16; i += kWave) {
       const int a = i >> 4;
-      route_out->code2[a][i & 15] = a < u ? s_code[rt.active[a]][32 + (i & 15)] : 0.0f;
+      route_out->code2[a][i & 15] = a < u ? s_code[s_rt.active[a]][32 + (i & 15)] : 0.0f;
     }
     if (lane < ns) {
-      w_out[lane] = s_slw[wave][lane];
-      idx_out[lane] = s_sle[wave][lane];
+      w_out[lane] = s_slw[lane];
+      idx_out[lane] = s_sle[lane];
     }
   }
-  const RouteHead &s_rt = rt;
 
   // ---- w1/w3 stream over the workgroup's range of the (active expert, 4-row tile) items
   const int lanej = lane & 3;
@@ -733,7 +747,6 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
   const size_t row_bytes = (size_t)(H >> 1);
   const size_t row_blocks = (size_t)(H >> 6);
   const uint32_t lane_const[2] = {(uint32_t)(lane & 31) << 2, ((uint32_t)(lane & 31) << 2) | 128u};
-  const bool bc = rs.bc;
 
   // Pointers of item i = (active expert a, tile): rebuilt from the LDS tables.
   auto item_expert = [&](int i, int &tile) {

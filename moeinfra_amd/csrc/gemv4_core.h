@@ -95,10 +95,18 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// DPP move of v with control CTRL (row_mask and bank_mask all set, no bound control).
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xf,
+                                                            0xf, false));
+}
+
 __device__ __forceinline__ float lanes_sum16(float v) {
-  // Sum over the 16 lanes that share l % 4 (the block index occupies lane bits 2..5).
-  v += __shfl_xor(v, 4, kWave);
-  v += __shfl_xor(v, 8, kWave);
+  // Sum over the 16 lanes that share l % 4 (the block index occupies lane bits 2..5):
+  // rotations by 4 and 8 within each 16-lane row (DPP), then the two cross-row pairs.
+  v += dpp_mov<0x124>(v);  // row_ror:4
+  v += dpp_mov<0x128>(v);  // row_ror:8
   v += __shfl_xor(v, 16, kWave);
   v += __shfl_xor(v, 32, kWave);
   return v;
