@@ -55,11 +55,19 @@ def nf4_expert_bytes(h: int, f: int) -> int:
     return 3 * (n // 2 + n // 64 * 4)
 
 
-def gateup_bytes(u: int, h: int, f: int, t: int, k: int) -> int:
+def decode_form(t: int, k: int, e: int, h: int, f: int) -> bool:
+    """Whether the layer call runs as the two-launch decode form (routing fused into the
+    gate/up kernel, combine into the down kernel)."""
+    return t <= 4 and t * k <= 8 and e <= 16 and h % 512 == 0 and f % 512 == 0
+
+
+def gateup_bytes(u: int, h: int, f: int, t: int, k: int, e: int) -> int:
     """Algorithmic HBM bytes of one gate/up launch: w1+w3 NF4 of the u routed experts,
-    the T activations read, the T*k h rows written."""
+    the T activations read, the T*k h rows written, and in the decode form the [E, H]
+    router gate it reads for the fused routing."""
     n = h * f
-    return u * 2 * (n // 2 + n // 64 * 4) + t * h * 2 + t * k * f * 2
+    gate = e * h * 2 if decode_form(t, k, e, h, f) else 0
+    return u * 2 * (n // 2 + n // 64 * 4) + t * h * 2 + t * k * f * 2 + gate
 
 
 def down_bytes(u: int, h: int, f: int, t: int, k: int, nsplit: int) -> int:
@@ -165,22 +173,26 @@ def main() -> int:
     # ------------------------------------------------------------------ kernel times
     gu_us = down_us = route_us = None
     if hip:
-        route_us = hip.mean_us([(e[0], e[1]) for e in evs])
+        # In the decode form the routing runs inside the gate/up kernel and events 0 and 1
+        # are recorded back to back: no routing time of its own.
+        route_us = None if decode_form(T, K, E, H, F) else hip.mean_us([(e[0], e[1]) for e in evs])
         gu_us = hip.mean_us([(e[1], e[2]) for e in evs])
         down_us = hip.mean_us([(e[2], e[3]) for e in evs])
     u_mean = sum(u_per_layer) / L
     prof_layers = [s_ % L for s_ in range(args_ns.steps)]
-    gu_bytes = sum(gateup_bytes(u_per_layer[l], H, F, T, K) for l in prof_layers) / len(prof_layers)
+    gu_bytes = sum(gateup_bytes(u_per_layer[l], H, F, T, K, E) for l in prof_layers) / len(prof_layers)
     ly_bytes = sum(layer_bytes(u, H, F, T, E) for u in u_per_layer) / L
     layer_us = ms_per_step * 1e3 / L
     layer_gbps = ly_bytes / (layer_us * 1e-6) / 1e9
 
+    gu_kernel = ("decode_gateup_kernel (routing + NF4 w1/w3 GEMV + SwiGLU)" if decode_form(T, K, E, H, F)
+                 else "gateup_kernel / gemv4_kernel (NF4 w1/w3 + SwiGLU)")
     roofline = None
     if gu_us:
         ach = gu_bytes / (gu_us * 1e-6) / 1e9
         roofline = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBPS,
                     "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBPS, 4),
-                    "traffic": _traffic("gateup_nf4_decode_t%d" % T), "kernel": "gemv4_kernel<true> (gate/up)",
+                    "traffic": _traffic("gateup_nf4_decode_t%d" % T), "kernel": gu_kernel,
                     "bytes_per_launch": int(gu_bytes), "avg_launch_us": round(gu_us, 2)}
 
     # ------------------------------------------------------------------ CPU baseline

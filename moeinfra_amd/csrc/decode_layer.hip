@@ -38,6 +38,9 @@ constexpr int kDecWaves = 8;
 constexpr int kDecThreads = kDecWaves * kWave;
 // The down kernel splits K (= F) of every (tile, expert) into at most this many parts.
 constexpr int kDecMaxKParts = 8;
+// Items per workgroup whose sums the single-token gate/up path keeps in LDS until the end.
+constexpr int kRawSlots = 32;
+
 
 // Routing of one decode step, written by workgroup 0 of the gate/up kernel and read by
 // the down kernel.  "Active" experts are those with at least one routed slot, in
@@ -316,7 +319,13 @@ __device__ __forceinline__ void stream_aligned(GrabFn &&grab, PtrFn &&set_ptrs,
   }
   store_abs();
   hook();
+  // The next two items are known ahead, and the next item's pointers are set up at the
+  // start of the current one: the work counter's and the LDS tables' latencies stay off
+  // the step that switches the loads to the next item.
   int nxt = grab();
+  int nxt2 = nxt >= 0 ? grab() : -1;
+  ItemPtr<NP> Pn = P;
+  if (nxt >= 0) set_ptrs(Pn, nxt);
 
   f32x4 acc[NP];
 #pragma unroll
@@ -332,7 +341,7 @@ __device__ __forceinline__ void stream_aligned(GrabFn &&grab, PtrFn &&set_ptrs,
 #pragma unroll
     for (int d = 0; d < NSQ; ++d) {
       if (d == kNext && nxt >= 0) {
-        set_ptrs(P, nxt);
+        P = Pn;
         load_abs();
       }
       const int g = d + DEPTH - 1;  // stage sequence index of this step's load
@@ -388,7 +397,9 @@ __device__ __forceinline__ void stream_aligned(GrabFn &&grab, PtrFn &&set_ptrs,
     if (nxt < 0) break;
     store_abs();
     cur = nxt;
-    nxt = grab();
+    nxt = nxt2;
+    if (nxt >= 0) set_ptrs(Pn, nxt);
+    nxt2 = nxt >= 0 ? grab() : -1;
   }
 }
 
@@ -576,6 +587,9 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
   __shared__ __attribute__((aligned(16))) uint8_t s_slowbits[16];  // per-expert codebook flags
   __shared__ __attribute__((aligned(16))) float s_aslot[kDecWaves][2 * kASlotFloats];
   __shared__ int32_t s_ticket;  // next item of the workgroup's range (single-token path)
+  // Single-token path: per item of the workgroup, the per-lane sums of w1 and w3 (row
+  // j = lane % 4 of the tile, block lane / 4).
+  __shared__ float s_raw[kRawSlots][2][kWave];
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
@@ -795,17 +809,44 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
   auto hook = [&]() {};
   const bool slow = slow1;
   if (!slow && bc && nsq == 8 && T == 1) {
-    // Single token: the workgroup's items are shared through the work counter.
+    // Single token: the workgroup's items are shared through the work counter.  With at
+    // most kRawSlots items per workgroup, an item's per-lane sums go to LDS as they are (no
+    // cross-lane reduction or SwiGLU in the stream) and the workgroup reduces them after
+    // the stream (blocks 0 to 15 in order) and writes h.
     auto grab = [&]() -> int {
       int t = 0;
       if (lane == 0) t = __hip_atomic_fetch_add(&s_ticket, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
       t = __builtin_amdgcn_readfirstlane(t) + wlo;
       return t < whi ? t : -1;
     };
-    auto finish1 = [&](f32x4 (&ac)[2], int i) { finish_item(ac, i, 1); };
+    const gx_t xb = (gx_t)x + blk * 32 + lanej * 8;
+    const int nit = whi - wlo;
+    if (nit > kRawSlots) {
+      auto finish1 = [&](f32x4 (&ac)[2], int i) { finish_item(ac, i, 1); };
+      stream_aligned<2, 8, kGateUpDepth, true, true, kLookahead>(
+          grab, set_ptrs, finish1, hook, s_tbl, lane_const, row_blocks, s_aslot[wave], xb);
+      return;
+    }
+    auto finish_raw = [&](f32x4 (&ac)[2], int i) {
+      s_raw[i - wlo][0][lane] = ac[0][0];
+      s_raw[i - wlo][1][lane] = ac[1][0];
+    };
     stream_aligned<2, 8, kGateUpDepth, true, true, kLookahead>(
-        grab, set_ptrs, finish1, hook, s_tbl, lane_const, row_blocks, s_aslot[wave],
-        (gx_t)x + blk * 32 + lanej * 8);
+        grab, set_ptrs, finish_raw, hook, s_tbl, lane_const, row_blocks, s_aslot[wave], xb);
+    __syncthreads();
+    if (tid < 4 * nit) {
+      const int slot = tid >> 2;
+      const int j = tid & 3;
+      float g = 0.0f, up = 0.0f;
+#pragma unroll
+      for (int b = 0; b < 16; ++b) {
+        g += s_raw[slot][0][4 * b + j];
+        up += s_raw[slot][1][4 * b + j];
+      }
+      int tile;
+      const int a = item_expert(wlo + slot, tile);
+      h_out[(size_t)s_rt.offsets[a] * F + tile * 4 + j] = swiglu_bf16(g, up);
+    }
     return;
   }
   // Other shapes: each wave takes a contiguous part of the workgroup's range.
@@ -927,10 +968,10 @@ decode_down_kernel(const ExpertTable tab, const DecodeRoute *__restrict__ route,
   };
   auto hook = [&]() {};
   const bool slow = s_rt.slow2 != 0;
+  const int npairs = (ntl + 1) >> 1;
   if (!slow && bc && nsq == 4) {
     // Single token: units of two tiles (pair tp: tiles 2tp, 2tp+1) share the activation
     // operand; the workgroup's units are shared through the work counter.
-    const int npairs = (ntl + 1) >> 1;
     const int n_pu = u * npairs * kparts;
     auto pair_fields = [&](int i, int &tp, int &kp) {
       kp = i % kparts;
