@@ -171,3 +171,61 @@ def test_single_expert_matches_oracle(cuda_device, T, H, F):
     got = ops.expert_swiglu(ex.c_struct(), x.to(cuda_device), H, F)
     err = orc.rel_l2(orc.bf16_to_f32(bits(got)), orc.bf16_to_f32(want))
     assert err <= 1e-2, err
+
+
+# ------------------------------------------------------------------------------ decode layer
+# Shapes that reach the branches of the two-launch decode form (T <= 4, T*k <= 8, E <= 16,
+# H and F multiples of 512): 16 experts (the 16-expert kernel instantiation), an odd number
+# of 4-row output tiles per workgroup in the single-token down GEMV's two-tile units
+# (H = 2560: 640 tiles over 256 CUs -> 3 per workgroup), and two-token batches with 16
+# experts and a skewed router.
+@pytest.mark.parametrize("H,F,E,T,seed,skew", [
+    (512, 1024, 16, 1, 21, False),
+    (512, 1024, 16, 4, 22, False),
+    (1024, 2048, 16, 2, 23, True),
+    (2560, 2048, 8, 1, 24, False),
+])
+def test_decode_layer_branches(cuda_device, H, F, E, T, seed, skew):
+    want, i_want, got, i_got, lg = _layer_case(cuda_device, H, F, E, T, seed, skew)
+    tie = near_tie_rows(lg)
+    np.testing.assert_array_equal(i_got[~tie], i_want[~tie])
+    ok = ~tie
+    err = orc.rel_l2(orc.bf16_to_f32(got[ok]), orc.bf16_to_f32(want[ok]))
+    assert err <= 1e-2, err
+
+
+def test_decode_single_token_long_ffn(cuda_device):
+    """Single token, hidden 4096 (the single-token gate/up stream) with F = 16896: 33 items
+    per workgroup on 256 CUs, more than the workgroup keeps in LDS, so the per-item
+    reduction path runs.  Weights are drawn and quantised on the GPU; the oracle
+    dequantises the routed experts."""
+    from moeinfra_amd import ops
+    from moeinfra_amd._lib import MoeNf4Expert
+
+    H, F, E = 4096, 16896, 4
+    g = torch.Generator(device=cuda_device).manual_seed(77)
+    keep = []
+    for e in range(E):
+        st = {}
+        for name, shape in (("w1", (F, H)), ("w3", (F, H)), ("w2", (H, F))):
+            w = (torch.randn(shape, generator=g, device=cuda_device) * 0.02).to(torch.bfloat16)
+            st[name] = ops.nf4_quantize(w)
+            del w
+        keep.append(st)
+    gate = (torch.randn((E, H), generator=g, device=cuda_device) * 0.02).to(torch.bfloat16)
+    table = ops.expert_table([MoeNf4Expert(*(t.data_ptr() for n in ("w1", "w3", "w2")
+                                             for t in st[n])) for st in keep])
+    x = torch.randn((1, H), generator=g, device=cuda_device).to(torch.bfloat16)
+    out, _, w, idx = ops.layer_forward(table, E, gate, x, 2, F)
+    torch.cuda.synchronize()
+
+    def expert_fn(e, rows):
+        st = {n: (keep[e][n][0].cpu().numpy().reshape(-1), keep[e][n][1].cpu().numpy())
+              for n in ("w1", "w3", "w2")}
+        return orc.swiglu(rows, *orc.dequant_expert(st, H, F, threads=8))
+
+    want, (lg_o, w_o, idx_o) = orc.moe_layer(bits(x), bits(gate), expert_fn)
+    ok = ~near_tie_rows(lg_o)
+    np.testing.assert_array_equal(idx.cpu().numpy()[ok], idx_o[ok])
+    err = orc.rel_l2(orc.bf16_to_f32(bits(out)[ok]), orc.bf16_to_f32(want[ok]))
+    assert err <= 1e-2, err
