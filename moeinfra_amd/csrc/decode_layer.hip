@@ -3,27 +3,28 @@
 // slots and E <= 16 experts (Mixtral decode: T = 1, k = 2, E = 8).
 //
 // Why: at batch 1 a Mixtral layer streams ~198 MB of NF4 weights; every extra kernel
-// boundary costs a few microseconds (cache write-back/invalidate, ramp-up), and any
-// chain of dependent global loads before a workgroup's first weight load delays the
-// whole stream by one memory round trip per link.  So:
+// boundary costs about a microsecond, and any chain of dependent global loads before a
+// wave's first weight load delays the whole stream by one memory round trip per link.
+// Both kernels run one 8-wave workgroup per CU (one copy of the 64 KB codebook table per
+// CU; the CU's waves share its items through an LDS counter).  So:
 //
 //  decode_gateup_kernel  every workgroup recomputes the routing of the <= 4 tokens (the
-//    gate is 64 KB and stays in L2): logits = bf16(x . gate^T) with fp32 accumulation,
-//    fp32 softmax (+ optional per-expert bias), top-k (descending, ties keep the lower
-//    index), renormalised weights, then the grouping of the T*k slots by expert
+//    gate is 64 KB and stays in L2): logits = bf16(x . gate^T) with fp32 accumulation
+//    (MFMA), fp32 softmax (+ optional per-expert bias), top-k (descending, ties keep the
+//    lower index), renormalised weights, then the grouping of the T*k slots by expert
 //    (engine/router.py:50-94, model/moe_layer.py:142-191).  The workgroup then streams
 //    its share of the (active expert, 4-row tile) list of w1/w3 and writes
 //    h = bf16(silu(bf16(w1 x)) * bf16(w3 x)) per routed row.  Workgroup 0 publishes the
 //    routing outputs and a compact descriptor (DecodeRoute) for the down kernel.
 //
 //  decode_down_kernel  one descriptor load, then each workgroup owns whole 4-row tiles
-//    of the output and runs them for every active expert, its four waves splitting K
-//    into quarters; the quarters meet in LDS, each expert's row value is rounded to bf16
-//    (the expert's output dtype) and the slots of each token are combined in ascending
-//    expert order, o = bf16(o + bf16(y_e) * w_e) (model/moe_layer.py:147,187-191).
+//    of the output and runs them for every active expert, K split into parts that meet
+//    in LDS; each expert's row value is rounded to bf16 (the expert's output dtype) and
+//    the slots of each token are combined in ascending expert order,
+//    o = bf16(o + bf16(y_e) * w_e) (model/moe_layer.py:147,187-191).
 //
-// Both kernels stream 4-row tiles through the D-stage register pipeline of the
-// 4x4x4 MFMA GEMV (gemv4_core.h), with the NF4 codebook table in LDS.
+// Both kernels stream 4-row tiles through the register pipeline of the 4x4x4 MFMA GEMV
+// (gemv4_core.h), with the NF4 codebook table in LDS.
 #include "gemv4_core.h"
 
 namespace moe {
