@@ -26,6 +26,7 @@ import sys
 import time
 
 HBM_PEAK_GBPS = 8000.0
+MFMA_BF16_TFLOPS = 2500.0  # dense bf16 MFMA peak of MI355X
 METRIC = "decode tok/s Mixtral-8x7B-shape NF4 (bs=1); MoE-layer HBM GB/s vs peak"
 HERE = os.path.dirname(os.path.abspath(__file__))
 
@@ -47,6 +48,10 @@ def parse_args():
                         "scales the FETCH_SIZE / WRITE_SIZE counters) and exit")
     p.add_argument("--no-kernel-events", action="store_true",
                    help="do not bracket kernels with HIP events (headline timing only)")
+    p.add_argument("--mode", choices=["decode", "reconstruct"], default="decode",
+                   help="decode (default): the headline MoE-path benchmark; reconstruct: one "
+                        "Mixtral expert's NF4 -> bf16 reconstruction from HBM (K1) and from a "
+                        "pinned host staging slot (H2D + K1), one JSON line each")
     return p.parse_args()
 
 
@@ -92,6 +97,8 @@ def main() -> int:
 
     if args.copy_calibration > 0:
         return _copy_calibration(args.copy_calibration)
+    if args.mode == "reconstruct":
+        return _reconstruct(args)
 
     from moeinfra_amd import _lib, ops, synth
 
@@ -188,12 +195,21 @@ def main() -> int:
     gu_kernel = ("decode_gateup_kernel (routing + NF4 w1/w3 GEMV + SwiGLU)" if decode_form(T, K, E, H, F)
                  else "gateup_kernel / gemv4_kernel (NF4 w1/w3 + SwiGLU)")
     roofline = None
-    if gu_us:
+    if gu_us and decode_form(T, K, E, H, F):
         ach = gu_bytes / (gu_us * 1e-6) / 1e9
         roofline = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBPS,
                     "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBPS, 4),
                     "traffic": _traffic("gateup_nf4_decode_t%d" % T), "kernel": gu_kernel,
                     "bytes_per_launch": int(gu_bytes), "avg_launch_us": round(gu_us, 2)}
+    elif gu_us:
+        # Batches (prefill): the w1/w3 GEMMs, 2 x 2 * (T*k) * H * F flops per launch, on the
+        # bf16 MFMA roofline.
+        flops = 4.0 * T * K * H * F
+        ach = flops / (gu_us * 1e-6) / 1e12
+        roofline = {"bound": "mfma", "achieved": round(ach, 1), "peak": MFMA_BF16_TFLOPS,
+                    "unit": "TFLOP/s", "frac": round(ach / MFMA_BF16_TFLOPS, 4), "traffic": None,
+                    "kernel": gu_kernel, "flops_per_launch": flops, "avg_launch_us": round(gu_us, 2),
+                    "gbps_algorithmic": round(gu_bytes / (gu_us * 1e-6) / 1e9, 1)}
 
     # ------------------------------------------------------------------ CPU baseline
     cpu = None
@@ -288,6 +304,119 @@ def _copy_calibration(mib: int) -> int:
         dst.copy_(src)
     torch.cuda.synchronize()
     print(json.dumps({"copy_calibration_bytes": n, "copies": 10}), flush=True)
+    return 0
+
+
+def _reconstruct(args) -> int:
+    """Standalone reconstruction of one Mixtral-8x7B expert (w1, w3 [14336, 4096], w2
+    [4096, 14336]): (a) NF4 resident in HBM -> bf16 with the dequant kernel (451,411,968
+    algorithmic bytes per expert: 99,090,432 read + 352,321,536 written); (b) from a pinned
+    host staging slot (the reference's ReusablePinnedStagingPool hand-off): H2D of the
+    99,090,432 NF4 bytes on a side stream, then the dequant.  Synthetic bf16 N(0, 0.02)
+    weights quantised on the GPU."""
+    import torch
+
+    from moeinfra_amd import _lib, ops, synth
+
+    H, F = synth.MIXTRAL_HIDDEN, synth.MIXTRAL_FFN
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    lib = _lib.lib()
+    gen = torch.Generator(device=dev).manual_seed(args.seed)
+    mats = {}
+    for name, shape in (("w1", (F, H)), ("w3", (F, H)), ("w2", (H, F))):
+        w = (torch.randn(shape, generator=gen, device=dev) * 0.02).to(torch.bfloat16)
+        packed, absmax, code = ops.nf4_quantize(w)
+        mats[name] = (packed, absmax, code, shape, torch.empty(shape, dtype=torch.bfloat16, device=dev))
+        del w
+    # Measured ceilings for the same traffic shapes: a device copy (read + write of n bytes)
+    # and a fill (write only).
+    n = 256 << 20
+    src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+    dstc = torch.empty_like(src)
+    c0, c1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    for _ in range(3):
+        dstc.copy_(src)
+    c0.record()
+    for _ in range(10):
+        dstc.copy_(src)
+    c1.record()
+    torch.cuda.synchronize()
+    copy_gbps = 2 * n / (c0.elapsed_time(c1) * 1e-3 / 10) / 1e9
+    c0.record()
+    for _ in range(10):
+        dstc.fill_(3)
+    c1.record()
+    torch.cuda.synchronize()
+    fill_gbps = n / (c0.elapsed_time(c1) * 1e-3 / 10) / 1e9
+    del src, dstc
+    nf4_bytes = sum(m[0].numel() + m[1].numel() * 4 for m in mats.values())
+    alg = nf4_bytes + sum(m[4].numel() * 2 for m in mats.values())
+    stream = torch.cuda.current_stream(dev)
+
+    def dequant_all(src):
+        for name, (packed, absmax, code, shape, out) in mats.items():
+            p, a = src[name] if src else (packed, absmax)
+            rc = lib.moe_nf4_dequant_bf16(p.data_ptr(), a.data_ptr(), code.data_ptr(),
+                                          out.data_ptr(), out.numel(), 64, stream.cuda_stream)
+            _lib.check(rc, "moe_nf4_dequant_bf16")
+
+    reps = max(args.steps, 10)
+    for _ in range(3):
+        dequant_all(None)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(reps):
+        dequant_all(None)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / reps
+    gbps = alg / (us * 1e-6) / 1e9
+    print(json.dumps({
+        "metric": "NF4 expert reconstruction from HBM (K1 dequant, w1+w3+w2)", "value": round(gbps, 1),
+        "unit": "GB/s", "n_gpus": 1, "steps": reps, "higher_is_better": True, "dtype": "u8->bf16",
+        "data": "synthetic (bf16 N(0,0.02) weights NF4-quantised on the GPU)",
+        "config": {"workload": "one Mixtral-8x7B expert, w1/w3 [14336,4096] + w2 [4096,14336], NF4 blocksize 64"},
+        "us_per_expert": round(us, 2), "bytes_per_expert": alg,
+        "measured_ceilings_gbps": {"device_copy_read_plus_write": round(copy_gbps, 1),
+                                   "fill_write_only": round(fill_gbps, 1)},
+        "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "kernel": "nf4_dequant_kernel"}}), flush=True)
+
+    # (b) pinned host slot -> device (side stream) -> dequant
+    host = {n: (m[0].cpu().pin_memory(), m[1].cpu().pin_memory()) for n, m in mats.items()}
+    dst = {n: (torch.empty_like(m[0]), torch.empty_like(m[1])) for n, m in mats.items()}
+    side = torch.cuda.Stream(dev)
+    torch.cuda.synchronize()
+    t_h2d, t_all = [], []
+    for it in range(reps + 2):
+        a0 = torch.cuda.Event(enable_timing=True)
+        a1 = torch.cuda.Event(enable_timing=True)
+        a2 = torch.cuda.Event(enable_timing=True)
+        a0.record(side)
+        with torch.cuda.stream(side):
+            for n in mats:
+                dst[n][0].copy_(host[n][0], non_blocking=True)
+                dst[n][1].copy_(host[n][1], non_blocking=True)
+        a1.record(side)
+        stream.wait_stream(side)
+        dequant_all(dst)
+        a2.record(stream)
+        torch.cuda.synchronize()
+        if it >= 2:
+            t_h2d.append(a0.elapsed_time(a1) * 1e3)
+            t_all.append(a0.elapsed_time(a2) * 1e3)
+    t_h2d.sort()
+    t_all.sort()
+    h2d_us, all_us = t_h2d[len(t_h2d) // 2], t_all[len(t_all) // 2]
+    print(json.dumps({
+        "metric": "NF4 expert H2D staging (pinned slot -> HBM) + reconstruction", "value": round(nf4_bytes / (h2d_us * 1e-6) / 1e9, 2),
+        "unit": "GB/s (H2D)", "n_gpus": 1, "steps": reps, "higher_is_better": True, "dtype": "u8",
+        "data": "synthetic (bf16 N(0,0.02) weights NF4-quantised on the GPU, copied to pinned host memory)",
+        "config": {"workload": "one Mixtral-8x7B expert: 99,090,432 NF4 bytes host -> device on a side stream, then K1"},
+        "h2d_us_median": round(h2d_us, 1), "h2d_plus_dequant_us_median": round(all_us, 1),
+        "bytes_h2d": nf4_bytes}), flush=True)
     return 0
 
 

@@ -10,7 +10,10 @@ namespace moe {
 namespace {
 
 constexpr int kDequantThreads = 256;
-constexpr int kValsPerThread = 32;
+// A wave dequantises chunks of 2048 values: lane l handles the 8 values at 512*s + 8*l of
+// each quarter s, so each of its four 16-byte stores is part of one contiguous 1 KB store
+// of the wave (and each 4-byte load part of a contiguous 256-byte load).
+constexpr int kDequantChunk = 2048;
 
 __global__ void __launch_bounds__(kDequantThreads)
 nf4_dequant_kernel(const uint8_t *__restrict__ packed, const float *__restrict__ absmax,
@@ -20,32 +23,34 @@ nf4_dequant_kernel(const uint8_t *__restrict__ packed, const float *__restrict__
   if (threadIdx.x < 16) s_code[threadIdx.x] = code[threadIdx.x];
   __syncthreads();
 
-  const int64_t nvec = numel / kValsPerThread;
-  const int64_t stride = (int64_t)gridDim.x * kDequantThreads;
-  for (int64_t v = (int64_t)blockIdx.x * kDequantThreads + threadIdx.x; v < nvec; v += stride) {
-    const int64_t base = v * kValsPerThread;
-    const uint4 q = *reinterpret_cast<const uint4 *>(packed + base / 2);
-    // blocksize is a multiple of 32, so all 32 values share one absmax.
-    const float a = absmax[base / blocksize];
-    const uint32_t words[4] = {q.x, q.y, q.z, q.w};
-    uint32_t o[16];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t nchunk = numel / kDequantChunk;
+  const int64_t waves = (int64_t)gridDim.x * (kDequantThreads / kWave);
+  for (int64_t c = (int64_t)blockIdx.x * (kDequantThreads / kWave) + (threadIdx.x >> 6); c < nchunk;
+       c += waves) {
+    const int64_t base = c * kDequantChunk;
+    uint32_t q[4];
+    float a[4];
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
+    for (int s = 0; s < 4; ++s) {
+      const int64_t v0 = base + 512 * s + 8 * lane;
+      q[s] = *reinterpret_cast<const uint32_t *>(packed + v0 / 2);
+      a[s] = absmax[v0 / blocksize];  // blocksize is a multiple of 32: one block per 8 values
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      uint32_t o[4];
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
-        const uint32_t byte = (words[w] >> (8 * b)) & 0xffu;
-        const float hi = s_code[byte >> 4] * a;   // value 2j   (high nibble)
-        const float lo = s_code[byte & 15u] * a;  // value 2j+1 (low nibble)
-        o[w * 4 + b] = pack_bf16x2(hi, lo);
+        const uint32_t byte = (q[s] >> (8 * b)) & 0xffu;
+        o[b] = pack_bf16x2(s_code[byte >> 4] * a[s], s_code[byte & 15u] * a[s]);
       }
+      *reinterpret_cast<uint4 *>(out + base + 512 * s + 8 * lane) = make_uint4(o[0], o[1], o[2], o[3]);
     }
-    uint4 *dst = reinterpret_cast<uint4 *>(out + base);
-#pragma unroll
-    for (int s = 0; s < 4; ++s) dst[s] = make_uint4(o[4 * s], o[4 * s + 1], o[4 * s + 2], o[4 * s + 3]);
   }
-  // Tail: fewer than 32 values left (numel is even); one thread finishes them.
-  if (blockIdx.x == 0 && threadIdx.x == 0) {
-    for (int64_t i = nvec * kValsPerThread; i < numel; i += 2) {
+  // Tail: fewer than one chunk left (numel is even), two values per thread of workgroup 0.
+  if (blockIdx.x == 0) {
+    for (int64_t i = nchunk * kDequantChunk + 2 * threadIdx.x; i < numel; i += 2 * kDequantThreads) {
       const uint32_t byte = packed[i / 2];
       out[i] = f32_to_bf16(s_code[byte >> 4] * absmax[i / blocksize]);
       out[i + 1] = f32_to_bf16(s_code[byte & 15u] * absmax[(i + 1) / blocksize]);
@@ -100,9 +105,9 @@ extern "C" int moe_nf4_dequant_bf16(const void *packed, const void *absmax, cons
   MOE_REQUIRE(packed && absmax && code16 && out_bf16, "null device pointer");
   MOE_REQUIRE(((uintptr_t)packed % 16) == 0 && ((uintptr_t)out_bf16 % 16) == 0,
               "packed and out must be 16-byte aligned");
-  const int64_t nvec = numel / moe::kValsPerThread;
-  int64_t blocks = (nvec + moe::kDequantThreads - 1) / moe::kDequantThreads;
-  const int64_t cap = (int64_t)moe::device_cu_count() * 32;
+  const int64_t nchunk = numel / moe::kDequantChunk;
+  int64_t blocks = (nchunk + (moe::kDequantThreads / moe::kWave) - 1) / (moe::kDequantThreads / moe::kWave);
+  const int64_t cap = (int64_t)moe::device_cu_count() * 8;
   if (blocks > cap) blocks = cap;
   if (blocks < 1) blocks = 1;
   hipLaunchKernelGGL(moe::nf4_dequant_kernel, dim3((unsigned)blocks), dim3(moe::kDequantThreads),
