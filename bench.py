@@ -192,8 +192,12 @@ def main() -> int:
     layer_us = ms_per_step * 1e3 / L
     layer_gbps = ly_bytes / (layer_us * 1e-6) / 1e9
 
-    gu_kernel = ("decode_gateup_kernel (routing + NF4 w1/w3 GEMV + SwiGLU)" if decode_form(T, K, E, H, F)
-                 else "gateup_kernel / gemv4_kernel (NF4 w1/w3 + SwiGLU)")
+    if decode_form(T, K, E, H, F):
+        gu_kernel = "decode_gateup_kernel (routing + NF4 w1/w3 GEMV + SwiGLU)"
+    elif T * K >= 32 * min(T * K, E):  # the library's choice of the batched GEMM
+        gu_kernel = "expert_gemm_kernel<gate/up> (LDS-staged NF4 GEMM + SwiGLU)"
+    else:
+        gu_kernel = "gateup_kernel / gemv4_kernel (NF4 w1/w3 + SwiGLU)"
     roofline = None
     if gu_us and decode_form(T, K, E, H, F):
         ach = gu_bytes / (gu_us * 1e-6) / 1e9

@@ -437,6 +437,12 @@ int choose_nsplit(int64_t T, int32_t k, int32_t E, int32_t H) {
 }
 
 bool gemv4_supported(int64_t max_tokens_per_expert, int32_t H, int32_t F);
+bool expert_gemm_supported(int32_t H, int32_t F);
+int launch_expert_gemm(const void *tab, const void *x, int32_t H, int32_t F, const void *route,
+                       void *h_ws, void *ypart, int phases, hipStream_t stream);
+// Average routed rows per expert from which a layer uses the batched GEMM.
+constexpr int64_t kGemmMinRowsPerExpert = 32;
+
 int launch_gemv4(const void *tab, const void *x, int32_t H, int32_t F, const void *route,
                  void *h_ws, void *ypart, int phases, int64_t active_max, int64_t rows_total,
                  const void *fused_combine, hipStream_t stream);
@@ -480,6 +486,11 @@ int launch_expert_ffn(const moe_nf4_expert_t *experts, int32_t E, const void *x,
   if (nsplit == 1 && gemv4_supported(max_tokens_per_expert, H, F))
     return launch_gemv4(&tab, x, H, F, &rt, h_ws, ypart, phases, active_max, rows_total, fused,
                         stream);
+  // Many tokens per expert on average: the LDS-staged GEMM streams each weight tile once per
+  // 128 tokens (the per-tile kernels below re-stream it every 16 or 32 tokens).
+  if (nsplit == 1 && fused == nullptr && rows_total >= kGemmMinRowsPerExpert * active_max &&
+      expert_gemm_supported(H, F))
+    return launch_expert_gemm(&tab, x, H, F, &rt, h_ws, ypart, phases, stream);
   MOE_REQUIRE(fused == nullptr, "a fused combine needs the small-batch GEMV path");
   const int wpt_gu = 1;  // a wave streams a whole w1/w3 row tile
   const int wpt_dn = 4;  // four waves split each w2 row tile's K range

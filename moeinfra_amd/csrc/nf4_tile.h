@@ -63,7 +63,8 @@ __device__ __forceinline__ void lookup8(const uint32_t *tbl, uint2 q, uint32_t l
 }
 
 // Loads the work item's codebooks and (re)builds the lookup table when they differ from
-// the resident ones.  Must be called by every thread of the workgroup; acts as a barrier.
+// the resident ones.  Must be called by all NT threads of the workgroup; acts as a barrier.
+template <int NT = kFfnThreads>
 __device__ __forceinline__ void ensure_table(uint32_t *tbl, uint32_t *s_raw, float *s_code,
                                              const float *code_lo, const float *code_hi,
                                              bool &built) {
@@ -80,7 +81,7 @@ __device__ __forceinline__ void ensure_table(uint32_t *tbl, uint32_t *s_raw, flo
       s_code[tid] = __builtin_bit_cast(float, mine);
     }
     __syncthreads();
-    for (int i = tid; i < kTableWords; i += kFfnThreads) {
+    for (int i = tid; i < kTableWords; i += NT) {
       const int v = i >> 6;                   // packed byte value
       const int half = (i & 32) ? 16 : 0;     // replicas 32-63 use the second codebook
       tbl[i] = pack_bf16x2(s_code[half + (v >> 4)], s_code[half + (v & 15)]);

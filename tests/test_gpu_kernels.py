@@ -229,3 +229,22 @@ def test_decode_single_token_long_ffn(cuda_device):
     np.testing.assert_array_equal(idx.cpu().numpy()[ok], idx_o[ok])
     err = orc.rel_l2(orc.bf16_to_f32(bits(out)[ok]), orc.bf16_to_f32(want[ok]))
     assert err <= 1e-2, err
+
+
+# ------------------------------------------------------------------------------ batched GEMM
+# From 32 routed rows per expert on average the layer runs the LDS-staged expert GEMM
+# (expert_gemm.hip): partial 128-token tiles, uniform and skewed routing, several tiles
+# per expert.
+@pytest.mark.parametrize("H,F,E,T,seed,skew", [
+    (512, 1024, 8, 160, 31, False),
+    (256, 512, 8, 300, 32, True),
+    (1024, 3584, 8, 512, 33, False),
+    (1024, 3584, 8, 700, 34, True),
+])
+def test_layer_batched_gemm(cuda_device, H, F, E, T, seed, skew):
+    want, i_want, got, i_got, lg = _layer_case(cuda_device, H, F, E, T, seed, skew)
+    tie = near_tie_rows(lg)
+    np.testing.assert_array_equal(i_got[~tie], i_want[~tie])
+    ok = ~tie
+    err = orc.rel_l2(orc.bf16_to_f32(got[ok]), orc.bf16_to_f32(want[ok]))
+    assert err <= 1e-2, err
