@@ -18,6 +18,8 @@ constexpr int kWave = 64;
 // ---------------------------------------------------------------- vector types
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
+// 16 bytes as a native vector (unlike HIP's uint4 struct, copies of it stay in registers).
+typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4;
 
 // ---------------------------------------------------------------- bf16 helpers
 // Round-to-nearest-even float -> bf16 bits (v_cvt_pk_bf16_f32 on gfx950).

@@ -12,8 +12,8 @@
 // 16-row tiles of w2, 128 rows apart), for all 128 tokens of the tile (eight 16-token
 // MFMA tiles).  The K loop runs over 64-value NF4 blocks:
 //  * the token tile's 128 x 64 activations are loaded cooperatively (one 16-byte load per
-//    thread and half block), two blocks ahead, and staged in LDS (double buffer, rows padded
-//    to 144 bytes so that the 16-byte reads of 8 lanes hit distinct banks);
+//    thread and half block), two blocks ahead, and staged in LDS (double buffer, 128-byte
+//    rows whose 16-byte chunks are XOR-swizzled by the row, see a_swizzle);
 //  * each lane's 8 packed bytes per stream and block come from a register ring 8 blocks
 //    deep (the HBM latency), and are turned into bf16 operands by the 64 KB LDS table;
 //  * per 16-token tile and stream, two MFMAs (K = 32 each) produce the block's partial
@@ -30,9 +30,26 @@ constexpr int kGemmWaves = 8;
 constexpr int kGemmThreads = kGemmWaves * kWave;
 constexpr int kGemmM = 128;             // tokens per item
 constexpr int kGemmMT = kGemmM / 16;    // 16-token MFMA tiles per item
-constexpr int kARowHalves = 72;         // LDS row stride of the activation tile, in bf16
+constexpr int kARowHalves = 64;         // LDS row stride of the activation tile, in bf16
 constexpr int kGemmBDepth = 8;          // weight blocks in flight per wave
-constexpr int kGemmADepth = 2;          // activation blocks in flight per thread
+constexpr int kGemmADepth = 4;          // activation blocks in flight per thread
+// The block loop is unrolled by kGemmBDepth from block 0, so b % kGemmADepth and b % 2 are
+// those of the unrolled index: the activation registers and LDS buffers are then indexed
+// statically (a dynamic index would make the compiler move the register array to LDS).
+// Loads complete in issue order (vmcnt), so the wait for the activations of block b + 1
+// also waits for every weight load issued before them: kGemmADepth - 1 blocks is the
+// latency the loads of both operands get.
+static_assert(kGemmBDepth % kGemmADepth == 0 && kGemmADepth % 2 == 0,
+              "buffer indices must follow the unrolled index");
+
+// Position of 16-byte chunk c (of 8) of activation-tile row r: c ^ a_swizzle(r & 15).
+// gfx950 serves a 64-lane ds_read_b128 16 lanes per cycle, in the lane groups
+// {0-3, 12-15, 20-27} and {4-11, 16-19, 28-31} (and the same + 32), over 64 four-byte
+// banks.  The MFMA operand read has lane (n, g) fetch chunk 2g (then 2g + 1) of row n; with
+// this swizzle the 16 lanes of every group cover 16 distinct (row parity, position) pairs,
+// i.e. all 64 banks once.  The cooperative stores (8 lanes per cycle, one row) stay
+// conflict-free for any swizzle.
+__device__ __forceinline__ int a_swizzle(int r) { return ((r >> 1) & 3) | (((r + 4) >> 1) & 4); }
 
 template <bool GATEUP>
 __global__ void __launch_bounds__(kGemmThreads, 1)
@@ -42,6 +59,8 @@ expert_gemm_kernel(const ExpertTable tab, const uint16_t *__restrict__ act, int 
   __shared__ __attribute__((aligned(16))) uint16_t s_a[2][kGemmM * kARowHalves];
   __shared__ uint32_t s_raw[32];
   __shared__ float s_code[32];
+  __shared__ int s_ex[MOE_MAX_EXPERTS][4];  // per active expert: id, rows, row offset, first item
+  __shared__ int s_nitems;
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
@@ -59,33 +78,76 @@ expert_gemm_kernel(const ExpertTable tab, const uint16_t *__restrict__ act, int 
   bool built = false;
 
   // Items: for each active expert (ascending), its token tiles x weight tiles, the token
-  // tile fastest so that concurrent items share weight tiles in L2.
-  int n_items = 0;
+  // tile fastest so that concurrent items share weight tiles in L2.  Wave 0 stages the
+  // active experts' ids, row counts, row offsets and first item indices in LDS once, so
+  // that decoding an item is one LDS read and a ballot instead of a chain of global loads.
+  static_assert(MOE_MAX_EXPERTS <= kWave, "one lane per active expert");
   const int n_active = rt.active[0];
-  for (int a = 0; a < n_active; ++a) {
-    const int cnt = rt.counts[rt.active[1 + a]];
-    n_items += ((cnt + kGemmM - 1) / kGemmM) * n_tiles;
+  if (n_active == 0) return;  // uniform over the grid, before any barrier
+  if (wave == 0) {
+    int e = 0, cnt = 0, items = 0;
+    if (lane < n_active) {
+      e = rt.active[1 + lane];
+      cnt = rt.counts[e];
+      items = ((cnt + kGemmM - 1) / kGemmM) * n_tiles;
+    }
+    int incl = items;  // inclusive prefix sum over the lanes
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+      const int v = __shfl_up(incl, o);
+      if (lane >= o) incl += v;
+    }
+    if (lane < n_active) {
+      s_ex[lane][0] = e;
+      s_ex[lane][1] = cnt;
+      s_ex[lane][2] = rt.offsets[e];
+      s_ex[lane][3] = incl - items;
+    }
+    if (lane == kWave - 1) s_nitems = incl;
   }
+  // Codebooks: when every active expert holds the codebooks of the first one (the usual
+  // case: one NF4 codebook for all tensors), the table is built once for the launch;
+  // otherwise it is checked per item.
+  int cb_diff = 0;
+  {
+    const int e0 = rt.active[1];
+    const float *lo0 = (const float *)(GATEUP ? tab.e[e0].w1_code : tab.e[e0].w2_code);
+    const float *hi0 = (const float *)(GATEUP ? tab.e[e0].w3_code : tab.e[e0].w2_code);
+    for (int i = tid; i < n_active * 32; i += kGemmThreads) {
+      const int e = rt.active[1 + (i >> 5)], j = i & 15;
+      const float *lo = (const float *)(GATEUP ? tab.e[e].w1_code : tab.e[e].w2_code);
+      const float *hi = (const float *)(GATEUP ? tab.e[e].w3_code : tab.e[e].w2_code);
+      const float *x = (i & 16) ? hi : lo;
+      const float *x0 = (i & 16) ? hi0 : lo0;
+      cb_diff |= __builtin_bit_cast(uint32_t, x[j]) != __builtin_bit_cast(uint32_t, x0[j]);
+    }
+  }
+  const bool per_item_table = __syncthreads_or(cb_diff) != 0;  // also publishes s_ex
+  if (!per_item_table) {
+    const moe_nf4_expert_t &ex0 = tab.e[s_ex[0][0]];
+    if (GATEUP)
+      ensure_table<kGemmThreads>(s_tbl, s_raw, s_code, (const float *)ex0.w1_code, (const float *)ex0.w3_code, built);
+    else
+      ensure_table<kGemmThreads>(s_tbl, s_raw, s_code, (const float *)ex0.w2_code, (const float *)ex0.w2_code, built);
+  }
+  const int n_items = s_nitems;
 
   for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
-    int rem = item, a = 0, e = 0, cnt = 0, mtiles = 0;
-    for (;;) {  // at most n_active steps
-      e = rt.active[1 + a];
-      cnt = rt.counts[e];
-      mtiles = (cnt + kGemmM - 1) / kGemmM;
-      if (rem < mtiles * n_tiles) break;
-      rem -= mtiles * n_tiles;
-      ++a;
-    }
+    // The item's expert: the last active expert whose first item is <= item.
+    const int a = __popcll(__ballot(lane < n_active && s_ex[lane < n_active ? lane : 0][3] <= item)) - 1;
+    const int e = s_ex[a][0], cnt = s_ex[a][1], off = s_ex[a][2];
+    const int rem = item - s_ex[a][3];
+    const int mtiles = (cnt + kGemmM - 1) / kGemmM;
     const int nt = rem / mtiles;
     const int mt_i = rem - nt * mtiles;
-    const int off = rt.offsets[e];
     const int m_base = mt_i * kGemmM;
     const moe_nf4_expert_t &ex = tab.e[e];
-    if (GATEUP)
-      ensure_table<kGemmThreads>(s_tbl, s_raw, s_code, (const float *)ex.w1_code, (const float *)ex.w3_code, built);
-    else
-      ensure_table<kGemmThreads>(s_tbl, s_raw, s_code, (const float *)ex.w2_code, (const float *)ex.w2_code, built);
+    if (per_item_table) {
+      if (GATEUP)
+        ensure_table<kGemmThreads>(s_tbl, s_raw, s_code, (const float *)ex.w1_code, (const float *)ex.w3_code, built);
+      else
+        ensure_table<kGemmThreads>(s_tbl, s_raw, s_code, (const float *)ex.w2_code, (const float *)ex.w2_code, built);
+    }
 
     // Weight streams of this lane: row (row0 + n) of each stream.
     const int row0 = nt * WROWS + 16 * wave;
@@ -117,27 +179,36 @@ expert_gemm_kernel(const ExpertTable tab, const uint16_t *__restrict__ act, int 
       asrc[h2] = act + src_row * K + 8 * ac;
     }
 
-    uint4 abuf[kGemmADepth][2];
-    auto load_a = [&](uint4 (&dst)[2], int b) {
+    // Rows ar0 and ar0 + 64 share the swizzle (64 is a multiple of 16).
+    const int a_st = ar0 * kARowHalves + 8 * (ac ^ a_swizzle(ar0));
+    u32x4 abuf[kGemmADepth][2];
+    auto load_a = [&](u32x4 (&dst)[2], int b) {
       const int bb = b < NB ? b : NB - 1;  // past the end: the last block again (unused)
 #pragma unroll
       for (int h2 = 0; h2 < 2; ++h2)
-        dst[h2] = *reinterpret_cast<const uint4 *>(asrc[h2] + (size_t)bb * 64);
+        dst[h2] = *reinterpret_cast<const u32x4 *>(asrc[h2] + (size_t)bb * 64);
     };
-    auto store_a = [&](const uint4 (&src)[2], int buf) {
+    auto store_a = [&](const u32x4 (&src)[2], int buf) {
 #pragma unroll
       for (int h2 = 0; h2 < 2; ++h2)
-        *reinterpret_cast<uint4 *>(&s_a[buf][(ar0 + 64 * h2) * kARowHalves + 8 * ac]) = src[h2];
+        *reinterpret_cast<u32x4 *>(&s_a[buf][a_st + 64 * h2 * kARowHalves]) = src[h2];
     };
+    // Operand reads of lane (n, g): chunks 2g and 2g + 1 of row n (+ 16 m).
+    const int a_rd0 = n * kARowHalves + 8 * ((2 * g) ^ a_swizzle(n));
+    const int a_rd1 = n * kARowHalves + 8 * ((2 * g + 1) ^ a_swizzle(n));
     uint2 bq[kGemmBDepth][2];
-    float bs[kGemmBDepth][2];
     auto load_b = [&](int slot, int b) {
       const int bb = b < NB ? b : NB - 1;
 #pragma unroll
-      for (int p = 0; p < 2; ++p) {
-        bq[slot][p] = *reinterpret_cast<const uint2 *>(wq[p] + (size_t)bb * 32);
-        bs[slot][p] = wa[p][bb];
-      }
+      for (int p = 0; p < 2; ++p) bq[slot][p] = *reinterpret_cast<const uint2 *>(wq[p] + (size_t)bb * 32);
+    };
+    // Absmax of blocks 4j..4j+3 as one 16-byte load per stream (rows hold NB % 4 == 0
+    // values), two groups of four in registers: group j lives in slot j % 2.
+    f32x4 bs4[2][2];
+    auto load_s = [&](int slot, int b4) {
+      const int bb = b4 < NB ? b4 : NB - 4;
+#pragma unroll
+      for (int p = 0; p < 2; ++p) bs4[slot][p] = *reinterpret_cast<const f32x4 *>(wa[p] + bb);
     };
 
     f32x4 acc[2][kGemmMT];
@@ -146,11 +217,14 @@ expert_gemm_kernel(const ExpertTable tab, const uint16_t *__restrict__ act, int 
 #pragma unroll
       for (int m = 0; m < kGemmMT; ++m) acc[p][m] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    // Prologue: activation block 0 to LDS, block 1 in registers, weight blocks 0..D-2.
-    load_a(abuf[0], 0);
-    load_a(abuf[1], 1);
+    // Prologue: activation block 0 to LDS, blocks 1..DA-1 in registers, weight blocks
+    // 0..DB-2.
+#pragma unroll
+    for (int d = 0; d < kGemmADepth; ++d) load_a(abuf[d], d);
 #pragma unroll
     for (int d = 0; d < kGemmBDepth - 1; ++d) load_b(d, d);
+    load_s(0, 0);
+    load_s(1, 4);
     store_a(abuf[0], 0);
     __syncthreads();
 
@@ -160,8 +234,11 @@ expert_gemm_kernel(const ExpertTable tab, const uint16_t *__restrict__ act, int 
         const int b = b0 + d;
         if (b < NB) {
           load_b((d + kGemmBDepth - 1) % kGemmBDepth, b + kGemmBDepth - 1);
-          load_a(abuf[b & 1], b + 2);  // block b's registers were stored at block b-1
-          const uint16_t *sa = s_a[b & 1];
+          // Once the blocks of a group are done (block b = 4j + 4 starts), group j + 2
+          // replaces it: four blocks ahead of its first use.
+          if (d % 4 == 0 && b >= 4) load_s((d / 4 + 1) % 2, b + 4);
+          load_a(abuf[d % kGemmADepth], b + kGemmADepth);  // block b's were stored at b-1
+          const uint16_t *sa = s_a[d & 1];
           bf16x8 w0[2], w1[2];
 #pragma unroll
           for (int p = 0; p < 2; ++p) {
@@ -172,14 +249,13 @@ expert_gemm_kernel(const ExpertTable tab, const uint16_t *__restrict__ act, int 
           }
 #pragma unroll
           for (int m = 0; m < kGemmMT; ++m) {
-            const uint4 *pa = reinterpret_cast<const uint4 *>(sa + (m * 16 + n) * kARowHalves + 16 * g);
-            const bf16x8 a0 = as_bf16x8(pa[0]);
-            const bf16x8 a1 = as_bf16x8(pa[1]);
+            const bf16x8 a0 = as_bf16x8(*reinterpret_cast<const u32x4 *>(sa + m * 16 * kARowHalves + a_rd0));
+            const bf16x8 a1 = as_bf16x8(*reinterpret_cast<const u32x4 *>(sa + m * 16 * kARowHalves + a_rd1));
 #pragma unroll
-            for (int p = 0; p < 2; ++p) scale_acc(acc[p][m], mfma_block(a0, w0[p], a1, w1[p]), bs[d][p]);
+            for (int p = 0; p < 2; ++p) scale_acc(acc[p][m], mfma_block(a0, w0[p], a1, w1[p]), bs4[(d / 4) % 2][p][d % 4]);
           }
-          // Block b+1's activations (loaded at block b-1) to the other buffer.
-          store_a(abuf[(b + 1) & 1], (b + 1) & 1);
+          // Block b+1's activations (loaded at block b+1-DA) to the other buffer.
+          store_a(abuf[(d + 1) % kGemmADepth], (d + 1) & 1);
           __syncthreads();
         }
       }
@@ -208,8 +284,9 @@ expert_gemm_kernel(const ExpertTable tab, const uint16_t *__restrict__ act, int 
 }  // namespace
 
 // The batched form of K4: gate/up (phases bit 0) and/or down (bit 1) with the LDS-staged
-// GEMM.  Needs H % 256 == 0 and F % 128 == 0; writes ypart as one split.
-bool expert_gemm_supported(int32_t H, int32_t F) { return H % 256 == 0 && F % 128 == 0; }
+// GEMM.  Needs H % 256 == 0 (down tiles of 256 rows) and F % 256 == 0 (gate/up tiles of 128
+// rows; absmax rows of a multiple of 4 blocks); writes ypart as one split.
+bool expert_gemm_supported(int32_t H, int32_t F) { return H % 256 == 0 && F % 256 == 0; }
 
 int launch_expert_gemm(const void *tab_v, const void *x, int32_t H, int32_t F, const void *route_v,
                        void *h_ws, void *ypart, int phases, hipStream_t stream) {
