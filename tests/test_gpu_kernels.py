@@ -248,3 +248,18 @@ def test_layer_batched_gemm(cuda_device, H, F, E, T, seed, skew):
     ok = ~tie
     err = orc.rel_l2(orc.bf16_to_f32(got[ok]), orc.bf16_to_f32(want[ok]))
     assert err <= 1e-2, err
+
+
+# Batched layers whose experts do not share one codebook: the GEMM rebuilds its lookup
+# table per work item.  Expert 0 keeps the NF4 codebook, so the first active expert's
+# table is not the one of every item.
+@pytest.mark.parametrize("H,F,T", [(512, 1024, 300), (256, 512, 160)])
+def test_layer_batched_gemm_mixed_codebooks(cuda_device, H, F, T):
+    codes = {e: (orc.NF4_CODE * np.float32(0.75 + 0.05 * e)).astype(np.float32)
+             for e in (1, 4, 6)}
+    want, i_want, got, i_got, lg = _layer_case(cuda_device, H, F, 8, T, 40 + T, codes=codes)
+    tie = near_tie_rows(lg)
+    np.testing.assert_array_equal(i_got[~tie], i_want[~tie])
+    ok = ~tie
+    err = orc.rel_l2(orc.bf16_to_f32(got[ok]), orc.bf16_to_f32(want[ok]))
+    assert err <= 1e-2, err
