@@ -446,6 +446,10 @@ constexpr int64_t kGemmMinRowsPerExpert = 32;
 int launch_gemv4(const void *tab, const void *x, int32_t H, int32_t F, const void *route,
                  void *h_ws, void *ypart, int phases, int64_t active_max, int64_t rows_total,
                  const void *fused_combine, hipStream_t stream);
+bool skinny_supported(int32_t H, int32_t F);
+int launch_skinny(const void *tab, const void *x, int64_t T, int64_t rows_total, int32_t H,
+                  int32_t F, const void *route, void *h_ws, void *ypart, int phases,
+                  hipStream_t stream);
 
 // phases: bit 0 = gate/up (x -> h), bit 1 = down (h -> ypart).  Up to 4 tokens per expert
 // use the 4x4x4 MFMA GEMV (expert_gemv4.hip); more use the 16x16x32 tiles below.
@@ -491,6 +495,11 @@ int launch_expert_ffn(const moe_nf4_expert_t *experts, int32_t E, const void *x,
   if (nsplit == 1 && fused == nullptr && rows_total >= kGemmMinRowsPerExpert * active_max &&
       expert_gemm_supported(H, F))
     return launch_expert_gemm(&tab, x, H, F, &rt, h_ws, ypart, phases, stream);
+  // Fewer: the mid-batch kernels stream each weight tile once per 32 tokens of its expert
+  // at the HBM rate (32x32x16 MFMA, 16-byte weight loads, activations from L2).
+  if (nsplit == 1 && fused == nullptr && skinny_supported(H, F) && rows_total <= 2048 &&
+      T * (int64_t)H * 2 < ((int64_t)1 << 31) && rows_total * (int64_t)F * 2 < ((int64_t)1 << 31))
+    return launch_skinny(&tab, x, T, rows_total, H, F, &rt, h_ws, ypart, phases, stream);
   MOE_REQUIRE(fused == nullptr, "a fused combine needs the small-batch GEMV path");
   const int wpt_gu = 1;  // a wave streams a whole w1/w3 row tile
   const int wpt_dn = 4;  // four waves split each w2 row tile's K range

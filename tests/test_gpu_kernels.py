@@ -263,3 +263,78 @@ def test_layer_batched_gemm_mixed_codebooks(cuda_device, H, F, T):
     ok = ~tie
     err = orc.rel_l2(orc.bf16_to_f32(got[ok]), orc.bf16_to_f32(want[ok]))
     assert err <= 1e-2, err
+
+
+# ------------------------------------------------------------------------------ mid-size batches
+# Between the decode form (T <= 4) and the batched GEMM (>= 32 routed rows per expert on
+# average) the layer runs the mid-batch kernels (expert_skinny.hip): 32-token chunks per
+# expert (a hot expert under skewed routing takes several), uniform and skewed routing,
+# shapes whose K does not split evenly over the eight waves (F = 768: 12 blocks).
+@pytest.mark.parametrize("H,F,E,T,seed,skew", [
+    (512, 1024, 8, 6, 51, False),
+    (512, 768, 8, 9, 52, True),
+    (1024, 2048, 8, 64, 53, False),
+    (512, 1024, 8, 100, 54, True),
+    (1024, 3584, 8, 40, 55, True),
+])
+def test_layer_mid_batch(cuda_device, H, F, E, T, seed, skew):
+    want, i_want, got, i_got, lg = _layer_case(cuda_device, H, F, E, T, seed, skew)
+    tie = near_tie_rows(lg)
+    np.testing.assert_array_equal(i_got[~tie], i_want[~tie])
+    ok = ~tie
+    err = orc.rel_l2(orc.bf16_to_f32(got[ok]), orc.bf16_to_f32(want[ok]))
+    assert err <= 1e-2, err
+
+
+def test_layer_mid_batch_mixed_codebooks(cuda_device):
+    """Mid-batch layer whose experts do not share one codebook: the kernels rebuild the
+    lookup table at the work items whose codebooks differ."""
+    codes = {e: (orc.NF4_CODE * np.float32(0.75 + 0.05 * e)).astype(np.float32)
+             for e in (1, 4, 6)}
+    want, i_want, got, i_got, lg = _layer_case(cuda_device, 512, 1024, 8, 24, 56, codes=codes)
+    tie = near_tie_rows(lg)
+    np.testing.assert_array_equal(i_got[~tie], i_want[~tie])
+    ok = ~tie
+    err = orc.rel_l2(orc.bf16_to_f32(got[ok]), orc.bf16_to_f32(want[ok]))
+    assert err <= 1e-2, err
+
+
+@pytest.mark.parametrize("T,skew", [(16, False), (32, True)])
+def test_layer_mid_batch_mixtral(cuda_device, T, skew):
+    """Full Mixtral-8x7B expert shapes (hidden 4096, FFN 14336) at decode batches 16 and 32:
+    weights drawn and quantised on the GPU, the oracle dequantises the routed experts."""
+    from moeinfra_amd import ops, synth
+    from moeinfra_amd._lib import MoeNf4Expert
+
+    H, F, E = 4096, 14336, 8
+    g = torch.Generator(device=cuda_device).manual_seed(600 + T)
+    keep = []
+    for e in range(E):
+        st = {}
+        for name, shape in (("w1", (F, H)), ("w3", (F, H)), ("w2", (H, F))):
+            w = (torch.randn(shape, generator=g, device=cuda_device) * 0.02).to(torch.bfloat16)
+            st[name] = ops.nf4_quantize(w)
+            del w
+        keep.append(st)
+    gate = (torch.randn((E, H), generator=g, device=cuda_device) * 0.02).to(torch.bfloat16)
+    table = ops.expert_table([MoeNf4Expert(*(t.data_ptr() for n in ("w1", "w3", "w2")
+                                             for t in st[n])) for st in keep])
+    x = torch.randn((T, H), generator=g, device=cuda_device).to(torch.bfloat16)
+    bias = synth.zipf_bias(E, T).to(cuda_device) if skew else None
+    out, _, w, idx = ops.layer_forward(table, E, gate, x, 2, F, bias=bias)
+    torch.cuda.synchronize()
+    cache = {}
+
+    def expert_fn(e, rows):
+        if e not in cache:
+            st = {n: (keep[e][n][0].cpu().numpy().reshape(-1), keep[e][n][1].cpu().numpy())
+                  for n in ("w1", "w3", "w2")}
+            cache[e] = orc.dequant_expert(st, H, F, threads=8)
+        return orc.swiglu(rows, *cache[e])
+
+    b = None if bias is None else bias.cpu().numpy()
+    want, (lg_o, w_o, idx_o) = orc.moe_layer(bits(x), bits(gate), expert_fn, bias=b)
+    ok = ~near_tie_rows(lg_o, bias=b)
+    np.testing.assert_array_equal(idx.cpu().numpy()[ok], idx_o[ok])
+    err = orc.rel_l2(orc.bf16_to_f32(bits(out)[ok]), orc.bf16_to_f32(want[ok]))
+    assert err <= 1e-2, err
