@@ -181,6 +181,39 @@ int moe_layer_forward_nf4_profiled(const moe_nf4_expert_t *experts, int32_t E,
                                    void *weights_f32, void *idx_i64, void *workspace,
                                    int64_t workspace_bytes, void *const *events, void *stream);
 
+/* ---------------------------------------------------------------- decoder (end-to-end)
+ * The dense parts of a Mixtral decoder layer around the MoE block, which the reference
+ * runs as Hugging Face modules (engine/engine.py:211-314 builds MixtralRMSNorm,
+ * MixtralRotaryEmbedding and the eager attention of MixtralDecoderLayer;
+ * engine/decoder_layer.py:37-41 swaps in the MoE block).  bf16 tensors, fp32
+ * accumulation, bf16 rounding after each elementwise op as on bf16 torch tensors.
+ *
+ * r = residual_in ? bf16(x + residual_in) : x (written to residual_out when given);
+ * out = bf16(weight * bf16(r * rsqrt(mean(r^2) + eps))), per row of [T, H]. */
+int moe_add_rmsnorm_bf16(const void *x, const void *residual_in, const void *weight, float eps,
+                         int64_t T, int32_t H, void *residual_out, void *out, void *stream);
+
+/* Rotary embedding (rotate-half convention, cos/sin of pos * inv_freq rounded to bf16) of
+ * the q and k heads of qkv [T, (n_q + 2 n_kv) * head_dim] at positions *pos0 + t (pos0 a
+ * device int32); q to q_out [T, n_q, head_dim], k and v to the caches
+ * [n_kv, max_seq, head_dim] at those positions. */
+int moe_rope_kv_bf16(const void *qkv, int64_t T, int32_t n_q_heads, int32_t n_kv_heads,
+                     int32_t head_dim, const void *inv_freq_f32, const void *pos0_i32,
+                     int64_t max_seq, void *q_out, void *k_cache, void *v_cache, void *stream);
+
+/* Grouped-query causal attention of q [T, n_q, head_dim] (query t at position *pos0 + t)
+ * against the caches: bf16(bf16(q.k) * scaling) scores, fp32 softmax rounded to bf16,
+ * fp32-accumulated sum of the probabilities times v; out [T, n_q * head_dim]. */
+int moe_attention_bf16(const void *q, const void *k_cache, const void *v_cache, int64_t T,
+                       int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
+                       const void *pos0_i32, int64_t max_seq, float scaling, void *out,
+                       void *stream);
+
+/* y[T, N] = bf16(x[T, K] W[N, K]^T) with fp32 accumulation, 1 <= T <= 4: the decode-time
+ * q/k/v/o projections and lm_head (nn.Linear without bias on bf16 tensors). */
+int moe_gemv_bf16(const void *weight, const void *x, int64_t T, int32_t N, int32_t K, void *y,
+                  void *stream);
+
 #ifdef __cplusplus
 }
 #endif

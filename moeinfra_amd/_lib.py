@@ -60,6 +60,13 @@ SIGNATURES = {
     "moe_layer_forward_nf4_profiled": ([ctypes.POINTER(MoeNf4Expert), _i32, _vp, _vp, _vp, _i64,
                                         _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _i64,
                                         ctypes.POINTER(_vp), _vp], ctypes.c_int),
+    "moe_add_rmsnorm_bf16": ([_vp, _vp, _vp, ctypes.c_float, _i64, _i32, _vp, _vp, _vp],
+                             ctypes.c_int),
+    "moe_rope_kv_bf16": ([_vp, _i64, _i32, _i32, _i32, _vp, _vp, _i64, _vp, _vp, _vp, _vp],
+                         ctypes.c_int),
+    "moe_attention_bf16": ([_vp, _vp, _vp, _i64, _i32, _i32, _i32, _vp, _i64, ctypes.c_float,
+                            _vp, _vp], ctypes.c_int),
+    "moe_gemv_bf16": ([_vp, _vp, _i64, _i32, _i32, _vp, _vp], ctypes.c_int),
 }
 
 _lock = threading.Lock()

@@ -1,0 +1,221 @@
+"""Native Mixtral decoder for the end-to-end run: the dense parts of each decoder layer
+(RMSNorm, rotary embedding, grouped-query attention with a KV cache, the attention
+projections, lm_head) on this package's HIP kernels, around the NF4 MoE layer.
+
+The reference builds the same stack from Hugging Face modules (engine/engine.py:192-327:
+embed_tokens, MixtralRotaryEmbedding, MixtralDecoderLayer with its MoE block swapped for
+MoELayer, final MixtralRMSNorm, lm_head) and runs it eagerly with a DynamicCache
+(engine/engine.py:329-385, 500-627).  Here the decoder layer is
+
+    x1 = rmsnorm(h; input_layernorm)               h_mid = bf16(h + o_proj(attn(x1)))
+    x2 = rmsnorm(h_mid; post_attention_layernorm)  h_out = bf16(h_mid + moe(x2))
+
+with the residual adds fused into the next RMSNorm, q/k/v in one projection, the KV cache
+preallocated [layer][kv head][max_seq][head_dim] and the position a device int32, so that
+one decode step is a fixed sequence of kernel launches (capturable as a HIP graph).
+Decode-size batches (up to 4 tokens) use the bandwidth-bound GEMV kernel for the
+projections; longer prompts use the library GEMM.
+"""
+from __future__ import annotations
+
+import dataclasses
+import math
+from typing import List, Optional
+
+import torch
+
+from .. import _lib, ops
+
+
+@dataclasses.dataclass(frozen=True)
+class MixtralShape:
+    """Architecture of the decoder (defaults: Mixtral-8x7B)."""
+
+    hidden: int = 4096
+    ffn: int = 14336
+    layers: int = 32
+    n_heads: int = 32
+    n_kv_heads: int = 8
+    head_dim: int = 128
+    vocab: int = 32000
+    experts: int = 8
+    top_k: int = 2
+    rope_theta: float = 1e6
+    rms_eps: float = 1e-5
+
+    @property
+    def qkv_rows(self) -> int:
+        return (self.n_heads + 2 * self.n_kv_heads) * self.head_dim
+
+
+@dataclasses.dataclass
+class LayerWeights:
+    input_norm: torch.Tensor       # [H] bf16
+    qkv: torch.Tensor              # [(nq + 2 nkv) hd, H] bf16: q_proj; k_proj; v_proj
+    o_proj: torch.Tensor           # [H, nq hd] bf16
+    post_norm: torch.Tensor        # [H] bf16
+    gate: torch.Tensor             # [E, H] bf16 (router)
+    experts: list                  # per expert {"w1"|"w3"|"w2": (packed, absmax, code)}
+    table: Optional[object] = None  # ctypes expert table (device pointers), all-resident
+
+
+@dataclasses.dataclass
+class DecoderWeights:
+    shape: MixtralShape
+    embed: torch.Tensor            # [V, H] bf16
+    layers: List[LayerWeights]
+    final_norm: torch.Tensor       # [H] bf16
+    lm_head: torch.Tensor          # [V, H] bf16
+
+
+def _normal(shape, gen, device, std=0.02):
+    return (torch.randn(shape, generator=gen, device=device) * std).to(torch.bfloat16)
+
+
+def synthesize(shape: MixtralShape, seed: int, device, experts_on=None) -> DecoderWeights:
+    """Random-init weights of the architecture (bf16 N(0, 0.02) linear and embedding weights,
+    unit norm weights, as a freshly initialised model), experts NF4-quantised by the library.
+    Drawn on ``device`` in a fixed order from one seeded generator; ``experts_on`` is where
+    the NF4 expert tensors are kept (default: ``device``)."""
+    from .._lib import MoeNf4Expert
+
+    dev = torch.device(device)
+    keep = torch.device(experts_on) if experts_on is not None else dev
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    H, F, E = shape.hidden, shape.ffn, shape.experts
+    embed = _normal((shape.vocab, H), gen, dev)
+    layers = []
+    for _ in range(shape.layers):
+        qkv = _normal((shape.qkv_rows, H), gen, dev)
+        o = _normal((H, shape.n_heads * shape.head_dim), gen, dev)
+        gate = _normal((E, H), gen, dev)
+        experts = []
+        for _e in range(E):
+            st = {}
+            for name, s in (("w1", (F, H)), ("w3", (F, H)), ("w2", (H, F))):
+                w = _normal(s, gen, dev)
+                p, a, c = ops.nf4_quantize(w)
+                del w
+                st[name] = (p.to(keep), a.to(keep), c.to(keep)) if keep != dev else (p, a, c)
+            experts.append(st)
+        table = None
+        if keep.type == "cuda":
+            table = ops.expert_table([MoeNf4Expert(*(t.data_ptr() for n in ("w1", "w3", "w2")
+                                                     for t in st[n])) for st in experts])
+        ones = torch.ones(H, dtype=torch.bfloat16, device=dev)
+        layers.append(LayerWeights(ones, qkv, o, ones.clone(), gate, experts, table))
+    final = torch.ones(H, dtype=torch.bfloat16, device=dev)
+    lm_head = _normal((shape.vocab, H), gen, dev)
+    return DecoderWeights(shape, embed, layers, final, lm_head)
+
+
+def rope_inv_freq(shape: MixtralShape) -> torch.Tensor:
+    """inv_freq[i] = 1 / theta^(2i / head_dim) in fp32, as MixtralRotaryEmbedding computes it."""
+    i = torch.arange(0, shape.head_dim, 2, dtype=torch.int64).float()
+    return 1.0 / (shape.rope_theta ** (i / shape.head_dim))
+
+
+class NativeDecoder:
+    """Device state (KV cache, position, buffers) and the prefill / decode forward passes.
+
+    ``moe`` is a callable (layer_id, x [T, H] bf16) -> [T, H] bf16 for the MoE block; by
+    default the all-resident layer entry point on the weights' expert tables.
+    """
+
+    GEMV_MAX_TOKENS = 4
+
+    def __init__(self, weights: DecoderWeights, max_seq: int, device, moe=None) -> None:
+        s = weights.shape
+        self.w = weights
+        self.s = s
+        self.dev = torch.device(device)
+        self.max_seq = int(max_seq)
+        self.lib = _lib.lib()
+        L = s.layers
+        self.k_cache = torch.zeros((L, s.n_kv_heads, self.max_seq, s.head_dim), dtype=torch.bfloat16,
+                                   device=self.dev)
+        self.v_cache = torch.zeros_like(self.k_cache)
+        self.pos = torch.zeros((1,), dtype=torch.int32, device=self.dev)
+        self.inv_freq = rope_inv_freq(s).to(self.dev)
+        self.scaling = float(s.head_dim ** -0.5)
+        self.moe = moe if moe is not None else self._moe_resident
+        self._moe_bufs = {}
+
+    # ------------------------------------------------------------------ pieces
+    def _stream(self) -> int:
+        return torch.cuda.current_stream(self.dev).cuda_stream
+
+    def _linear(self, W: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
+        T = x.shape[0]
+        if T <= self.GEMV_MAX_TOKENS and W.shape[1] % 512 == 0:
+            y = torch.empty((T, W.shape[0]), dtype=torch.bfloat16, device=self.dev)
+            _lib.check(self.lib.moe_gemv_bf16(W.data_ptr(), x.data_ptr(), T, W.shape[0], W.shape[1],
+                                              y.data_ptr(), self._stream()), "gemv")
+            return y
+        return x @ W.t()  # nn.Linear without bias on bf16 tensors
+
+    def _norm(self, x, residual, weight, residual_out=None):
+        out = torch.empty_like(x)
+        _lib.check(self.lib.moe_add_rmsnorm_bf16(
+            x.data_ptr(), 0 if residual is None else residual.data_ptr(), weight.data_ptr(),
+            self.s.rms_eps, x.shape[0], x.shape[1],
+            0 if residual_out is None else residual_out.data_ptr(), out.data_ptr(),
+            self._stream()), "add_rmsnorm")
+        return out
+
+    def _attention(self, l: int, x1: torch.Tensor) -> torch.Tensor:
+        s, T = self.s, x1.shape[0]
+        qkv = self._linear(self.w.layers[l].qkv, x1)
+        q = torch.empty((T, s.n_heads * s.head_dim), dtype=torch.bfloat16, device=self.dev)
+        kc, vc = self.k_cache[l], self.v_cache[l]
+        _lib.check(self.lib.moe_rope_kv_bf16(qkv.data_ptr(), T, s.n_heads, s.n_kv_heads, s.head_dim,
+                                             self.inv_freq.data_ptr(), self.pos.data_ptr(),
+                                             self.max_seq, q.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+                                             self._stream()), "rope_kv")
+        a = torch.empty_like(q)
+        _lib.check(self.lib.moe_attention_bf16(q.data_ptr(), kc.data_ptr(), vc.data_ptr(), T,
+                                               s.n_heads, s.n_kv_heads, s.head_dim,
+                                               self.pos.data_ptr(), self.max_seq, self.scaling,
+                                               a.data_ptr(), self._stream()), "attention")
+        return self._linear(self.w.layers[l].o_proj, a)
+
+    def _moe_resident(self, l: int, x: torch.Tensor) -> torch.Tensor:
+        s, T = self.s, x.shape[0]
+        lw = self.w.layers[l]
+        if T not in self._moe_bufs:
+            ws_bytes = self.lib.moe_layer_workspace_bytes(T, s.top_k, s.experts, s.hidden, s.ffn)
+            self._moe_bufs[T] = (torch.empty((ws_bytes,), dtype=torch.uint8, device=self.dev),
+                                 torch.empty((T, s.top_k), dtype=torch.float32, device=self.dev),
+                                 torch.empty((T, s.top_k), dtype=torch.int64, device=self.dev))
+        ws, w, idx = self._moe_bufs[T]
+        out = torch.empty_like(x)
+        _lib.check(self.lib.moe_layer_forward_nf4(lw.table, s.experts, lw.gate.data_ptr(), None,
+                                                  x.data_ptr(), T, s.hidden, s.ffn, s.top_k,
+                                                  out.data_ptr(), None, w.data_ptr(), idx.data_ptr(),
+                                                  ws.data_ptr(), ws.numel(), self._stream()),
+                   "moe_layer_forward_nf4")
+        return out
+
+    # ------------------------------------------------------------------ forward
+    def forward(self, ids: torch.Tensor) -> torch.Tensor:
+        """Run tokens ``ids`` [T] (device int64) at positions pos .. pos + T - 1 through the
+        stack, append their keys/values to the cache, advance the position, and return the
+        logits [1, V] (bf16) of the last token."""
+        s = self.s
+        T = ids.shape[0]
+        h = self.w.embed.index_select(0, ids)          # [T, H]
+        resid = torch.empty_like(h)
+        x1 = self._norm(h, None, self.w.layers[0].input_norm)
+        for l, lw in enumerate(self.w.layers):
+            a = self._attention(l, x1)
+            x2 = self._norm(a, h, lw.post_norm, residual_out=resid)    # resid = h + attn
+            m = self.moe(l, x2)
+            nxt = self.w.layers[l + 1].input_norm if l + 1 < s.layers else self.w.final_norm
+            h_new = torch.empty_like(h)
+            x1 = self._norm(m, resid, nxt, residual_out=h_new)          # h_new = resid + moe
+            h = h_new
+        self.pos += T
+        return self._linear(self.w.lm_head, x1[T - 1:T].contiguous())
+
+    def reset(self) -> None:
+        self.pos.zero_()

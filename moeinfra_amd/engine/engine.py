@@ -1,0 +1,214 @@
+"""End-to-end inference engine (the generate() surface of engine/engine.py:440-627 of the
+reference) over the native decoder (decoder.py) and the NF4 MoE layer.
+
+generate(request): prefill the prompt (the last position's logits give the first token),
+then greedy decode; ttft_ms is the prefill time, tps = (generated - 1) / decode seconds
+(engine/engine.py:478-484).  Batch 1, like the reference's decode path.
+
+Two expert modes, as in the reference:
+* all-resident: every NF4 expert stays in HBM (288 GB holds all 23.6 GiB); the MoE block
+  is one call of the layer entry point, and the whole decode step (embedding, 32 decoder
+  layers, final norm, lm_head, argmax, position advance) is captured once as a HIP graph
+  and replayed per token.  Generated ids stay on the device until the end.
+* offload: the NF4 store lives in pinned host memory (CacheManager CPU tier) with a bounded
+  GPU tier; each layer's MoE block is the reference's MoELayer (route, make the routed
+  experts resident through the transfer scheduler's staged H2D, compute, demote the ones
+  that were not resident), optionally with the PrefetchEngine starting the next layer's
+  copies on the side stream.
+"""
+from __future__ import annotations
+
+import logging
+import time
+from typing import Optional
+
+import torch
+
+from .decoder import DecoderWeights, NativeDecoder
+from .prefetch import PrefetchEngine
+from .types import ForwardRequest, ForwardResult, PrefetchPolicy
+
+
+class InferenceEngine:
+    """Native Mixtral-shaped NF4 MoE inference engine on one GPU."""
+
+    def __init__(self, weights: DecoderWeights, max_seq: int = 1024, device="cuda:0",
+                 offload: bool = False, gpu_expert_slots: Optional[int] = None,
+                 prefetch: PrefetchPolicy = PrefetchPolicy.NONE, prefetch_depth: int = 1,
+                 use_graph: bool = True, logger: Optional[logging.Logger] = None) -> None:
+        self._logger = logger or logging.getLogger(__name__)
+        self.device = torch.device(device)
+        self.weights = weights
+        self.offload = offload
+        self.use_graph = use_graph and not offload
+        self._moe_layers = None
+        self.cache_manager = None
+        self.transfer_scheduler = None
+        self.prefetch_engine = None
+        moe = None
+        if offload:
+            moe = self._build_offload(gpu_expert_slots, prefetch, prefetch_depth)
+        self.decoder = NativeDecoder(weights, max_seq, self.device, moe=moe)
+        self._graph = None
+        self._last_logits = None
+
+    # ------------------------------------------------------------------ offload wiring
+    def _build_offload(self, gpu_slots, policy, depth):
+        from ..cache.manager import CacheManager
+        from ..cache.types import EvictionPolicy
+        from ..model.expert import PrequantizedNF4Expert
+        from ..model.moe_layer import MoELayer
+        from ..transfer.pinned_memory import PinnedMemoryBudget
+        from ..transfer.reusable_staging import ReusablePinnedStagingPool
+        from ..transfer.scheduler import TransferScheduler
+        from .router import ExpertRouter
+
+        s = self.weights.shape
+        n_experts = s.layers * s.experts
+        gpu_slots = n_experts if gpu_slots is None else int(gpu_slots)
+        cm = CacheManager(gpu_slots=max(gpu_slots, 1), cpu_slots=n_experts, policy=EvictionPolicy.LRU)
+        for l, lw in enumerate(self.weights.layers):
+            for e, st in enumerate(lw.experts):
+                ex = PrequantizedNF4Expert.from_nf4_tensors(
+                    {n: (p.cpu(), a.cpu(), c.cpu()) for n, (p, a, c) in st.items()}, s.hidden, s.ffn)
+                cm.put(l, e, ex, device="cpu")
+        slot_bytes = cm.get_size_bytes(0, 0)
+        n_slots = 2 * s.experts
+        pool = ReusablePinnedStagingPool(PinnedMemoryBudget(n_slots * slot_bytes), slot_bytes)
+        self._transfer_stream = torch.cuda.Stream(self.device)
+        sched = TransferScheduler(cm, 24.0, n_slots, staging_pool=pool,
+                                  transfer_stream=self._transfer_stream)
+        self.cache_manager, self.transfer_scheduler = cm, sched
+        if policy != PrefetchPolicy.NONE:
+            self.prefetch_engine = PrefetchEngine(cm, sched, policy, depth, logger=self._logger)
+        self._moe_layers = [MoELayer(l, ExpertRouter(lw.gate, s.top_k), cm, None, sched,
+                                     logger=self._logger)
+                            for l, lw in enumerate(self.weights.layers)]
+        return self._moe_offload
+
+    def _moe_offload(self, l: int, x: torch.Tensor) -> torch.Tensor:
+        pe = self.prefetch_engine
+        if pe is not None:
+            # This layer's prefetched copies finish before it routes (their events are on
+            # the side stream); the compute stream waits for the side stream's work.
+            torch.cuda.current_stream(self.device).wait_stream(self._transfer_stream)
+            self._transfer_stream.synchronize()
+            pe.poll()
+        out = self._moe_layers[l].forward(x)
+        if pe is not None:
+            idx, _ = self._moe_layers[l].router.route(x)
+            pe.on_layer_complete(l, idx)
+        return out
+
+    # ------------------------------------------------------------------ generate
+    @torch.no_grad()
+    def generate(self, request: ForwardRequest) -> ForwardResult:
+        ids = request.input_ids
+        if ids.ndim == 2 and ids.shape[1] + max(request.max_new_tokens - 1, 0) > self.decoder.max_seq:
+            raise ValueError(f"prompt ({ids.shape[1]}) + new tokens ({request.max_new_tokens}) "
+                             f"exceed max_seq {self.decoder.max_seq}")
+        stage = {}
+        t0 = time.perf_counter()
+        logits = self._prefill(request.input_ids, request.attention_mask)
+        torch.cuda.synchronize(self.device)
+        ttft_ms = (time.perf_counter() - t0) * 1e3
+        stage["prefill"] = ttft_ms
+        t1 = time.perf_counter()
+        tokens = self._decode(logits, request.max_new_tokens)
+        torch.cuda.synchronize(self.device)
+        decode_ms = (time.perf_counter() - t1) * 1e3
+        stage["decode"] = decode_ms
+        steps = max(len(tokens) - 1, 0)
+        tps = steps / (decode_ms / 1e3) if steps > 0 and decode_ms > 0 else 0.0
+        last = self._last_logits if self._last_logits is not None else logits
+        return ForwardResult(logits=last, token_ids=tokens, ttft_ms=ttft_ms, tps=tps,
+                             stage_timings=stage)
+
+    @torch.no_grad()
+    def _prefill(self, input_ids: torch.Tensor, attention_mask=None) -> torch.Tensor:
+        """Encode the prompt [1, S] into the KV cache; logits [1, 1, V] of its last token."""
+        if input_ids.ndim != 2:
+            raise ValueError(f"input_ids must have shape (batch, seq_len), got {tuple(input_ids.shape)}")
+        if input_ids.shape[0] != 1:
+            raise ValueError("the decode path supports batch_size=1")
+        if input_ids.shape[1] <= 0:
+            raise ValueError("input_ids must contain at least one token")
+        if attention_mask is not None and attention_mask.shape != input_ids.shape:
+            raise ValueError("attention_mask must have the same shape as input_ids")
+        if attention_mask is not None and not bool(attention_mask.all()):
+            raise NotImplementedError("padded prompts are not supported (batch 1, causal mask)")
+        if input_ids.shape[1] > self.decoder.max_seq:
+            raise ValueError(f"prompt of {input_ids.shape[1]} tokens exceeds max_seq {self.decoder.max_seq}")
+        self.decoder.reset()
+        ids = input_ids[0].to(device=self.device, dtype=torch.long)
+        logits = self.decoder.forward(ids).reshape(1, 1, -1)
+        self._last_logits = logits
+        return logits
+
+    def _capture(self, n_max: int):
+        """Graph of one decode step: token in -> logits, argmax, token out, position + 1,
+        generated id stored at the step counter."""
+        dec = self.decoder
+        self._tok = torch.zeros((1,), dtype=torch.long, device=self.device)
+        self._gen = torch.zeros((n_max,), dtype=torch.long, device=self.device)
+        self._ctr = torch.zeros((1,), dtype=torch.long, device=self.device)
+        pos_save = dec.pos.clone()
+        kc, vc = dec.k_cache.clone(), dec.v_cache.clone()
+
+        def body():
+            logits = dec.forward(self._tok)
+            nxt = logits.argmax(dim=-1)
+            self._tok.copy_(nxt)
+            self._gen.index_copy_(0, self._ctr, nxt)
+            self._ctr.add_(1)
+            return logits
+
+        side = torch.cuda.Stream(self.device)
+        side.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(side):
+            for _ in range(2):  # warm up allocations and library state outside the capture
+                body()
+        torch.cuda.current_stream(self.device).wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            self._graph_logits = body()
+        # The warm-up and the capture advanced the state: restore it.
+        dec.pos.copy_(pos_save)
+        dec.k_cache.copy_(kc)
+        dec.v_cache.copy_(vc)
+        self._graph = graph
+        self._graph_n = n_max
+
+    @torch.no_grad()
+    def _decode(self, next_token_logits: torch.Tensor, max_new_tokens: int) -> list:
+        """Greedy decode from the prompt's logits (engine/engine.py:568-627)."""
+        if max_new_tokens < 0:
+            raise ValueError("max_new_tokens must be non-negative")
+        if max_new_tokens == 0:
+            return []
+        if next_token_logits.shape[0] != 1:
+            raise ValueError("Current decode path supports batch_size=1")
+        dec = self.decoder
+        first = next_token_logits[:, -1, :].argmax(dim=-1)
+        if max_new_tokens == 1:
+            return [int(first.item())]
+        if self.use_graph:
+            if self._graph is None or self._graph_n < max_new_tokens:
+                self._capture(max(max_new_tokens, 64))
+            self._tok.copy_(first)
+            self._ctr.zero_()
+            self._gen[0:1].copy_(first)
+            self._ctr.add_(1)
+            for _ in range(1, max_new_tokens):
+                self._graph.replay()
+            self._last_logits = self._graph_logits.reshape(1, 1, -1)
+            return [int(v) for v in self._gen[:max_new_tokens].tolist()]
+        tok = first
+        gen = [tok]
+        logits = next_token_logits
+        for _ in range(1, max_new_tokens):
+            logits = dec.forward(tok)
+            tok = logits.argmax(dim=-1)
+            gen.append(tok)
+        self._last_logits = logits.reshape(1, 1, -1)
+        return [int(v) for v in torch.cat(gen).tolist()]

@@ -291,6 +291,21 @@ class PrequantizedNF4Expert:
         return cls(w1=dict(w1), w2=dict(w2), w3=dict(w3), hidden_size=hidden_size,
                    intermediate_size=intermediate_size)
 
+    @classmethod
+    def from_nf4_tensors(cls, states: dict, hidden_size: int,
+                         intermediate_size: int) -> "PrequantizedNF4Expert":
+        """Serialized expert from {"w1"|"w3"|"w2": (packed uint8, absmax fp32, code fp32)}
+        (w1/w3 [intermediate, hidden], w2 [hidden, intermediate]), with the keys the
+        reference's store uses (model/expert.py:193-198)."""
+        shapes = {"w1": (intermediate_size, hidden_size), "w3": (intermediate_size, hidden_size),
+                  "w2": (hidden_size, intermediate_size)}
+        ser = {}
+        for name, (packed, absmax, code) in states.items():
+            qs = NF4QuantState(absmax=absmax, code=code, shape=torch.Size(shapes[name]))
+            ser[name] = {"weight": packed.reshape(-1, 1), "weight.absmax": absmax,
+                         "weight.quant_map": code, "weight." + _BLOB_KEY: qs.blob()}
+        return cls.from_serialized(ser["w1"], ser["w2"], ser["w3"], hidden_size, intermediate_size)
+
     @property
     def device(self) -> torch.device:
         return self.w1["weight"].device

@@ -1,0 +1,221 @@
+"""End-to-end decoder on the GPU: the dense kernels (RMSNorm, rotary + KV cache,
+attention, GEMV) against CPU restatements of the Hugging Face modules the reference runs,
+and the whole engine (prefill + greedy decode, graph-replayed and eager, all-resident and
+offload) against the CPU reference decoder, teacher-forced on the engine's tokens."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from decoder_ref import RefDecoder, rel_l2, rmsnorm, rope, top2_gap
+from helpers import bits
+
+pytestmark = pytest.mark.gpu
+
+
+def _bf16(shape, seed, std=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(shape, generator=g) * std).to(torch.bfloat16)
+
+
+def _ulps(a: torch.Tensor, b: torch.Tensor) -> np.ndarray:
+    x = bits(a).astype(np.int32)
+    y = bits(b).astype(np.int32)
+    # bf16 bit patterns -> ordered integers (sign-magnitude to two's complement)
+    x = np.where(x & 0x8000, -(x & 0x7FFF), x)
+    y = np.where(y & 0x8000, -(y & 0x7FFF), y)
+    return np.abs(x - y)
+
+
+@pytest.mark.parametrize("T,H,with_res", [(1, 4096, True), (40, 4096, True), (3, 512, False)])
+def test_add_rmsnorm(cuda_device, T, H, with_res):
+    from moeinfra_amd import _lib
+
+    x, r, w = _bf16((T, H), 1), _bf16((T, H), 2), _bf16((H,), 3, 0.5)
+    dev = lambda t: t.to(cuda_device)
+    out = torch.empty((T, H), dtype=torch.bfloat16, device=cuda_device)
+    r_out = torch.empty_like(out)
+    xd, rd, wd = dev(x), dev(r), dev(w)
+    _lib.check(_lib.lib().moe_add_rmsnorm_bf16(xd.data_ptr(), rd.data_ptr() if with_res else 0,
+                                               wd.data_ptr(), 1e-5, T, H,
+                                               r_out.data_ptr() if with_res else 0, out.data_ptr(),
+                                               torch.cuda.current_stream().cuda_stream), "norm")
+    torch.cuda.synchronize()
+    resid = x + r if with_res else x
+    if with_res:
+        np.testing.assert_array_equal(bits(r_out), bits(resid))        # one bf16 add: exact
+    want = rmsnorm(resid, w, 1e-5)
+    u = _ulps(out.cpu(), want)
+    assert u.max() <= 1 and (u > 0).mean() < 0.02                     # fp32 sum order only
+
+
+def test_rope_and_cache_write(cuda_device):
+    from moeinfra_amd import _lib
+    from moeinfra_amd.engine.decoder import MixtralShape, rope_inv_freq
+
+    s = MixtralShape()
+    T, p0, max_seq = 5, 37, 128
+    qkv = _bf16((T, s.qkv_rows), 4)
+    inv = rope_inv_freq(s)
+    kc = torch.zeros((s.n_kv_heads, max_seq, s.head_dim), dtype=torch.bfloat16, device=cuda_device)
+    vc = torch.zeros_like(kc)
+    q = torch.empty((T, s.n_heads * s.head_dim), dtype=torch.bfloat16, device=cuda_device)
+    pos = torch.tensor([p0], dtype=torch.int32, device=cuda_device)
+    qd, invd = qkv.to(cuda_device), inv.to(cuda_device)
+    _lib.check(_lib.lib().moe_rope_kv_bf16(qd.data_ptr(), T, s.n_heads, s.n_kv_heads, s.head_dim,
+                                           invd.data_ptr(), pos.data_ptr(), max_seq, q.data_ptr(),
+                                           kc.data_ptr(), vc.data_ptr(),
+                                           torch.cuda.current_stream().cuda_stream), "rope")
+    torch.cuda.synchronize()
+    nq, nkv, hd = s.n_heads, s.n_kv_heads, s.head_dim
+    positions = torch.arange(p0, p0 + T)
+    want_q = rope(qkv[:, :nq * hd].reshape(T, nq, hd), positions, inv).reshape(T, -1)
+    want_k = rope(qkv[:, nq * hd:(nq + nkv) * hd].reshape(T, nkv, hd), positions, inv)
+    want_v = qkv[:, (nq + nkv) * hd:].reshape(T, nkv, hd)
+    kc, vc = kc.cpu(), vc.cpu()
+    assert _ulps(q.cpu(), want_q).max() <= 1                              # cos/sin libm last bit
+    assert _ulps(kc[:, p0:p0 + T].transpose(0, 1).contiguous(), want_k).max() <= 1
+    np.testing.assert_array_equal(bits(vc[:, p0:p0 + T].transpose(0, 1).contiguous()), bits(want_v))
+    assert not kc[:, :p0].any() and not kc[:, p0 + T:].any()              # other rows untouched
+
+
+@pytest.mark.parametrize("T,p0", [(1, 0), (1, 71), (40, 0), (7, 20)])
+def test_attention(cuda_device, T, p0):
+    from moeinfra_amd import _lib
+
+    nq, nkv, hd, max_seq = 32, 8, 128, 256
+    S = p0 + T
+    q = _bf16((T, nq, hd), 5)
+    k = _bf16((nkv, S, hd), 6)
+    v = _bf16((nkv, S, hd), 7)
+    kc = torch.zeros((nkv, max_seq, hd), dtype=torch.bfloat16)
+    vc = torch.zeros_like(kc)
+    kc[:, :S], vc[:, :S] = k, v
+    out = torch.empty((T, nq * hd), dtype=torch.bfloat16, device=cuda_device)
+    pos = torch.tensor([p0], dtype=torch.int32, device=cuda_device)
+    qd, kd, vd = q.to(cuda_device), kc.to(cuda_device), vc.to(cuda_device)
+    _lib.check(_lib.lib().moe_attention_bf16(qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), T, nq, nkv,
+                                             hd, pos.data_ptr(), max_seq, hd ** -0.5, out.data_ptr(),
+                                             torch.cuda.current_stream().cuda_stream), "attention")
+    torch.cuda.synchronize()
+    # Reference: eager attention in fp32 with the bf16 roundings of the bf16 module.
+    K = k.float().repeat_interleave(nq // nkv, dim=0)
+    V = v.float().repeat_interleave(nq // nkv, dim=0)
+    sc = torch.matmul(q.float().transpose(0, 1), K.transpose(1, 2)).to(torch.bfloat16)
+    sc = (sc.float() * (hd ** -0.5)).to(torch.bfloat16).float()
+    mask = torch.full((T, S), float("-inf"))
+    for t in range(T):
+        mask[t, :p0 + t + 1] = 0.0
+    p = torch.softmax(sc + mask, dim=-1).to(torch.bfloat16).float()
+    want = torch.matmul(p, V).transpose(0, 1).reshape(T, nq * hd)
+    assert rel_l2(out.cpu(), want) < 4e-3
+
+
+@pytest.mark.parametrize("T,N,K", [(1, 6144, 4096), (1, 4096, 4096), (1, 1000, 512), (4, 515, 1024)])
+def test_gemv(cuda_device, T, N, K):
+    from moeinfra_amd import _lib
+
+    W = _bf16((N, K), 8, 0.02)
+    x = _bf16((T, K), 9)
+    y = torch.empty((T, N), dtype=torch.bfloat16, device=cuda_device)
+    Wd, xd = W.to(cuda_device), x.to(cuda_device)
+    _lib.check(_lib.lib().moe_gemv_bf16(Wd.data_ptr(), xd.data_ptr(), T, N, K, y.data_ptr(),
+                                        torch.cuda.current_stream().cuda_stream), "gemv")
+    torch.cuda.synchronize()
+    want = (x.float() @ W.float().t()).to(torch.bfloat16)
+    u = _ulps(y.cpu(), want)
+    assert u.max() <= 1 and (u > 0).mean() < 0.05
+
+
+# --------------------------------------------------------------------------- engine
+def _small_shape():
+    from moeinfra_amd.engine.decoder import MixtralShape
+
+    return MixtralShape(hidden=512, ffn=1024, layers=2, n_heads=8, n_kv_heads=2, head_dim=64,
+                        vocab=640, experts=8, top_k=2)
+
+
+_E2E = {}
+
+
+def _small_engine_weights(device):
+    if "w" not in _E2E:
+        from moeinfra_amd.engine.decoder import synthesize
+
+        _E2E["w"] = synthesize(_small_shape(), seed=5, device=device)
+    return _E2E["w"]
+
+
+def _check_against_reference(res, weights, prompt, tol=2e-2):
+    ref = RefDecoder(weights)
+    want = ref.forward(prompt[0].tolist())
+    toks = res.token_ids
+    logits_seen = [want]
+    for t in toks[:-1]:
+        logits_seen.append(ref.forward([t]))
+    for step, (tok, lg) in enumerate(zip(toks, logits_seen)):
+        if int(lg.argmax()) != tok:
+            assert top2_gap(lg) < 0.05 * float(lg.abs().max()), (step, tok, int(lg.argmax()))
+    assert rel_l2(res.logits.float().cpu().reshape(-1), logits_seen[-1].reshape(-1)) < tol
+
+
+@pytest.mark.parametrize("use_graph", [True, False])
+def test_engine_matches_reference(cuda_device, use_graph):
+    from moeinfra_amd.engine.engine import InferenceEngine
+    from moeinfra_amd.engine.types import ForwardRequest
+
+    w = _small_engine_weights(cuda_device)
+    prompt = torch.randint(0, w.shape.vocab, (1, 12), generator=torch.Generator().manual_seed(3))
+    eng = InferenceEngine(w, max_seq=64, device=cuda_device, use_graph=use_graph)
+    res = eng.generate(ForwardRequest(prompt, max_new_tokens=8))
+    assert len(res.token_ids) == 8 and res.tps > 0 and res.ttft_ms > 0
+    _check_against_reference(res, w, prompt)
+    _E2E.setdefault("tokens", {})[use_graph] = (res.token_ids, bits(res.logits))
+
+
+def test_engine_graph_replays_match_eager(cuda_device):
+    """Graph replays give bit-identical tokens and logits to eager steps, also when the
+    engine generates twice (a second prefill resets the position and cache)."""
+    from moeinfra_amd.engine.engine import InferenceEngine
+    from moeinfra_amd.engine.types import ForwardRequest
+
+    w = _small_engine_weights(cuda_device)
+    prompt = torch.randint(0, w.shape.vocab, (1, 9), generator=torch.Generator().manual_seed(4))
+    outs = []
+    for use_graph in (False, True):
+        eng = InferenceEngine(w, max_seq=64, device=cuda_device, use_graph=use_graph)
+        for _ in range(2):
+            res = eng.generate(ForwardRequest(prompt, max_new_tokens=10))
+            outs.append((res.token_ids, bits(res.logits)))
+    for toks, lg in outs[1:]:
+        assert toks == outs[0][0]
+        np.testing.assert_array_equal(lg, outs[0][1])
+
+
+def test_engine_offload_matches_reference(cuda_device):
+    """Offload mode: the NF4 store on the host, 4 GPU expert slots, next-layer prefetch."""
+    from moeinfra_amd.engine.engine import InferenceEngine
+    from moeinfra_amd.engine.types import ForwardRequest, PrefetchPolicy
+
+    w = _small_engine_weights(cuda_device)
+    prompt = torch.randint(0, w.shape.vocab, (1, 6), generator=torch.Generator().manual_seed(6))
+    for policy in (PrefetchPolicy.NONE, PrefetchPolicy.NEXT_LAYER):
+        eng = InferenceEngine(w, max_seq=64, device=cuda_device, offload=True, gpu_expert_slots=4,
+                              prefetch=policy)
+        res = eng.generate(ForwardRequest(prompt, max_new_tokens=5))
+        _check_against_reference(res, w, prompt)
+
+
+def test_engine_rejects_bad_requests(cuda_device):
+    from moeinfra_amd.engine.engine import InferenceEngine
+    from moeinfra_amd.engine.types import ForwardRequest
+
+    w = _small_engine_weights(cuda_device)
+    eng = InferenceEngine(w, max_seq=16, device=cuda_device)
+    with pytest.raises(ValueError):
+        eng.generate(ForwardRequest(torch.zeros((12,), dtype=torch.long)))
+    with pytest.raises(ValueError):
+        eng.generate(ForwardRequest(torch.zeros((1, 20), dtype=torch.long)))
+    with pytest.raises(ValueError):
+        eng.generate(ForwardRequest(torch.zeros((1, 4), dtype=torch.long), max_new_tokens=-1))
