@@ -145,6 +145,14 @@ class InferenceEngine:
         self._last_logits = logits
         return logits
 
+    def prepare(self, max_new_tokens: int) -> None:
+        """Capture the decode-step graph for up to ``max_new_tokens`` generated tokens now,
+        so that no later generate() of that length captures inside its timed decode
+        (all-resident graph mode; nothing to do in eager or offload mode)."""
+        if self.use_graph and (self._graph is None or self._graph_n < max_new_tokens):
+            with torch.no_grad():
+                self._capture(max(max_new_tokens, 64))
+
     def _capture(self, n_max: int):
         """Graph of one decode step: token in -> logits, argmax, token out, position + 1,
         generated id stored at the step counter."""

@@ -80,16 +80,25 @@ class RefDecoder:
     """Teacher-forced reference decoder over a weights object with the fields of
     moeinfra_amd.engine.decoder.DecoderWeights (embed, layers[input_norm, qkv, o_proj,
     post_norm, gate, experts], final_norm, lm_head, shape); forward(ids) appends to its
-    own KV cache and returns the last token's fp32 logits [1, V]."""
+    own KV cache and returns the last token's fp32 logits [1, V].  ``layers``: all (None),
+    the first n (an int) or the listed layer indices; ``threads``: host threads of the NF4
+    dequantisation."""
 
-    def __init__(self, weights, layers=None):
+    def __init__(self, weights, layers=None, threads: int = 8):
         w = weights
         s = w.shape
         self.s = s
+        self.threads = int(threads)
         cpu = lambda t: t.detach().cpu()
         self.embed, self.final_norm, self.lm_head = cpu(w.embed), cpu(w.final_norm), cpu(w.lm_head)
         self.layers = []
-        for lw in (w.layers if layers is None else w.layers[:layers]):
+        if layers is None:
+            chosen = w.layers
+        elif isinstance(layers, int):
+            chosen = w.layers[:layers]
+        else:
+            chosen = [w.layers[i] for i in layers]
+        for lw in chosen:
             states = [{n: (cpu(p).numpy().reshape(-1), cpu(a).numpy()) for n, (p, a, _c) in st.items()}
                       for st in lw.experts]
             self.layers.append(dict(inn=cpu(lw.input_norm), qkv=cpu(lw.qkv), o=cpu(lw.o_proj),
@@ -100,12 +109,12 @@ class RefDecoder:
         self.inv_freq = inv_freq(s.head_dim, s.rope_theta)
         self.pos = 0
 
-    def _moe(self, L, x: torch.Tensor, threads: int = 8) -> torch.Tensor:
+    def _moe(self, L, x: torch.Tensor) -> torch.Tensor:
         s = self.s
 
         def expert_fn(e, rows):
             if e not in L["cache"]:
-                L["cache"][e] = orc.dequant_expert(L["states"][e], s.hidden, s.ffn, threads=threads)
+                L["cache"][e] = orc.dequant_expert(L["states"][e], s.hidden, s.ffn, threads=self.threads)
             return orc.swiglu(rows, *L["cache"][e])
 
         out, _ = orc.moe_layer(_bits(x), _bits(L["gate"]), expert_fn, k=s.top_k)
