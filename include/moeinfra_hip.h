@@ -214,6 +214,32 @@ int moe_attention_bf16(const void *q, const void *k_cache, const void *v_cache, 
 int moe_gemv_bf16(const void *weight, const void *x, int64_t T, int32_t N, int32_t K, void *y,
                   void *stream);
 
+/* Fused single-token (decode-step) forms of the above, bit-identical to the unfused
+ * sequence; each saves a launch and its dependent-latency chain (engine/engine.py:568-627
+ * runs these modules once per generated token).
+ *
+ * moe_qkv_rope_bf16: r = x[*x_row] (+ residual) -> residual_out (x_row: device int64, null
+ * for row 0; rows outside [0, x_rows) clamp), then moe_add_rmsnorm_bf16 of r, the q/k/v
+ * projection (weight [(n_q + 2 n_kv) * head_dim, H]) and moe_rope_kv_bf16 at *pos0: q to
+ * q_out, k and v to the cache row *pos0.  H a multiple of 512 up to 8192. */
+int moe_qkv_rope_bf16(const void *weight, const void *x, const void *x_row_i64, int64_t x_rows,
+                      const void *residual, const void *norm_weight, float eps, int32_t H,
+                      int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
+                      const void *inv_freq_f32, const void *pos0_i32, int64_t max_seq,
+                      void *residual_out, void *q_out, void *k_cache, void *v_cache, void *stream);
+
+/* moe_head_argmax_bf16: the final norm of r = x + residual, logits[N] = W[N, K] xn (bf16),
+ * token = argmax (torch.argmax order: NaN first, then the larger value, then the lower
+ * index) as a device int64; when gen_ctr is given, gen[*gen_ctr] = token (if the index is
+ * in [0, gen_cap)) and *gen_ctr += 1; when pos is given, *pos += 1.  Two launches (the
+ * head with per-workgroup candidates in cand_ws, then a one-workgroup reduction).
+ * cand_ws: at least 8 bytes (8 per workgroup used, up to 4 per CU).  K a multiple of 512
+ * up to 8192. */
+int moe_head_argmax_bf16(const void *weight, const void *x, const void *residual,
+                         const void *norm_weight, float eps, int32_t N, int32_t K, void *logits,
+                         void *cand_ws, int64_t cand_ws_bytes, void *token_i64, void *gen_i64,
+                         int64_t gen_cap, void *gen_ctr_i64, void *pos_i32, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

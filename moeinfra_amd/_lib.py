@@ -67,6 +67,10 @@ SIGNATURES = {
     "moe_attention_bf16": ([_vp, _vp, _vp, _i64, _i32, _i32, _i32, _vp, _i64, ctypes.c_float,
                             _vp, _vp], ctypes.c_int),
     "moe_gemv_bf16": ([_vp, _vp, _i64, _i32, _i32, _vp, _vp], ctypes.c_int),
+    "moe_qkv_rope_bf16": ([_vp, _vp, _vp, _i64, _vp, _vp, ctypes.c_float, _i32, _i32, _i32, _i32,
+                           _vp, _vp, _i64, _vp, _vp, _vp, _vp, _vp], ctypes.c_int),
+    "moe_head_argmax_bf16": ([_vp, _vp, _vp, _vp, ctypes.c_float, _i32, _i32, _vp, _vp, _i64, _vp,
+                              _vp, _i64, _vp, _vp, _vp], ctypes.c_int),
 }
 
 _lock = threading.Lock()

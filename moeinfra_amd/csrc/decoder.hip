@@ -31,135 +31,203 @@ __device__ __forceinline__ float block_sum(float v, float *s_part) {
   return t;
 }
 
+// One row of the residual add + RMSNorm, run by all kNormThreads threads of a workgroup:
+// r = x (+ res) with one bf16 add (written to res_out when given), then
+// out = bf16(w * bf16(r * inv)), inv = 1 / sqrt(mean(r^2) + eps) from fp32 statistics.
+// Thread t takes the 8-value chunks (t + i * kNormThreads) * 8 for i < CH (chunks past H
+// load the last chunk again, in bounds, and count for nothing), so every caller with the
+// same H sums in the same order.  All loads are issued before any is used.  `out` may be LDS.
+template <int CH>
+__device__ __forceinline__ void rmsnorm_row(const uint16_t *x, const uint16_t *res, const uint16_t *w,
+                                            float eps, int H, uint16_t *res_out, uint16_t *out,
+                                            float *s_part) {
+  uint4 xv[CH], rs[CH], wv[CH];
+  const bool has_res = res != nullptr;
+  const uint16_t *rp = has_res ? res : x;  // without a residual: loads of x, unused
+#pragma unroll
+  for (int i = 0; i < CH; ++i) {
+    int c = (threadIdx.x + i * kNormThreads) * 8;
+    c = c < H ? c : H - 8;
+    wv[i] = *reinterpret_cast<const uint4 *>(w + c);
+    xv[i] = *reinterpret_cast<const uint4 *>(x + c);
+    rs[i] = *reinterpret_cast<const uint4 *>(rp + c);
+  }
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < CH; ++i) {
+    uint4 v = xv[i];
+    if (has_res) {
+      const uint32_t a[4] = {v.x, v.y, v.z, v.w}, b[4] = {rs[i].x, rs[i].y, rs[i].z, rs[i].w};
+      uint32_t o[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        o[j] = pack_bf16x2(bf16lo_to_f32(a[j]) + bf16lo_to_f32(b[j]),
+                           bf16hi_to_f32(a[j]) + bf16hi_to_f32(b[j]));
+      v = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+    xv[i] = v;
+    const uint32_t a[4] = {v.x, v.y, v.z, v.w};
+    float t = ss;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float lo = bf16lo_to_f32(a[j]), hi = bf16hi_to_f32(a[j]);
+      t += lo * lo + hi * hi;
+    }
+    ss = (threadIdx.x + i * kNormThreads) * 8 < H ? t : ss;
+  }
+  const float inv = 1.0f / sqrtf(block_sum(ss, s_part) / (float)H + eps);
+#pragma unroll
+  for (int i = 0; i < CH; ++i) {
+    const int c = (threadIdx.x + i * kNormThreads) * 8;
+    if (c < H) {
+      const uint32_t a[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
+      const uint32_t g[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
+      uint32_t o[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        o[j] = pack_bf16x2(bf16lo_to_f32(g[j]) * bf16r(bf16lo_to_f32(a[j]) * inv),
+                           bf16hi_to_f32(g[j]) * bf16r(bf16hi_to_f32(a[j]) * inv));
+      if (res_out != nullptr) *reinterpret_cast<uint4 *>(res_out + c) = xv[i];
+      *reinterpret_cast<uint4 *>(out + c) = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+  }
+}
+
+template <int CH>
 __global__ void __launch_bounds__(kNormThreads)
 add_rmsnorm_kernel(const uint16_t *__restrict__ x, const uint16_t *__restrict__ res_in,
                    const uint16_t *__restrict__ w, float eps, int H,
                    uint16_t *__restrict__ res_out, uint16_t *__restrict__ out) {
   __shared__ float s_part[kNormThreads / kWave];
   const size_t base = (size_t)blockIdx.x * H;
-  uint4 rv[kNormMaxChunks];
-  float ss = 0.0f;
-#pragma unroll
-  for (int i = 0; i < kNormMaxChunks; ++i) {
-    const int c = (threadIdx.x + i * kNormThreads) * 8;
-    if (c < H) {
-      uint4 v = *reinterpret_cast<const uint4 *>(x + base + c);
-      if (res_in != nullptr) {
-        const uint4 r = *reinterpret_cast<const uint4 *>(res_in + base + c);
-        const uint32_t a[4] = {v.x, v.y, v.z, v.w}, b[4] = {r.x, r.y, r.z, r.w};
-        uint32_t o[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          o[j] = pack_bf16x2(bf16lo_to_f32(a[j]) + bf16lo_to_f32(b[j]),
-                             bf16hi_to_f32(a[j]) + bf16hi_to_f32(b[j]));
-        v = make_uint4(o[0], o[1], o[2], o[3]);
-        if (res_out != nullptr) *reinterpret_cast<uint4 *>(res_out + base + c) = v;
-      }
-      rv[i] = v;
-      const uint32_t a[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float lo = bf16lo_to_f32(a[j]), hi = bf16hi_to_f32(a[j]);
-        ss += lo * lo + hi * hi;
-      }
-    }
-  }
-  const float inv = 1.0f / sqrtf(block_sum(ss, s_part) / (float)H + eps);
-#pragma unroll
-  for (int i = 0; i < kNormMaxChunks; ++i) {
-    const int c = (threadIdx.x + i * kNormThreads) * 8;
-    if (c < H) {
-      const uint4 wv = *reinterpret_cast<const uint4 *>(w + c);
-      const uint32_t a[4] = {rv[i].x, rv[i].y, rv[i].z, rv[i].w}, g[4] = {wv.x, wv.y, wv.z, wv.w};
-      uint32_t o[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        o[j] = pack_bf16x2(bf16lo_to_f32(g[j]) * bf16r(bf16lo_to_f32(a[j]) * inv),
-                           bf16hi_to_f32(g[j]) * bf16r(bf16hi_to_f32(a[j]) * inv));
-      *reinterpret_cast<uint4 *>(out + base + c) = make_uint4(o[0], o[1], o[2], o[3]);
-    }
-  }
+  rmsnorm_row<CH>(x + base, res_in ? res_in + base : nullptr, w, eps, H,
+                  res_out ? res_out + base : nullptr, out + base, s_part);
 }
 
 constexpr int kRopeThreads = 256;
+constexpr int kRopeMaxHalf = 256;  // head_dim <= 512
 
-// Token t (blockIdx.x) at position pos0 + t: q heads and k heads rotated pairwise (value i
-// with i + hd/2), q to q_out [T, nq, hd], k and v to the cache rows [kv head][pos][hd].
+__device__ __forceinline__ void unpack8(const uint4 v, float *f) {
+  const uint32_t a[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    f[2 * e] = bf16lo_to_f32(a[e]);
+    f[2 * e + 1] = bf16hi_to_f32(a[e]);
+  }
+}
+
+// Token t (blockIdx.x) at position pos0 + t.  The hd/2 rotary angles of the position are
+// evaluated once (cos/sin rounded to bf16, as the bf16 module's cos/sin tensors) into LDS;
+// then each thread rotates 8 consecutive values of the first half of a q or k head with the
+// matching 8 of the second half (value i pairs with i + hd/2), 16-byte loads and stores.
+// q goes to q_out [T, nq, hd]; k and v go to the cache rows [kv head][pos][hd].
 __global__ void __launch_bounds__(kRopeThreads)
 rope_kv_kernel(const uint16_t *__restrict__ qkv, int nq, int nkv, int hd,
                const float *__restrict__ inv_freq, const int32_t *__restrict__ pos0,
                int64_t max_seq, uint16_t *__restrict__ q_out, uint16_t *__restrict__ kc,
                uint16_t *__restrict__ vc) {
+  __shared__ float s_cos[kRopeMaxHalf], s_sin[kRopeMaxHalf];
   const int t = blockIdx.x;
   const int pos = *pos0 + t;
   if (pos < 0 || pos >= max_seq) return;  // the cache has no row for it (caller error)
   const int half = hd >> 1;
+  for (int i = threadIdx.x; i < half; i += kRopeThreads) {
+    const float ang = (float)pos * inv_freq[i];
+    s_cos[i] = bf16r(cosf(ang));
+    s_sin[i] = bf16r(sinf(ang));
+  }
+  __syncthreads();
   const int row = (nq + 2 * nkv) * hd;
   const uint16_t *src = qkv + (size_t)t * row;
-  for (int idx = threadIdx.x; idx < (nq + nkv) * half; idx += kRopeThreads) {
-    const int head = idx / half, i = idx - head * half;
-    const uint16_t *hx = src + (size_t)head * hd;  // k heads follow the q heads
-    const float x1 = bf16_to_f32(hx[i]), x2 = bf16_to_f32(hx[i + half]);
-    const float ang = (float)pos * inv_freq[i];
-    const float c = bf16r(cosf(ang)), s = bf16r(sinf(ang));
-    const uint16_t o1 = f32_to_bf16(bf16r(x1 * c) + bf16r(-x2 * s));
-    const uint16_t o2 = f32_to_bf16(bf16r(x2 * c) + bf16r(x1 * s));
-    uint16_t *dst;
-    if (head < nq)
-      dst = q_out + ((size_t)t * nq + head) * hd;
-    else
-      dst = kc + ((size_t)(head - nq) * max_seq + pos) * hd;
-    dst[i] = o1;
-    dst[i + half] = o2;
+  const int cph = half >> 3;  // 8-value chunks per half head
+  for (int idx = threadIdx.x; idx < (nq + nkv) * cph; idx += kRopeThreads) {
+    const int head = idx / cph, c = idx - head * cph;
+    const uint16_t *hx = src + (size_t)head * hd + c * 8;  // k heads follow the q heads
+    float x1[8], x2[8];
+    unpack8(*reinterpret_cast<const uint4 *>(hx), x1);
+    unpack8(*reinterpret_cast<const uint4 *>(hx + half), x2);
+    uint32_t o1[4], o2[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float r1[2], r2[2];
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        const int i = c * 8 + 2 * e + k;
+        const float co = s_cos[i], si = s_sin[i];
+        const float a = x1[2 * e + k], b = x2[2 * e + k];
+        r1[k] = bf16r(a * co) + bf16r(-b * si);
+        r2[k] = bf16r(b * co) + bf16r(a * si);
+      }
+      o1[e] = pack_bf16x2(r1[0], r1[1]);
+      o2[e] = pack_bf16x2(r2[0], r2[1]);
+    }
+    uint16_t *dst = head < nq ? q_out + ((size_t)t * nq + head) * hd
+                              : kc + ((size_t)(head - nq) * max_seq + pos) * hd;
+    *reinterpret_cast<uint4 *>(dst + c * 8) = make_uint4(o1[0], o1[1], o1[2], o1[3]);
+    *reinterpret_cast<uint4 *>(dst + half + c * 8) = make_uint4(o2[0], o2[1], o2[2], o2[3]);
   }
   const uint16_t *vsrc = src + (size_t)(nq + nkv) * hd;
-  for (int idx = threadIdx.x; idx < nkv * hd; idx += kRopeThreads) {
-    const int head = idx / hd, d = idx - head * hd;
-    vc[((size_t)head * max_seq + pos) * hd + d] = vsrc[idx];
+  const int cpr = hd >> 3;
+  for (int idx = threadIdx.x; idx < nkv * cpr; idx += kRopeThreads) {
+    const int head = idx / cpr, c = idx - head * cpr;
+    *reinterpret_cast<uint4 *>(vc + ((size_t)head * max_seq + pos) * hd + c * 8) =
+        *reinterpret_cast<const uint4 *>(vsrc + (size_t)head * hd + c * 8);
   }
 }
 
 constexpr int kAttnThreads = 256;
 constexpr int kAttnMaxKeys = 8192;
 constexpr int kAttnMaxHeadDim = 256;
+constexpr int kAttnRowsInFlight = 4;  // cache rows per thread per pass
 
 // One workgroup per (query head, token): scores of keys 0 .. pos0 + t (causal), bf16 scores
 // scaled in bf16, fp32 softmax rounded to bf16, then the bf16 probabilities times V with
-// fp32 accumulation.
+// fp32 accumulation.  A cache row of hd bf16 is read by hd/8 consecutive lanes, 16 bytes
+// each, so the workgroup covers 256/(hd/8) rows per load instruction and keeps 4 such
+// loads in flight per thread; a score is the xor-shuffle sum over its row's lanes.  Rows
+// past the last key are clamped to it (in bounds) and their results discarded.
 __global__ void __launch_bounds__(kAttnThreads)
 attention_kernel(const uint16_t *__restrict__ q, const uint16_t *__restrict__ kc,
                  const uint16_t *__restrict__ vc, int nq, int nkv, int hd,
                  const int32_t *__restrict__ pos0, int64_t max_seq, float scaling,
                  uint16_t *__restrict__ out) {
-  __shared__ float s_q[kAttnMaxHeadDim];
   __shared__ float s_p[kAttnMaxKeys];
   __shared__ float s_red[kAttnThreads / kWave];
-  __shared__ float s_acc[kAttnThreads];
+  __shared__ __attribute__((aligned(16))) float s_acc[kAttnThreads * 8];
   const int h = blockIdx.x, t = blockIdx.y;
   const int kvh = h / (nq / nkv);
   // Keys 0 .. pos0 + t, bounded by the cache (a position past it is a caller error).
   const int nkeys = min(*pos0 + t + 1, (int)max_seq);
-  const uint16_t *qr = q + ((size_t)t * nq + h) * hd;
-  for (int d = threadIdx.x; d < hd; d += kAttnThreads) s_q[d] = bf16_to_f32(qr[d]);
-  __syncthreads();
-  const uint16_t *kbase = kc + (size_t)kvh * max_seq * hd;
-  const uint16_t *vbase = vc + (size_t)kvh * max_seq * hd;
+  const int lpr = hd >> 3;               // lanes per row: a power of two <= 32
+  const int rpp = kAttnThreads / lpr;    // rows per load instruction of the workgroup
+  const int sub = threadIdx.x & (lpr - 1), rr = threadIdx.x / lpr;
+  float qf[8];
+  unpack8(*reinterpret_cast<const uint4 *>(q + ((size_t)t * nq + h) * hd + sub * 8), qf);
+  const uint16_t *kbase = kc + (size_t)kvh * max_seq * hd + sub * 8;
+  const uint16_t *vbase = vc + (size_t)kvh * max_seq * hd + sub * 8;
   float mx = -INFINITY;
-  for (int j = threadIdx.x; j < nkeys; j += kAttnThreads) {
-    const uint4 *kr = reinterpret_cast<const uint4 *>(kbase + (size_t)j * hd);
-    float dot = 0.0f;
-    for (int c = 0; c < hd / 8; ++c) {
-      const uint4 kv = kr[c];
-      const uint32_t a[4] = {kv.x, kv.y, kv.z, kv.w};
+  for (int j0 = 0; j0 < nkeys; j0 += kAttnRowsInFlight * rpp) {
+    uint4 kv[kAttnRowsInFlight];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        dot = fmaf(s_q[8 * c + 2 * e], bf16lo_to_f32(a[e]), dot);
-        dot = fmaf(s_q[8 * c + 2 * e + 1], bf16hi_to_f32(a[e]), dot);
+    for (int u = 0; u < kAttnRowsInFlight; ++u) {
+      const int j = min(j0 + u * rpp + rr, nkeys - 1);
+      kv[u] = *reinterpret_cast<const uint4 *>(kbase + (size_t)j * hd);
+    }
+#pragma unroll
+    for (int u = 0; u < kAttnRowsInFlight; ++u) {
+      float kf[8];
+      unpack8(kv[u], kf);
+      float dot = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dot = fmaf(qf[e], kf[e], dot);
+      for (int o = lpr >> 1; o > 0; o >>= 1) dot += __shfl_xor(dot, o, kWave);
+      const int j = j0 + u * rpp + rr;
+      if (j < nkeys) {
+        const float sc = bf16r(bf16r(dot) * scaling);
+        if (sub == 0) s_p[j] = sc;
+        mx = fmaxf(mx, sc);
       }
     }
-    const float sc = bf16r(bf16r(dot) * scaling);
-    s_p[j] = sc;
-    mx = fmaxf(mx, sc);
   }
   // block max
   {
@@ -180,16 +248,38 @@ attention_kernel(const uint16_t *__restrict__ q, const uint16_t *__restrict__ kc
   sum = block_sum(sum, s_red);
   for (int j = threadIdx.x; j < nkeys; j += kAttnThreads) s_p[j] = bf16r(s_p[j] / sum);
   __syncthreads();
-  // out[d] = sum_j p_j v_j[d]: thread (part, d) sums keys part, part + parts, ...
-  const int parts = kAttnThreads / hd;  // hd divides kAttnThreads
-  const int d = threadIdx.x % hd, part = threadIdx.x / hd;
-  float acc = 0.0f;
-  for (int j = part; j < nkeys; j += parts) acc = fmaf(s_p[j], bf16_to_f32(vbase[(size_t)j * hd + d]), acc);
-  s_acc[threadIdx.x] = acc;
+  // out[d] = sum_j p_j v_j[d]: thread (rr, sub) accumulates dims sub*8 .. sub*8+7 over rows
+  // rr, rr + rpp, ...; then the rpp partial rows are summed through LDS.
+  float acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
+  for (int j0 = 0; j0 < nkeys; j0 += kAttnRowsInFlight * rpp) {
+    uint4 vv[kAttnRowsInFlight];
+#pragma unroll
+    for (int u = 0; u < kAttnRowsInFlight; ++u) {
+      const int j = min(j0 + u * rpp + rr, nkeys - 1);
+      vv[u] = *reinterpret_cast<const uint4 *>(vbase + (size_t)j * hd);
+    }
+#pragma unroll
+    for (int u = 0; u < kAttnRowsInFlight; ++u) {
+      const int j = j0 + u * rpp + rr;
+      if (j < nkeys) {
+        const float p = s_p[j];
+        float vf[8];
+        unpack8(vv[u], vf);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] = fmaf(p, vf[e], acc[e]);
+      }
+    }
+  }
+  float4 *sa = reinterpret_cast<float4 *>(s_acc + rr * hd + sub * 8);
+  sa[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+  sa[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
   __syncthreads();
-  if (part == 0) {
-    for (int p = 1; p < parts; ++p) acc += s_acc[p * hd + d];
-    out[((size_t)t * nq + h) * hd + d] = f32_to_bf16(acc);
+  for (int d = threadIdx.x; d < hd; d += kAttnThreads) {
+    float o = 0.0f;
+    for (int r = 0; r < rpp; ++r) o += s_acc[r * hd + d];
+    out[((size_t)t * nq + h) * hd + d] = f32_to_bf16(o);
   }
 }
 
@@ -259,6 +349,302 @@ gemv_kernel(const uint16_t *__restrict__ W, const uint16_t *__restrict__ x, int 
   }
 }
 
+constexpr int kGemv1Chunks = 8;  // 1 KB chunks of a row in flight per step (8 KB)
+
+__device__ __forceinline__ void gemv1_acc(const uint4 a, const uint4 b, const uint4 xv, float &acc0,
+                                          float &acc1) {
+  const uint32_t xa[4] = {xv.x, xv.y, xv.z, xv.w};
+  const uint32_t wa[4] = {a.x, a.y, a.z, a.w};
+  const uint32_t wb[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    acc0 = fmaf(bf16lo_to_f32(wa[e]), bf16lo_to_f32(xa[e]), acc0);
+    acc0 = fmaf(bf16hi_to_f32(wa[e]), bf16hi_to_f32(xa[e]), acc0);
+    acc1 = fmaf(bf16lo_to_f32(wb[e]), bf16lo_to_f32(xa[e]), acc1);
+    acc1 = fmaf(bf16hi_to_f32(wb[e]), bf16hi_to_f32(xa[e]), acc1);
+  }
+}
+
+// Chunks c .. c + 7 of a row (lane slice w = row + lane * 8); chunks past the row's end
+// repeat its last chunk (in bounds) and are masked out by gemv1_dot8.
+__device__ __forceinline__ void gemv1_load8(uint4 (&a)[kGemv1Chunks], const uint16_t *w, int c,
+                                            int nchunk) {
+#pragma unroll
+  for (int u = 0; u < kGemv1Chunks; ++u) {
+    const int cc = c + u < nchunk ? c + u : nchunk - 1;
+    a[u] = *reinterpret_cast<const uint4 *>(w + cc * 512);
+  }
+}
+
+// acc += chunks c .. c + 7 (those < nchunk) of two rows against the x slices xl + chunk*512.
+// The mask is a select, not a branch, so the loads before it stay where they are issued.
+__device__ __forceinline__ void gemv1_dot8(const uint4 (&a)[kGemv1Chunks], const uint4 (&b)[kGemv1Chunks],
+                                           const uint16_t *xl, int c, int nchunk, float &acc0,
+                                           float &acc1) {
+#pragma unroll
+  for (int u = 0; u < kGemv1Chunks; ++u) {
+    const int cc = c + u < nchunk ? c + u : nchunk - 1;
+    const uint4 xv = *reinterpret_cast<const uint4 *>(xl + cc * 512);
+    float t0 = acc0, t1 = acc1;
+    gemv1_acc(a[u], b[u], xv, t0, t1);
+    const bool ok = c + u < nchunk;
+    acc0 = ok ? t0 : acc0;
+    acc1 = ok ? t1 : acc1;
+  }
+}
+
+// One token's rows n0 and n1 of W x: the whole row pair in steps of 8 KB per row, the
+// first step optionally already loaded into a / b.
+__device__ __forceinline__ void gemv1_pair(const uint16_t *w0, const uint16_t *w1, const uint16_t *xl,
+                                           int nchunk, uint4 (&a)[kGemv1Chunks],
+                                           uint4 (&b)[kGemv1Chunks], bool loaded, float &acc0,
+                                           float &acc1) {
+  acc0 = 0.0f;
+  acc1 = 0.0f;
+  for (int c = 0; c < nchunk; c += kGemv1Chunks) {
+    if (c > 0 || !loaded) {
+      gemv1_load8(a, w0, c, nchunk);
+      gemv1_load8(b, w1, c, nchunk);
+    }
+    gemv1_dot8(a, b, xl, c, nchunk, acc0, acc1);
+  }
+}
+
+// y = W x for one token, rows in pairs (n, n + 1) per wave, x read from xl's slices.
+__device__ __forceinline__ void gemv1_rows(const uint16_t *W, const uint16_t *xl, int N, int K,
+                                           uint16_t *y) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int gw = blockIdx.x * kGemvWaves + (threadIdx.x >> 6);
+  const int nw = gridDim.x * kGemvWaves;
+  const int nchunk = K / 512;
+  uint4 a[kGemv1Chunks], b[kGemv1Chunks];
+  for (int n0 = gw * 2; n0 < N; n0 += nw * 2) {
+    const int n1 = n0 + 1 < N ? n0 + 1 : n0;
+    float acc0, acc1;
+    gemv1_pair(W + (size_t)n0 * K + lane * 8, W + (size_t)n1 * K + lane * 8, xl, nchunk, a, b, false,
+               acc0, acc1);
+    acc0 = wave_sum(acc0);
+    acc1 = wave_sum(acc1);
+    if (lane == 0) {
+      y[n0] = f32_to_bf16(acc0);
+      if (n1 != n0) y[n1] = f32_to_bf16(acc1);
+    }
+  }
+}
+
+// T = 1: no LDS staging.  Each wave takes two rows at a time and issues the 1 KB chunks of
+// both rows (8 KB each per step) with the matching 16-byte slices of x (L2-resident after
+// the first waves) before it accumulates, so a wave has 16 weight loads in flight and no
+// workgroup barrier.  Per-lane accumulation order is that of the LDS-staged kernel.
+__global__ void __launch_bounds__(kGemvThreads)
+gemv1_kernel(const uint16_t *__restrict__ W, const uint16_t *__restrict__ x, int N, int K,
+             uint16_t *__restrict__ y) {
+  gemv1_rows(W, x + (threadIdx.x & (kWave - 1)) * 8, N, K, y);
+}
+
+// ---------------------------------------------------------------- fused decode-step kernels
+// One token.  Each removes a launch (about 4-5 us of dependent latency at batch 1) by doing
+// a neighbouring step inside the projection kernel, with the same arithmetic and summation
+// order as the separate kernels, so the results are bit-identical to them.
+constexpr int kFusedMaxH = 8192;
+constexpr int kFusedChunks = kFusedMaxH / (kNormThreads * 8);
+static_assert(kNormThreads == kGemvThreads, "the fused kernels run the norm and the GEMV in one workgroup");
+
+// qkv_rope: r = x[row] (+ residual) -> residual_out (workgroup 0), xn = rmsnorm(r) in every
+// workgroup's LDS, then the q/k/v projection with rows paired (i, i + hd/2) within a head,
+// so the wave holding both outputs applies the rotary embedding (cos/sin of position pos0
+// rounded to bf16) and writes q to q_out and k, v to the cache row pos0.  The first row
+// pair's first 8 KB per row are in flight before the norm.
+__global__ void __launch_bounds__(kNormThreads)
+qkv_rope_kernel(const uint16_t *__restrict__ W, const uint16_t *__restrict__ x,
+                const int64_t *__restrict__ x_row, int64_t x_rows, const uint16_t *__restrict__ res,
+                const uint16_t *__restrict__ nw, float eps, int H, int nq, int nkv, int hd,
+                const float *__restrict__ inv_freq, const int32_t *__restrict__ pos0, int64_t max_seq,
+                uint16_t *__restrict__ res_out, uint16_t *__restrict__ q_out, uint16_t *__restrict__ kc,
+                uint16_t *__restrict__ vc) {
+  __shared__ __attribute__((aligned(16))) uint16_t s_x[kFusedMaxH];
+  __shared__ float s_part[kNormThreads / kWave];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int gw = blockIdx.x * kGemvWaves + (threadIdx.x >> 6);
+  const int nwv = gridDim.x * kGemvWaves;
+  const int half = hd >> 1;
+  const int pairs = (nq + 2 * nkv) * half;
+  const int nchunk = H / 512;
+  auto rows_of = [&](int p, const uint16_t *&w0, const uint16_t *&w1) {
+    const int head = p / half, i = p - head * half;
+    w0 = W + (size_t)(head * hd + i) * H + lane * 8;
+    w1 = w0 + (size_t)half * H;
+  };
+  uint4 a[kGemv1Chunks], b[kGemv1Chunks];
+  const uint16_t *w0 = W, *w1 = W;
+  if (gw < pairs) {
+    rows_of(gw, w0, w1);
+    gemv1_load8(a, w0, 0, nchunk);
+    gemv1_load8(b, w1, 0, nchunk);
+  }
+  // The row id is read after the weight loads are issued (its scalar load would otherwise
+  // be waited for first).
+  __builtin_amdgcn_sched_barrier(0);
+  int64_t row = x_row != nullptr ? *x_row : 0;
+  row = row < 0 ? 0 : (row >= x_rows ? x_rows - 1 : row);  // ids outside the table clamp
+  const uint16_t *xr = x + (size_t)row * H;
+  rmsnorm_row<kFusedChunks>(xr, res, nw, eps, H, blockIdx.x == 0 ? res_out : nullptr, s_x, s_part);
+  __syncthreads();
+  const int pos = *pos0;
+  const bool pos_ok = pos >= 0 && pos < max_seq;  // else the cache has no row (caller error)
+  for (int p = gw; p < pairs; p += nwv) {
+    const bool loaded = p == gw;
+    if (!loaded) rows_of(p, w0, w1);
+    float acc0, acc1;
+    gemv1_pair(w0, w1, s_x + lane * 8, nchunk, a, b, loaded, acc0, acc1);
+    acc0 = wave_sum(acc0);
+    acc1 = wave_sum(acc1);
+    if (lane == 0) {
+      const int head = p / half, i = p - head * half;
+      const float y1 = bf16r(acc0), y2 = bf16r(acc1);
+      float o1 = y1, o2 = y2;
+      if (head < nq + nkv) {
+        const float ang = (float)pos * inv_freq[i];
+        const float co = bf16r(cosf(ang)), si = bf16r(sinf(ang));
+        o1 = bf16r(y1 * co) + bf16r(-y2 * si);
+        o2 = bf16r(y2 * co) + bf16r(y1 * si);
+      }
+      uint16_t *dst = nullptr;
+      if (head < nq)
+        dst = q_out + (size_t)head * hd;
+      else if (pos_ok)
+        dst = head < nq + nkv ? kc + ((size_t)(head - nq) * max_seq + pos) * hd
+                              : vc + ((size_t)(head - nq - nkv) * max_seq + pos) * hd;
+      if (dst != nullptr) {
+        dst[i] = f32_to_bf16(o1);
+        dst[i + half] = f32_to_bf16(o2);
+      }
+    }
+  }
+}
+
+// (value, index) order of torch.argmax: NaN above every number (the first NaN wins), then
+// the larger value, then the lower index.
+__device__ __forceinline__ bool argmax_better(float v, int i, float bv, int bi) {
+  const bool nv = v != v, nb = bv != bv;
+  if (nv != nb) return nv;
+  if (nv || v == bv) return i < bi;
+  return v > bv;
+}
+
+__device__ __forceinline__ void argmax_wave(float &v, int &i) {
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(v, o, kWave);
+    const int oi = __shfl_xor(i, o, kWave);
+    if (argmax_better(ov, oi, v, i)) {
+      v = ov;
+      i = oi;
+    }
+  }
+}
+
+// head_logits: r = x + residual, xn = rmsnorm(r) per workgroup (the final norm), logits =
+// W xn (bf16, rows (n, n + 1) per wave), and each workgroup's best (value, index) to cand.
+__global__ void __launch_bounds__(kNormThreads)
+head_logits_kernel(const uint16_t *__restrict__ W, const uint16_t *__restrict__ x,
+                   const uint16_t *__restrict__ res, const uint16_t *__restrict__ nw, float eps, int N,
+                   int K, uint16_t *__restrict__ logits, float *__restrict__ cand_v,
+                   int32_t *__restrict__ cand_i) {
+  __shared__ __attribute__((aligned(16))) uint16_t s_x[kFusedMaxH];
+  __shared__ float s_part[kNormThreads / kWave];
+  __shared__ float s_bv[kGemvWaves];
+  __shared__ int s_bi[kGemvWaves];
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
+  const int gw = blockIdx.x * kGemvWaves + wave;
+  const int nwv = gridDim.x * kGemvWaves;
+  const int nchunk = K / 512;
+  uint4 a[kGemv1Chunks], b[kGemv1Chunks];
+  const int f0 = gw * 2;
+  if (f0 < N) {
+    const int f1 = f0 + 1 < N ? f0 + 1 : f0;
+    gemv1_load8(a, W + (size_t)f0 * K + lane * 8, 0, nchunk);
+    gemv1_load8(b, W + (size_t)f1 * K + lane * 8, 0, nchunk);
+  }
+  rmsnorm_row<kFusedChunks>(x, res, nw, eps, K, nullptr, s_x, s_part);
+  __syncthreads();
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int n0 = f0; n0 < N; n0 += nwv * 2) {
+    const int n1 = n0 + 1 < N ? n0 + 1 : n0;
+    float acc0, acc1;
+    gemv1_pair(W + (size_t)n0 * K + lane * 8, W + (size_t)n1 * K + lane * 8, s_x + lane * 8, nchunk,
+               a, b, n0 == f0, acc0, acc1);
+    acc0 = wave_sum(acc0);
+    acc1 = wave_sum(acc1);
+    const float y0 = bf16r(acc0), y1 = bf16r(acc1);
+    if (argmax_better(y0, n0, bv, bi)) {
+      bv = y0;
+      bi = n0;
+    }
+    if (n1 != n0 && argmax_better(y1, n1, bv, bi)) {
+      bv = y1;
+      bi = n1;
+    }
+    if (lane == 0) {
+      logits[n0] = f32_to_bf16(acc0);
+      if (n1 != n0) logits[n1] = f32_to_bf16(acc1);
+    }
+  }
+  if (lane == 0) {
+    s_bv[wave] = bv;
+    s_bi[wave] = bi;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < kGemvWaves; ++w)
+      if (argmax_better(s_bv[w], s_bi[w], bv, bi)) {
+        bv = s_bv[w];
+        bi = s_bi[w];
+      }
+    cand_v[blockIdx.x] = bv;
+    cand_i[blockIdx.x] = bi;
+  }
+}
+
+// One workgroup: the best of the n candidates is the token; when given,
+// gen[*gen_ctr] = token (if the index is in [0, gen_cap)), *gen_ctr += 1, *pos += 1.
+// (A second launch is cheaper here than a device-scope fence per workgroup of the head.)
+__global__ void __launch_bounds__(kNormThreads)
+argmax_finish_kernel(const float *__restrict__ cand_v, const int32_t *__restrict__ cand_i, int n,
+                     int64_t *__restrict__ token, int64_t *__restrict__ gen, int64_t gen_cap,
+                     int64_t *__restrict__ gen_ctr, int32_t *__restrict__ pos) {
+  __shared__ float s_bv[kGemvWaves];
+  __shared__ int s_bi[kGemvWaves];
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int g = threadIdx.x; g < n; g += kNormThreads)
+    if (argmax_better(cand_v[g], cand_i[g], bv, bi)) {
+      bv = cand_v[g];
+      bi = cand_i[g];
+    }
+  argmax_wave(bv, bi);
+  if (lane == 0) {
+    s_bv[wave] = bv;
+    s_bi[wave] = bi;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < kGemvWaves; ++w)
+      if (argmax_better(s_bv[w], s_bi[w], bv, bi)) {
+        bv = s_bv[w];
+        bi = s_bi[w];
+      }
+    *token = bi;
+    if (gen_ctr != nullptr) {
+      const int64_t c = *gen_ctr;
+      if (gen != nullptr && c >= 0 && c < gen_cap) gen[c] = bi;
+      *gen_ctr = c + 1;
+    }
+    if (pos != nullptr) *pos += 1;
+  }
+}
+
 }  // namespace
 }  // namespace moe
 
@@ -273,9 +659,13 @@ extern "C" int moe_add_rmsnorm_bf16(const void *x, const void *residual_in, cons
   MOE_REQUIRE(((uintptr_t)x | (uintptr_t)weight | (uintptr_t)out | (uintptr_t)residual_in |
                (uintptr_t)residual_out) % 16 == 0,
               "tensors must be 16-byte aligned");
-  hipLaunchKernelGGL(moe::add_rmsnorm_kernel, dim3((unsigned)T), dim3(moe::kNormThreads), 0,
-                     (hipStream_t)stream, (const uint16_t *)x, (const uint16_t *)residual_in,
-                     (const uint16_t *)weight, eps, H, (uint16_t *)residual_out, (uint16_t *)out);
+  // Chunks per thread: the smallest power of two with 256 threads x 8 values x CH >= H.
+  const int chunks = (H + moe::kNormThreads * 8 - 1) / (moe::kNormThreads * 8);
+  auto kern = chunks <= 1 ? moe::add_rmsnorm_kernel<1> : chunks <= 2 ? moe::add_rmsnorm_kernel<2>
+            : chunks <= 4 ? moe::add_rmsnorm_kernel<4> : moe::add_rmsnorm_kernel<8>;
+  hipLaunchKernelGGL(kern, dim3((unsigned)T), dim3(moe::kNormThreads), 0, (hipStream_t)stream,
+                     (const uint16_t *)x, (const uint16_t *)residual_in, (const uint16_t *)weight,
+                     eps, H, (uint16_t *)residual_out, (uint16_t *)out);
   MOE_LAUNCH_CHECK();
   return MOE_STATUS_OK;
 }
@@ -284,11 +674,13 @@ extern "C" int moe_rope_kv_bf16(const void *qkv, int64_t T, int32_t n_q_heads, i
                                 int32_t head_dim, const void *inv_freq_f32, const void *pos0_i32,
                                 int64_t max_seq, void *q_out, void *k_cache, void *v_cache,
                                 void *stream) {
-  MOE_REQUIRE(T >= 0 && n_q_heads > 0 && n_kv_heads > 0 && head_dim > 0 && head_dim % 2 == 0 &&
-                  max_seq > 0,
-              "bad sizes");
+  MOE_REQUIRE(T >= 0 && n_q_heads > 0 && n_kv_heads > 0 && max_seq > 0, "bad sizes");
+  MOE_REQUIRE(head_dim > 0 && head_dim % 16 == 0 && head_dim / 2 <= moe::kRopeMaxHalf,
+              "head dim must be a multiple of 16 up to %d (got %d)", 2 * moe::kRopeMaxHalf, head_dim);
   if (T == 0) return MOE_STATUS_OK;
   MOE_REQUIRE(qkv && inv_freq_f32 && pos0_i32 && q_out && k_cache && v_cache, "null pointer");
+  MOE_REQUIRE(((uintptr_t)qkv | (uintptr_t)q_out | (uintptr_t)k_cache | (uintptr_t)v_cache) % 16 == 0,
+              "q/k/v and cache tensors must be 16-byte aligned");
   hipLaunchKernelGGL(moe::rope_kv_kernel, dim3((unsigned)T), dim3(moe::kRopeThreads), 0,
                      (hipStream_t)stream, (const uint16_t *)qkv, n_q_heads, n_kv_heads, head_dim,
                      (const float *)inv_freq_f32, (const int32_t *)pos0_i32, max_seq,
@@ -310,7 +702,8 @@ extern "C" int moe_attention_bf16(const void *q, const void *k_cache, const void
               moe::kAttnMaxKeys);
   if (T == 0) return MOE_STATUS_OK;
   MOE_REQUIRE(q && k_cache && v_cache && pos0_i32 && out, "null pointer");
-  MOE_REQUIRE(((uintptr_t)k_cache | (uintptr_t)v_cache) % 16 == 0, "KV cache must be 16-byte aligned");
+  MOE_REQUIRE(((uintptr_t)q | (uintptr_t)k_cache | (uintptr_t)v_cache) % 16 == 0,
+              "q and the KV cache must be 16-byte aligned");
   hipLaunchKernelGGL(moe::attention_kernel, dim3((unsigned)n_q_heads, (unsigned)T),
                      dim3(moe::kAttnThreads), 0, (hipStream_t)stream, (const uint16_t *)q,
                      (const uint16_t *)k_cache, (const uint16_t *)v_cache, n_q_heads, n_kv_heads,
@@ -335,11 +728,76 @@ extern "C" int moe_gemv_bf16(const void *weight, const void *x, int64_t T, int32
   const uint16_t *w = (const uint16_t *)weight, *xx = (const uint16_t *)x;
   uint16_t *yy = (uint16_t *)y;
   switch (T) {
-    case 1: hipLaunchKernelGGL(moe::gemv_kernel<1>, dim3(grid), dim3(moe::kGemvThreads), 0, s, w, xx, N, K, yy); break;
+    case 1: hipLaunchKernelGGL(moe::gemv1_kernel, dim3(grid), dim3(moe::kGemvThreads), 0, s, w, xx, N, K, yy); break;
     case 2: hipLaunchKernelGGL(moe::gemv_kernel<2>, dim3(grid), dim3(moe::kGemvThreads), 0, s, w, xx, N, K, yy); break;
     case 3: hipLaunchKernelGGL(moe::gemv_kernel<3>, dim3(grid), dim3(moe::kGemvThreads), 0, s, w, xx, N, K, yy); break;
     default: hipLaunchKernelGGL(moe::gemv_kernel<4>, dim3(grid), dim3(moe::kGemvThreads), 0, s, w, xx, N, K, yy); break;
   }
+  MOE_LAUNCH_CHECK();
+  return MOE_STATUS_OK;
+}
+
+namespace {
+int gemv1_grid(int64_t waves) {
+  int64_t grid = (waves + moe::kGemvWaves - 1) / moe::kGemvWaves;
+  const int64_t cap = (int64_t)moe::device_cu_count() * 4;
+  return (int)(grid > cap ? cap : grid);
+}
+}  // namespace
+
+extern "C" int moe_qkv_rope_bf16(const void *weight, const void *x, const void *x_row_i64,
+                                 int64_t x_rows, const void *residual, const void *norm_weight,
+                                 float eps, int32_t H, int32_t n_q_heads, int32_t n_kv_heads,
+                                 int32_t head_dim, const void *inv_freq_f32, const void *pos0_i32,
+                                 int64_t max_seq, void *residual_out, void *q_out, void *k_cache,
+                                 void *v_cache, void *stream) {
+  MOE_REQUIRE(H > 0 && H % 512 == 0 && H <= moe::kFusedMaxH,
+              "hidden size must be a positive multiple of 512 up to %d (got %d)", moe::kFusedMaxH, H);
+  MOE_REQUIRE(n_q_heads > 0 && n_kv_heads > 0 && head_dim > 0 && head_dim % 2 == 0 && max_seq > 0 &&
+                  x_rows > 0,
+              "bad sizes");
+  MOE_REQUIRE(weight && x && norm_weight && inv_freq_f32 && pos0_i32 && q_out && k_cache && v_cache,
+              "null pointer");
+  MOE_REQUIRE(((uintptr_t)weight | (uintptr_t)x | (uintptr_t)residual | (uintptr_t)norm_weight |
+               (uintptr_t)residual_out) % 16 == 0,
+              "weight, x, residual and norm tensors must be 16-byte aligned");
+  const int64_t pairs = (int64_t)(n_q_heads + 2 * n_kv_heads) * (head_dim / 2);
+  hipLaunchKernelGGL(moe::qkv_rope_kernel, dim3((unsigned)gemv1_grid(pairs)), dim3(moe::kNormThreads),
+                     0, (hipStream_t)stream, (const uint16_t *)weight, (const uint16_t *)x,
+                     (const int64_t *)x_row_i64, x_rows, (const uint16_t *)residual,
+                     (const uint16_t *)norm_weight, eps, H, n_q_heads, n_kv_heads, head_dim,
+                     (const float *)inv_freq_f32, (const int32_t *)pos0_i32, max_seq,
+                     (uint16_t *)residual_out, (uint16_t *)q_out, (uint16_t *)k_cache,
+                     (uint16_t *)v_cache);
+  MOE_LAUNCH_CHECK();
+  return MOE_STATUS_OK;
+}
+
+extern "C" int moe_head_argmax_bf16(const void *weight, const void *x, const void *residual,
+                                    const void *norm_weight, float eps, int32_t N, int32_t K,
+                                    void *logits, void *cand_ws, int64_t cand_ws_bytes,
+                                    void *token_i64, void *gen_i64, int64_t gen_cap,
+                                    void *gen_ctr_i64, void *pos_i32, void *stream) {
+  MOE_REQUIRE(K > 0 && K % 512 == 0 && K <= moe::kFusedMaxH,
+              "K must be a positive multiple of 512 up to %d (got %d)", moe::kFusedMaxH, K);
+  MOE_REQUIRE(N > 0, "N must be positive");
+  MOE_REQUIRE(weight && x && norm_weight && logits && cand_ws && token_i64, "null pointer");
+  MOE_REQUIRE(cand_ws_bytes >= 8, "candidate workspace must hold at least one entry (8 bytes)");
+  MOE_REQUIRE(((uintptr_t)weight | (uintptr_t)x | (uintptr_t)residual | (uintptr_t)norm_weight) % 16 == 0,
+              "weight, x, residual and norm tensors must be 16-byte aligned");
+  MOE_REQUIRE((uintptr_t)cand_ws % 4 == 0, "candidate workspace must be 4-byte aligned");
+  int grid = gemv1_grid((N + 1) / 2);
+  if (grid > cand_ws_bytes / 8) grid = (int)(cand_ws_bytes / 8);
+  float *cand_v = (float *)cand_ws;
+  int32_t *cand_i = (int32_t *)((char *)cand_ws + (size_t)grid * 4);
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(moe::head_logits_kernel, dim3((unsigned)grid), dim3(moe::kNormThreads), 0, s,
+                     (const uint16_t *)weight, (const uint16_t *)x, (const uint16_t *)residual,
+                     (const uint16_t *)norm_weight, eps, N, K, (uint16_t *)logits, cand_v, cand_i);
+  MOE_LAUNCH_CHECK();
+  hipLaunchKernelGGL(moe::argmax_finish_kernel, dim3(1), dim3(moe::kNormThreads), 0, s, cand_v,
+                     cand_i, grid, (int64_t *)token_i64, (int64_t *)gen_i64, gen_cap,
+                     (int64_t *)gen_ctr_i64, (int32_t *)pos_i32);
   MOE_LAUNCH_CHECK();
   return MOE_STATUS_OK;
 }

@@ -140,6 +140,7 @@ class NativeDecoder:
         self.scaling = float(s.head_dim ** -0.5)
         self.moe = moe if moe is not None else self._moe_resident
         self._moe_bufs = {}
+        self._sb = None  # single-token step buffers
 
     # ------------------------------------------------------------------ pieces
     def _stream(self) -> int:
@@ -216,6 +217,81 @@ class NativeDecoder:
             h = h_new
         self.pos += T
         return self._linear(self.w.lm_head, x1[T - 1:T].contiguous())
+
+    # ------------------------------------------------------------------ decode step
+    def fused_step_supported(self) -> bool:
+        """Whether the shape fits the fused single-token kernels (hidden and the attention
+        width multiples of 512, hidden up to 8192)."""
+        s = self.s
+        return (s.hidden % 512 == 0 and s.hidden <= 8192 and (s.n_heads * s.head_dim) % 512 == 0
+                and s.head_dim % 2 == 0)
+
+    def _step_buffers(self) -> dict:
+        if self._sb is None:
+            s, d = self.s, self.dev
+            bf = dict(dtype=torch.bfloat16, device=d)
+            cu = torch.cuda.get_device_properties(d).multi_processor_count
+            self._sb = {
+                "h": torch.empty((1, s.hidden), **bf),        # layer input (residual stream)
+                "resid": torch.empty((1, s.hidden), **bf),    # after attention
+                "x2": torch.empty((1, s.hidden), **bf),       # post-attention norm (MoE input)
+                "y": torch.empty((1, s.hidden), **bf),        # o_proj output
+                "q": torch.empty((1, s.n_heads * s.head_dim), **bf),
+                "a": torch.empty((1, s.n_heads * s.head_dim), **bf),
+                "logits": torch.empty((1, s.vocab), **bf),
+                "cand": torch.empty((8 * 4 * cu,), dtype=torch.uint8, device=d),
+            }
+        return self._sb
+
+    def decode_step(self, tok: torch.Tensor, gen: Optional[torch.Tensor] = None,
+                    gen_ctr: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """One generated token through the stack: ``tok`` (device int64 [1]) at the current
+        position; the greedy next token is written back into ``tok``, and with ``gen`` /
+        ``gen_ctr`` (device int64) stored at gen[gen_ctr] before gen_ctr += 1; the position
+        advances by one.  Returns the logits [1, V] (a buffer that the next step reuses).
+
+        Per layer four dense launches around the MoE block: norm + q/k/v + rotary + cache
+        write (moe_qkv_rope_bf16), attention, o_proj, residual + post-attention norm; then
+        the final norm, lm_head and argmax with the step's bookkeeping (moe_head_argmax_bf16,
+        two launches).  The results are bit-identical to forward() followed by argmax."""
+        if not self.fused_step_supported():
+            logits = self.forward(tok)
+            nxt = logits.argmax(dim=-1)
+            tok.copy_(nxt)
+            if gen is not None and gen_ctr is not None:
+                gen.index_copy_(0, gen_ctr.clamp(0, gen.numel() - 1), nxt)
+                gen_ctr.add_(1)
+            return logits
+        s, b, st, lib = self.s, self._step_buffers(), self._stream(), self.lib
+        nq, nkv, hd, H = s.n_heads, s.n_kv_heads, s.head_dim, s.hidden
+        x, x_row, x_rows, res = self.w.embed, tok.data_ptr(), s.vocab, None
+        m = None
+        for l, lw in enumerate(self.w.layers):
+            kc, vc = self.k_cache[l], self.v_cache[l]
+            _lib.check(lib.moe_qkv_rope_bf16(
+                lw.qkv.data_ptr(), x.data_ptr(), x_row, x_rows, res, lw.input_norm.data_ptr(),
+                s.rms_eps, H, nq, nkv, hd, self.inv_freq.data_ptr(), self.pos.data_ptr(),
+                self.max_seq, b["h"].data_ptr(), b["q"].data_ptr(), kc.data_ptr(), vc.data_ptr(),
+                st), "qkv_rope")
+            _lib.check(lib.moe_attention_bf16(b["q"].data_ptr(), kc.data_ptr(), vc.data_ptr(), 1,
+                                              nq, nkv, hd, self.pos.data_ptr(), self.max_seq,
+                                              self.scaling, b["a"].data_ptr(), st), "attention")
+            _lib.check(lib.moe_gemv_bf16(lw.o_proj.data_ptr(), b["a"].data_ptr(), 1, H, nq * hd,
+                                         b["y"].data_ptr(), st), "o_proj")
+            _lib.check(lib.moe_add_rmsnorm_bf16(b["y"].data_ptr(), b["h"].data_ptr(),
+                                                lw.post_norm.data_ptr(), s.rms_eps, 1, H,
+                                                b["resid"].data_ptr(), b["x2"].data_ptr(), st),
+                       "post-attention norm")
+            m = self.moe(l, b["x2"])
+            x, x_row, x_rows, res = m, None, 1, b["resid"].data_ptr()
+        gen_p = gen.data_ptr() if gen is not None else None
+        ctr_p = gen_ctr.data_ptr() if gen_ctr is not None else None
+        _lib.check(lib.moe_head_argmax_bf16(
+            self.w.lm_head.data_ptr(), m.data_ptr(), b["resid"].data_ptr(),
+            self.w.final_norm.data_ptr(), s.rms_eps, s.vocab, H, b["logits"].data_ptr(),
+            b["cand"].data_ptr(), b["cand"].numel(), tok.data_ptr(), gen_p,
+            0 if gen is None else gen.numel(), ctr_p, self.pos.data_ptr(), st), "lm_head + argmax")
+        return b["logits"]
 
     def reset(self) -> None:
         self.pos.zero_()

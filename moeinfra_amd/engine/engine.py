@@ -164,12 +164,7 @@ class InferenceEngine:
         kc, vc = dec.k_cache.clone(), dec.v_cache.clone()
 
         def body():
-            logits = dec.forward(self._tok)
-            nxt = logits.argmax(dim=-1)
-            self._tok.copy_(nxt)
-            self._gen.index_copy_(0, self._ctr, nxt)
-            self._ctr.add_(1)
-            return logits
+            return dec.decode_step(self._tok, self._gen, self._ctr)
 
         side = torch.cuda.Stream(self.device)
         side.wait_stream(torch.cuda.current_stream(self.device))
@@ -209,14 +204,15 @@ class InferenceEngine:
             self._ctr.add_(1)
             for _ in range(1, max_new_tokens):
                 self._graph.replay()
-            self._last_logits = self._graph_logits.reshape(1, 1, -1)
+            self._last_logits = self._graph_logits.reshape(1, 1, -1).clone()
             return [int(v) for v in self._gen[:max_new_tokens].tolist()]
-        tok = first
-        gen = [tok]
+        # Eager steps: the same decode_step as the graph body, one launch sequence per token.
+        tok = first.clone()
+        gen = torch.zeros((max_new_tokens,), dtype=torch.long, device=self.device)
+        ctr = torch.ones((1,), dtype=torch.long, device=self.device)
+        gen[0:1].copy_(first)
         logits = next_token_logits
         for _ in range(1, max_new_tokens):
-            logits = dec.forward(tok)
-            tok = logits.argmax(dim=-1)
-            gen.append(tok)
-        self._last_logits = logits.reshape(1, 1, -1)
-        return [int(v) for v in torch.cat(gen).tolist()]
+            logits = dec.decode_step(tok, gen, ctr)
+        self._last_logits = logits.reshape(1, 1, -1).clone()
+        return [int(v) for v in gen.tolist()]

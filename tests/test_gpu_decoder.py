@@ -128,6 +128,149 @@ def test_gemv(cuda_device, T, N, K):
     assert u.max() <= 1 and (u > 0).mean() < 0.05
 
 
+# --------------------------------------------------------------------------- fused step
+def _stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _unfused_norm(lib, x, res, w, eps=1e-5):
+    out = torch.empty_like(x)
+    r_out = torch.empty_like(x)
+    _lib_check(lib.moe_add_rmsnorm_bf16(x.data_ptr(), 0 if res is None else res.data_ptr(),
+                                        w.data_ptr(), eps, x.shape[0], x.shape[1], r_out.data_ptr(),
+                                        out.data_ptr(), _stream()), "norm")
+    return r_out, out
+
+
+def _unfused_gemv(lib, W, x):
+    y = torch.empty((x.shape[0], W.shape[0]), dtype=torch.bfloat16, device=x.device)
+    _lib_check(lib.moe_gemv_bf16(W.data_ptr(), x.data_ptr(), x.shape[0], W.shape[0], W.shape[1],
+                                 y.data_ptr(), _stream()), "gemv")
+    return y
+
+
+def _lib_check(rc, what):
+    from moeinfra_amd import _lib
+
+    _lib.check(rc, what)
+
+
+@pytest.mark.parametrize("H,nq,nkv,hd,pos,row,with_res", [
+    (4096, 32, 8, 128, 41, 7, True),     # Mixtral layer > 0
+    (4096, 32, 8, 128, 0, 3, False),     # Mixtral layer 0: embedding row, no residual
+    (512, 8, 2, 64, 13, -5, False),      # row ids outside the table clamp (to 0)
+    (1024, 4, 4, 128, 63, 99, True),     # ... and to the last row
+])
+def test_qkv_rope_fused_matches_unfused(cuda_device, H, nq, nkv, hd, pos, row, with_res):
+    """norm + q/k/v projection + rotary + cache write in one launch == the three kernels."""
+    from moeinfra_amd import _lib
+    from moeinfra_amd.engine.decoder import MixtralShape, rope_inv_freq
+
+    lib = _lib.lib()
+    rows, max_seq = 20, 64
+    dev = cuda_device
+    table = _bf16((rows, H), 11).to(dev)
+    res = _bf16((1, H), 12).to(dev) if with_res else None
+    nw = _bf16((H,), 13, 0.5).to(dev)
+    W = _bf16(((nq + 2 * nkv) * hd, H), 14, 0.02).to(dev)
+    inv = rope_inv_freq(MixtralShape(head_dim=hd)).to(dev)
+    p0 = torch.tensor([pos], dtype=torch.int32, device=dev)
+    rid = torch.tensor([row], dtype=torch.int64, device=dev)
+    caches = [torch.zeros((nkv, max_seq, hd), dtype=torch.bfloat16, device=dev) for _ in range(4)]
+    q_f = torch.empty((1, nq * hd), dtype=torch.bfloat16, device=dev)
+    h_f = torch.empty((1, H), dtype=torch.bfloat16, device=dev)
+    _lib.check(lib.moe_qkv_rope_bf16(W.data_ptr(), table.data_ptr(), rid.data_ptr(), rows,
+                                     None if res is None else res.data_ptr(), nw.data_ptr(), 1e-5, H,
+                                     nq, nkv, hd, inv.data_ptr(), p0.data_ptr(), max_seq,
+                                     h_f.data_ptr(), q_f.data_ptr(), caches[0].data_ptr(),
+                                     caches[1].data_ptr(), _stream()), "qkv_rope")
+    x = table[min(max(row, 0), rows - 1)][None].contiguous()
+    h_u, xn = _unfused_norm(lib, x, res, nw)
+    qkv = _unfused_gemv(lib, W, xn)
+    q_u = torch.empty_like(q_f)
+    _lib.check(lib.moe_rope_kv_bf16(qkv.data_ptr(), 1, nq, nkv, hd, inv.data_ptr(), p0.data_ptr(),
+                                    max_seq, q_u.data_ptr(), caches[2].data_ptr(),
+                                    caches[3].data_ptr(), _stream()), "rope")
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(bits(h_f), bits(h_u))
+    np.testing.assert_array_equal(bits(q_f), bits(q_u))
+    np.testing.assert_array_equal(bits(caches[0]), bits(caches[2]))   # k rows, others zero
+    np.testing.assert_array_equal(bits(caches[1]), bits(caches[3]))   # v rows
+    assert caches[0][:, pos].abs().sum() > 0 and not caches[0][:, :pos].any()
+
+
+def test_head_argmax(cuda_device):
+    """final norm + lm_head + argmax + step bookkeeping: logits equal the unfused kernels,
+    the token is torch.argmax of them, ties go to the lower index, and gen[ctr] is written
+    only inside gen_cap while ctr and pos always advance."""
+    from moeinfra_amd import _lib
+
+    lib = _lib.lib()
+    dev = cuda_device
+    V, H = 32000, 4096
+    x = _bf16((1, H), 32).to(dev)
+    res = _bf16((1, H), 33).to(dev)
+    nw = torch.ones((H,), dtype=torch.bfloat16, device=dev)
+    _, xn0 = _unfused_norm(lib, x, res, nw)
+    W = _bf16((V, H), 31, 0.02).to(dev)
+    # rows 777 and 20000 equal and aligned with the normalised input: a tie at the maximum
+    W[777] = (xn0[0].float().sign() * 0.05).to(torch.bfloat16)
+    W[20000] = W[777]
+    logits = torch.empty((1, V), dtype=torch.bfloat16, device=dev)
+    cu = torch.cuda.get_device_properties(dev).multi_processor_count
+    cand = torch.empty((8 * 4 * cu,), dtype=torch.uint8, device=dev)
+    tok = torch.full((1,), -1, dtype=torch.int64, device=dev)
+    gen = torch.full((3,), -1, dtype=torch.int64, device=dev)
+    gctr = torch.tensor([1], dtype=torch.int64, device=dev)
+    pos = torch.tensor([9], dtype=torch.int32, device=dev)
+    for cand_bytes in (cand.numel(), 8 * 3):  # full grid, then only three workgroups
+        _lib.check(lib.moe_head_argmax_bf16(W.data_ptr(), x.data_ptr(), res.data_ptr(), nw.data_ptr(),
+                                            1e-5, V, H, logits.data_ptr(), cand.data_ptr(),
+                                            cand_bytes, tok.data_ptr(),
+                                            gen.data_ptr(), gen.numel(), gctr.data_ptr(),
+                                            pos.data_ptr(), _stream()), "head")
+        torch.cuda.synchronize()
+        _, xn = _unfused_norm(lib, x, res, nw)
+        want = _unfused_gemv(lib, W, xn)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(bits(logits), bits(want))
+        lg = want.float().cpu()[0]
+        assert float(lg[777]) == float(lg[20000]) == float(lg.max())
+        assert int(tok.item()) == int(torch.argmax(lg)) == 777
+    assert gen.tolist() == [-1, 777, 777] and int(gctr.item()) == 3 and int(pos.item()) == 11
+    # gen_ctr at the capacity: nothing written, the counter still advances
+    _lib.check(lib.moe_head_argmax_bf16(W.data_ptr(), x.data_ptr(), res.data_ptr(), nw.data_ptr(),
+                                        1e-5, V, H, logits.data_ptr(), cand.data_ptr(), cand.numel(),
+                                        tok.data_ptr(), gen.data_ptr(), gen.numel(),
+                                        gctr.data_ptr(), None, _stream()), "head")
+    torch.cuda.synchronize()
+    assert gen.tolist() == [-1, 777, 777] and int(gctr.item()) == 4 and int(pos.item()) == 11
+
+
+def test_decode_step_matches_forward(cuda_device):
+    """The fused decode step == forward() + argmax, bit for bit, over several positions."""
+    from moeinfra_amd.engine.decoder import NativeDecoder
+
+    w = _small_engine_weights(cuda_device)
+    prompt = torch.randint(0, w.shape.vocab, (7,), generator=torch.Generator().manual_seed(8))
+    a = NativeDecoder(w, 32, cuda_device)
+    b = NativeDecoder(w, 32, cuda_device)
+    assert a.fused_step_supported()
+    la = a.forward(prompt.to(cuda_device))
+    lb = b.forward(prompt.to(cuda_device))
+    tok = la.argmax(dim=-1)
+    tok_b = tok.clone()
+    for _ in range(5):
+        lf = a.decode_step(tok)                       # writes the next token into tok
+        lu = b.forward(tok_b)
+        np.testing.assert_array_equal(bits(lf), bits(lu))
+        tok_b = lu.argmax(dim=-1)
+        assert int(tok.item()) == int(tok_b.item())
+    assert int(a.pos.item()) == int(b.pos.item()) == 12
+    np.testing.assert_array_equal(bits(a.k_cache), bits(b.k_cache))
+    np.testing.assert_array_equal(bits(a.v_cache), bits(b.v_cache))
+
+
 # --------------------------------------------------------------------------- engine
 def _small_shape():
     from moeinfra_amd.engine.decoder import MixtralShape
