@@ -20,14 +20,23 @@ constexpr int kNormMaxChunks = 8;  // 8-value chunks per thread: H <= 16384
 
 __device__ __forceinline__ float bf16r(float v) { return bf16_to_f32(f32_to_bf16(v)); }
 
+// Workgroup barrier that orders LDS only: a workgroup fence on all address spaces would
+// also wait for the wave's outstanding global loads (s_waitcnt vmcnt(0)), which in the
+// fused kernels are the weight rows still streaming in.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 __device__ __forceinline__ float block_sum(float v, float *s_part) {
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
   v = wave_sum(v);
   if (lane == 0) s_part[wave] = v;
-  __syncthreads();
+  lds_barrier();
   float t = 0.0f;
   for (int w = 0; w < (int)(blockDim.x >> 6); ++w) t += s_part[w];
-  __syncthreads();
+  lds_barrier();
   return t;
 }
 
@@ -36,28 +45,38 @@ __device__ __forceinline__ float block_sum(float v, float *s_part) {
 // out = bf16(w * bf16(r * inv)), inv = 1 / sqrt(mean(r^2) + eps) from fp32 statistics.
 // Thread t takes the 8-value chunks (t + i * kNormThreads) * 8 for i < CH (chunks past H
 // load the last chunk again, in bounds, and count for nothing), so every caller with the
-// same H sums in the same order.  All loads are issued before any is used.  `out` may be LDS.
+// same H sums in the same order.  Split in two so that a caller can issue other loads
+// between them: norm_load issues every load; norm_finish waits for them only (vmcnt is in
+// order, so loads issued after norm_load are not waited for).  `out` may point to LDS.
 template <int CH>
-__device__ __forceinline__ void rmsnorm_row(const uint16_t *x, const uint16_t *res, const uint16_t *w,
-                                            float eps, int H, uint16_t *res_out, uint16_t *out,
-                                            float *s_part) {
-  uint4 xv[CH], rs[CH], wv[CH];
-  const bool has_res = res != nullptr;
-  const uint16_t *rp = has_res ? res : x;  // without a residual: loads of x, unused
+struct NormRegs {
+  uint4 x[CH], r[CH], w[CH];
+};
+
+// RES: whether a residual is added (a compile-time choice, so that no load sits behind a
+// branch, where the compiler would sink it past later loads).
+template <int CH, bool RES>
+__device__ __forceinline__ void norm_load(NormRegs<CH> &g, const uint16_t *x, const uint16_t *res,
+                                          const uint16_t *w, int H) {
 #pragma unroll
   for (int i = 0; i < CH; ++i) {
     int c = (threadIdx.x + i * kNormThreads) * 8;
     c = c < H ? c : H - 8;
-    wv[i] = *reinterpret_cast<const uint4 *>(w + c);
-    xv[i] = *reinterpret_cast<const uint4 *>(x + c);
-    rs[i] = *reinterpret_cast<const uint4 *>(rp + c);
+    g.w[i] = *reinterpret_cast<const uint4 *>(w + c);
+    g.x[i] = *reinterpret_cast<const uint4 *>(x + c);
+    if (RES) g.r[i] = *reinterpret_cast<const uint4 *>(res + c);
   }
+}
+
+template <int CH, bool RES>
+__device__ __forceinline__ void norm_finish(NormRegs<CH> &g, float eps, int H, uint16_t *res_out,
+                                            uint16_t *out, float *s_part) {
   float ss = 0.0f;
 #pragma unroll
   for (int i = 0; i < CH; ++i) {
-    uint4 v = xv[i];
-    if (has_res) {
-      const uint32_t a[4] = {v.x, v.y, v.z, v.w}, b[4] = {rs[i].x, rs[i].y, rs[i].z, rs[i].w};
+    uint4 v = g.x[i];
+    if (RES) {
+      const uint32_t a[4] = {v.x, v.y, v.z, v.w}, b[4] = {g.r[i].x, g.r[i].y, g.r[i].z, g.r[i].w};
       uint32_t o[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j)
@@ -65,7 +84,7 @@ __device__ __forceinline__ void rmsnorm_row(const uint16_t *x, const uint16_t *r
                            bf16hi_to_f32(a[j]) + bf16hi_to_f32(b[j]));
       v = make_uint4(o[0], o[1], o[2], o[3]);
     }
-    xv[i] = v;
+    g.x[i] = v;
     const uint32_t a[4] = {v.x, v.y, v.z, v.w};
     float t = ss;
 #pragma unroll
@@ -80,28 +99,37 @@ __device__ __forceinline__ void rmsnorm_row(const uint16_t *x, const uint16_t *r
   for (int i = 0; i < CH; ++i) {
     const int c = (threadIdx.x + i * kNormThreads) * 8;
     if (c < H) {
-      const uint32_t a[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
-      const uint32_t g[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
+      const uint32_t a[4] = {g.x[i].x, g.x[i].y, g.x[i].z, g.x[i].w};
+      const uint32_t gw[4] = {g.w[i].x, g.w[i].y, g.w[i].z, g.w[i].w};
       uint32_t o[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        o[j] = pack_bf16x2(bf16lo_to_f32(g[j]) * bf16r(bf16lo_to_f32(a[j]) * inv),
-                           bf16hi_to_f32(g[j]) * bf16r(bf16hi_to_f32(a[j]) * inv));
-      if (res_out != nullptr) *reinterpret_cast<uint4 *>(res_out + c) = xv[i];
+        o[j] = pack_bf16x2(bf16lo_to_f32(gw[j]) * bf16r(bf16lo_to_f32(a[j]) * inv),
+                           bf16hi_to_f32(gw[j]) * bf16r(bf16hi_to_f32(a[j]) * inv));
+      if (res_out != nullptr) *reinterpret_cast<uint4 *>(res_out + c) = g.x[i];
       *reinterpret_cast<uint4 *>(out + c) = make_uint4(o[0], o[1], o[2], o[3]);
     }
   }
 }
 
-template <int CH>
+template <int CH, bool RES>
+__device__ __forceinline__ void rmsnorm_row(const uint16_t *x, const uint16_t *res, const uint16_t *w,
+                                            float eps, int H, uint16_t *res_out, uint16_t *out,
+                                            float *s_part) {
+  NormRegs<CH> g;
+  norm_load<CH, RES>(g, x, res, w, H);
+  norm_finish<CH, RES>(g, eps, H, res_out, out, s_part);
+}
+
+template <int CH, bool RES>
 __global__ void __launch_bounds__(kNormThreads)
 add_rmsnorm_kernel(const uint16_t *__restrict__ x, const uint16_t *__restrict__ res_in,
                    const uint16_t *__restrict__ w, float eps, int H,
                    uint16_t *__restrict__ res_out, uint16_t *__restrict__ out) {
   __shared__ float s_part[kNormThreads / kWave];
   const size_t base = (size_t)blockIdx.x * H;
-  rmsnorm_row<CH>(x + base, res_in ? res_in + base : nullptr, w, eps, H,
-                  res_out ? res_out + base : nullptr, out + base, s_part);
+  rmsnorm_row<CH, RES>(x + base, RES ? res_in + base : nullptr, w, eps, H,
+                       res_out ? res_out + base : nullptr, out + base, s_part);
 }
 
 constexpr int kRopeThreads = 256;
@@ -446,8 +474,7 @@ gemv1_kernel(const uint16_t *__restrict__ W, const uint16_t *__restrict__ x, int
 // One token.  Each removes a launch (about 4-5 us of dependent latency at batch 1) by doing
 // a neighbouring step inside the projection kernel, with the same arithmetic and summation
 // order as the separate kernels, so the results are bit-identical to them.
-constexpr int kFusedMaxH = 8192;
-constexpr int kFusedChunks = kFusedMaxH / (kNormThreads * 8);
+constexpr int kFusedMaxH = 8192;  // norm chunks per thread: up to 4
 static_assert(kNormThreads == kGemvThreads, "the fused kernels run the norm and the GEMV in one workgroup");
 
 // qkv_rope: r = x[row] (+ residual) -> residual_out (workgroup 0), xn = rmsnorm(r) in every
@@ -455,6 +482,7 @@ static_assert(kNormThreads == kGemvThreads, "the fused kernels run the norm and 
 // so the wave holding both outputs applies the rotary embedding (cos/sin of position pos0
 // rounded to bf16) and writes q to q_out and k, v to the cache row pos0.  The first row
 // pair's first 8 KB per row are in flight before the norm.
+template <bool RES, int CH>
 __global__ void __launch_bounds__(kNormThreads)
 qkv_rope_kernel(const uint16_t *__restrict__ W, const uint16_t *__restrict__ x,
                 const int64_t *__restrict__ x_row, int64_t x_rows, const uint16_t *__restrict__ res,
@@ -475,21 +503,23 @@ qkv_rope_kernel(const uint16_t *__restrict__ W, const uint16_t *__restrict__ x,
     w0 = W + (size_t)(head * hd + i) * H + lane * 8;
     w1 = w0 + (size_t)half * H;
   };
-  uint4 a[kGemv1Chunks], b[kGemv1Chunks];
-  const uint16_t *w0 = W, *w1 = W;
-  if (gw < pairs) {
-    rows_of(gw, w0, w1);
-    gemv1_load8(a, w0, 0, nchunk);
-    gemv1_load8(b, w1, 0, nchunk);
-  }
-  // The row id is read after the weight loads are issued (its scalar load would otherwise
-  // be waited for first).
-  __builtin_amdgcn_sched_barrier(0);
+  // The norm's loads (L2-resident, needed first) are issued before the first weight step,
+  // so that waiting for them does not wait for the weights.
   int64_t row = x_row != nullptr ? *x_row : 0;
   row = row < 0 ? 0 : (row >= x_rows ? x_rows - 1 : row);  // ids outside the table clamp
-  const uint16_t *xr = x + (size_t)row * H;
-  rmsnorm_row<kFusedChunks>(xr, res, nw, eps, H, blockIdx.x == 0 ? res_out : nullptr, s_x, s_part);
-  __syncthreads();
+  NormRegs<CH> g;
+  norm_load<CH, RES>(g, x + (size_t)row * H, res, nw, H);
+  // Unconditional (a wave past the last pair loads the last pair's rows and drops them): a
+  // conditional load here would make every later wait count it as possibly not issued,
+  // i.e. wait for the weights too.
+  uint4 a[kGemv1Chunks], b[kGemv1Chunks];
+  const uint16_t *w0 = W, *w1 = W;
+  rows_of(gw < pairs ? gw : pairs - 1, w0, w1);
+  gemv1_load8(a, w0, 0, nchunk);
+  gemv1_load8(b, w1, 0, nchunk);
+  __builtin_amdgcn_sched_barrier(0);  // keep the weight loads ahead of the norm arithmetic
+  norm_finish<CH, RES>(g, eps, H, blockIdx.x == 0 ? res_out : nullptr, s_x, s_part);
+  lds_barrier();
   const int pos = *pos0;
   const bool pos_ok = pos >= 0 && pos < max_seq;  // else the cache has no row (caller error)
   for (int p = gw; p < pairs; p += nwv) {
@@ -545,6 +575,7 @@ __device__ __forceinline__ void argmax_wave(float &v, int &i) {
 
 // head_logits: r = x + residual, xn = rmsnorm(r) per workgroup (the final norm), logits =
 // W xn (bf16, rows (n, n + 1) per wave), and each workgroup's best (value, index) to cand.
+template <bool RES, int CH>
 __global__ void __launch_bounds__(kNormThreads)
 head_logits_kernel(const uint16_t *__restrict__ W, const uint16_t *__restrict__ x,
                    const uint16_t *__restrict__ res, const uint16_t *__restrict__ nw, float eps, int N,
@@ -558,15 +589,19 @@ head_logits_kernel(const uint16_t *__restrict__ W, const uint16_t *__restrict__ 
   const int gw = blockIdx.x * kGemvWaves + wave;
   const int nwv = gridDim.x * kGemvWaves;
   const int nchunk = K / 512;
+  NormRegs<CH> g;
+  norm_load<CH, RES>(g, x, res, nw, K);
   uint4 a[kGemv1Chunks], b[kGemv1Chunks];
   const int f0 = gw * 2;
-  if (f0 < N) {
-    const int f1 = f0 + 1 < N ? f0 + 1 : f0;
-    gemv1_load8(a, W + (size_t)f0 * K + lane * 8, 0, nchunk);
-    gemv1_load8(b, W + (size_t)f1 * K + lane * 8, 0, nchunk);
+  {  // unconditional, as in qkv_rope_kernel (rows clamped to the last one)
+    const int p0 = f0 < N ? f0 : N - 1;
+    const int p1 = p0 + 1 < N ? p0 + 1 : p0;
+    gemv1_load8(a, W + (size_t)p0 * K + lane * 8, 0, nchunk);
+    gemv1_load8(b, W + (size_t)p1 * K + lane * 8, 0, nchunk);
   }
-  rmsnorm_row<kFusedChunks>(x, res, nw, eps, K, nullptr, s_x, s_part);
-  __syncthreads();
+  __builtin_amdgcn_sched_barrier(0);  // keep the weight loads ahead of the norm arithmetic
+  norm_finish<CH, RES>(g, eps, K, nullptr, s_x, s_part);
+  lds_barrier();
   float bv = -INFINITY;
   int bi = 0x7fffffff;
   for (int n0 = f0; n0 < N; n0 += nwv * 2) {
@@ -661,8 +696,11 @@ extern "C" int moe_add_rmsnorm_bf16(const void *x, const void *residual_in, cons
               "tensors must be 16-byte aligned");
   // Chunks per thread: the smallest power of two with 256 threads x 8 values x CH >= H.
   const int chunks = (H + moe::kNormThreads * 8 - 1) / (moe::kNormThreads * 8);
-  auto kern = chunks <= 1 ? moe::add_rmsnorm_kernel<1> : chunks <= 2 ? moe::add_rmsnorm_kernel<2>
-            : chunks <= 4 ? moe::add_rmsnorm_kernel<4> : moe::add_rmsnorm_kernel<8>;
+  const bool r = residual_in != nullptr;
+  auto kern = chunks <= 1 ? (r ? moe::add_rmsnorm_kernel<1, true> : moe::add_rmsnorm_kernel<1, false>)
+            : chunks <= 2 ? (r ? moe::add_rmsnorm_kernel<2, true> : moe::add_rmsnorm_kernel<2, false>)
+            : chunks <= 4 ? (r ? moe::add_rmsnorm_kernel<4, true> : moe::add_rmsnorm_kernel<4, false>)
+                          : (r ? moe::add_rmsnorm_kernel<8, true> : moe::add_rmsnorm_kernel<8, false>);
   hipLaunchKernelGGL(kern, dim3((unsigned)T), dim3(moe::kNormThreads), 0, (hipStream_t)stream,
                      (const uint16_t *)x, (const uint16_t *)residual_in, (const uint16_t *)weight,
                      eps, H, (uint16_t *)residual_out, (uint16_t *)out);
@@ -762,7 +800,11 @@ extern "C" int moe_qkv_rope_bf16(const void *weight, const void *x, const void *
                (uintptr_t)residual_out) % 16 == 0,
               "weight, x, residual and norm tensors must be 16-byte aligned");
   const int64_t pairs = (int64_t)(n_q_heads + 2 * n_kv_heads) * (head_dim / 2);
-  hipLaunchKernelGGL(moe::qkv_rope_kernel, dim3((unsigned)gemv1_grid(pairs)), dim3(moe::kNormThreads),
+  // Norm chunks per thread: 2 for H <= 4096, else 4.
+  const bool small = H <= moe::kNormThreads * 8 * 2;
+  auto kern = residual ? (small ? moe::qkv_rope_kernel<true, 2> : moe::qkv_rope_kernel<true, 4>)
+                       : (small ? moe::qkv_rope_kernel<false, 2> : moe::qkv_rope_kernel<false, 4>);
+  hipLaunchKernelGGL(kern, dim3((unsigned)gemv1_grid(pairs)), dim3(moe::kNormThreads),
                      0, (hipStream_t)stream, (const uint16_t *)weight, (const uint16_t *)x,
                      (const int64_t *)x_row_i64, x_rows, (const uint16_t *)residual,
                      (const uint16_t *)norm_weight, eps, H, n_q_heads, n_kv_heads, head_dim,
@@ -791,7 +833,10 @@ extern "C" int moe_head_argmax_bf16(const void *weight, const void *x, const voi
   float *cand_v = (float *)cand_ws;
   int32_t *cand_i = (int32_t *)((char *)cand_ws + (size_t)grid * 4);
   hipStream_t s = (hipStream_t)stream;
-  hipLaunchKernelGGL(moe::head_logits_kernel, dim3((unsigned)grid), dim3(moe::kNormThreads), 0, s,
+  const bool small = K <= moe::kNormThreads * 8 * 2;
+  auto kern = residual ? (small ? moe::head_logits_kernel<true, 2> : moe::head_logits_kernel<true, 4>)
+                       : (small ? moe::head_logits_kernel<false, 2> : moe::head_logits_kernel<false, 4>);
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(moe::kNormThreads), 0, s,
                      (const uint16_t *)weight, (const uint16_t *)x, (const uint16_t *)residual,
                      (const uint16_t *)norm_weight, eps, N, K, (uint16_t *)logits, cand_v, cand_i);
   MOE_LAUNCH_CHECK();
