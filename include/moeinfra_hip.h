@@ -181,6 +181,21 @@ int moe_layer_forward_nf4_profiled(const moe_nf4_expert_t *experts, int32_t E,
                                    void *weights_f32, void *idx_i64, void *workspace,
                                    int64_t workspace_bytes, void *const *events, void *stream);
 
+/* Single-token layer with the decoder's post-attention residual add and RMSNorm in front
+ * (engine/decoder_layer.py:37-41 feeds the MoE block post_attention_layernorm(h + attn)):
+ * r = x + residual -> residual_out, xn = moe_add_rmsnorm_bf16(r) with norm_weight, then
+ * moe_layer_forward_nf4 of xn at T = 1 -- bit-identical to that sequence, in the layer's
+ * two launches (every gate/up workgroup normalises the token itself).  No bias, no logits
+ * output.  workspace: moe_layer_norm_workspace_bytes(k, E, H, F) bytes, 256-byte aligned;
+ * H up to 8192. */
+int64_t moe_layer_norm_workspace_bytes(int32_t k, int32_t E, int32_t H, int32_t F);
+int moe_layer_forward_nf4_norm(const moe_nf4_expert_t *experts, int32_t E, const void *gate_bf16,
+                               const void *x_bf16, const void *residual_bf16,
+                               const void *norm_weight_bf16, float eps, int32_t H, int32_t F,
+                               int32_t k, void *residual_out_bf16, void *out_bf16,
+                               void *weights_f32, void *idx_i64, void *workspace,
+                               int64_t workspace_bytes, void *stream);
+
 /* ---------------------------------------------------------------- decoder (end-to-end)
  * The dense parts of a Mixtral decoder layer around the MoE block, which the reference
  * runs as Hugging Face modules (engine/engine.py:211-314 builds MixtralRMSNorm,

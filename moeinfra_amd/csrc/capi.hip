@@ -33,7 +33,17 @@ int64_t decode_route_bytes();
 int launch_decode_layer(const moe_nf4_expert_t *experts, int32_t E, const void *gate,
                         const void *bias, const void *x, int64_t T, int32_t H, int32_t F,
                         int32_t k, void *out, void *logits, void *weights, void *idx64,
-                        void *route_ws, void *h_ws, hipStream_t s, hipEvent_t *ev);
+                        void *route_ws, void *h_ws, hipStream_t s, hipEvent_t *ev,
+                        const void *norm);
+// Mirrors the layout of DecodeNorm (decode_layer.hip).
+struct DecodeNormArgs {
+  const uint16_t *res;
+  const uint16_t *w;
+  float eps;
+  uint16_t *res_out;
+  uint16_t *xs;
+};
+int64_t decode_norm_bytes();
 
 namespace {
 thread_local char g_last_error[512] = "";
@@ -159,7 +169,7 @@ int layer_forward(const moe_nf4_expert_t *experts, int32_t E, const void *gate_b
   if (decode_layer_supported(T, k, E, H, F))
     return launch_decode_layer(experts, E, gate_bf16, bias_f32, x_bf16, T, H, F, k, out_bf16,
                                logits_bf16, weights_f32, idx_i64, at<void>(workspace, w.droute),
-                               at<void>(workspace, w.h), s, ev);
+                               at<void>(workspace, w.h), s, ev, nullptr);
   if (ev) MOE_HIP_CHECK(hipEventRecord(ev[0], s));
   const bool small = route_small_supported(T, k);
   int rc;
@@ -262,4 +272,47 @@ extern "C" int moe_expert_swiglu_nf4(const moe_nf4_expert_t *expert, const void 
   if (rc != MOE_STATUS_OK) return rc;
   return moe::launch_reduce_splits(moe::at<float>(workspace, w.ypart), w.nsplit, T * (int64_t)H,
                                    (uint16_t *)y_bf16, s);
+}
+
+namespace {
+// The single-token layer with the fused norm: the layer workspace at T = 1, then one row of
+// normalised values per gate/up workgroup (at most one per CU).
+int64_t norm_ws_rows_offset(int32_t k, int32_t E, int32_t H, int32_t F) {
+  return moe::layer_ws(1, k, E, H, F).total;
+}
+}  // namespace
+
+extern "C" int64_t moe_layer_norm_workspace_bytes(int32_t k, int32_t E, int32_t H, int32_t F) {
+  if (k < 1 || E < 1 || H < 1 || F < 1) return -1;
+  return moe::align_up(norm_ws_rows_offset(k, E, H, F) +
+                       (int64_t)moe::device_cu_count() * H * 2);
+}
+
+extern "C" int moe_layer_forward_nf4_norm(const moe_nf4_expert_t *experts, int32_t E,
+                                          const void *gate_bf16, const void *x_bf16,
+                                          const void *residual_bf16, const void *norm_weight_bf16,
+                                          float eps, int32_t H, int32_t F, int32_t k,
+                                          void *residual_out_bf16, void *out_bf16,
+                                          void *weights_f32, void *idx_i64, void *workspace,
+                                          int64_t workspace_bytes, void *stream) {
+  MOE_REQUIRE(k >= 1 && E >= 1 && H >= 1 && F >= 1, "bad sizes");
+  MOE_REQUIRE(moe::decode_layer_supported(1, k, E, H, F),
+              "shape not supported by the single-token decode layer");
+  MOE_REQUIRE(x_bf16 && residual_bf16 && norm_weight_bf16 && residual_out_bf16 && out_bf16 &&
+                  weights_f32 && idx_i64 && gate_bf16,
+              "null pointer");
+  const int64_t need = moe_layer_norm_workspace_bytes(k, E, H, F);
+  MOE_REQUIRE(workspace != nullptr && workspace_bytes >= need,
+              "workspace too small: need %lld bytes, got %lld", (long long)need,
+              (long long)workspace_bytes);
+  MOE_REQUIRE(((uintptr_t)workspace % 256) == 0, "workspace must be 256-byte aligned");
+  static_assert(sizeof(moe::DecodeNormArgs) == 40, "DecodeNorm layout");
+  MOE_REQUIRE(moe::decode_norm_bytes() == (int64_t)sizeof(moe::DecodeNormArgs), "DecodeNorm layout");
+  const moe::LayerWs w = moe::layer_ws(1, k, E, H, F);
+  moe::DecodeNormArgs nrm{(const uint16_t *)residual_bf16, (const uint16_t *)norm_weight_bf16, eps,
+                          (uint16_t *)residual_out_bf16,
+                          moe::at<uint16_t>(workspace, norm_ws_rows_offset(k, E, H, F))};
+  return moe::launch_decode_layer(experts, E, gate_bf16, nullptr, x_bf16, 1, H, F, k, out_bf16,
+                                  nullptr, weights_f32, idx_i64, moe::at<void>(workspace, w.droute),
+                                  moe::at<void>(workspace, w.h), (hipStream_t)stream, nullptr, &nrm);
 }

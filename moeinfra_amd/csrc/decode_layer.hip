@@ -26,6 +26,7 @@
 // Both kernels stream 4-row tiles through the register pipeline of the 4x4x4 MFMA GEMV
 // (gemv4_core.h), with the NF4 codebook table in LDS.
 #include "gemv4_core.h"
+#include "norm_row.h"
 
 namespace moe {
 
@@ -61,6 +62,20 @@ struct DecodeRoute {
   float code2[kDecMaxSlots][16];   // w2 codebook of each active expert
 };
 static_assert(sizeof(DecodeRoute) % 16 == 0, "descriptor is copied in 16-byte words");
+
+// The post-attention residual add + RMSNorm in front of a single-token layer (the fused
+// form of the decoder's norm kernel): x is then the un-normalised attention output,
+// r = x + res goes to res_out (workgroup 0) and every workgroup normalises r itself, into
+// LDS for the gate products and into its own row of xs for the expert stream.
+struct DecodeNorm {
+  const uint16_t *res;
+  const uint16_t *w;
+  float eps;
+  uint16_t *res_out;
+  uint16_t *xs;  // [gridDim.x][H]
+};
+constexpr int kDecNormMaxH = 8192;
+constexpr int kDecNormChunks = kDecNormMaxH / (kNormThreads * 8);
 
 // The fields of DecodeRoute before code2 (a wave's private copy in the gate/up kernel).
 struct RouteHead {
@@ -256,13 +271,19 @@ struct StageQ {
   uint4 xa[NX];
 };
 
+// XREG activations from global memory or, for the fused-norm kernel, from LDS.
+__device__ __forceinline__ uint4 ld_x(gx_t p) { return ld_u4(p); }
+__device__ __forceinline__ uint4 ld_x(const uint16_t *lds_p) {
+  return *reinterpret_cast<const uint4 *>(lds_p);
+}
+
 template <int NP, int NSQ, int DEPTH, bool BC, bool XREG, bool LA, typename GrabFn,
-          typename PtrFn, typename FinishFn, typename Hook>
+          typename PtrFn, typename FinishFn, typename Hook, typename XPtr>
 __device__ __forceinline__ void stream_aligned(GrabFn &&grab, PtrFn &&set_ptrs,
                                                FinishFn &&finish, Hook &&hook,
                                                const uint32_t *tbl,
                                                const uint32_t (&lane_const)[NP], size_t arow,
-                                               float *aslot, gx_t xbase) {
+                                               float *aslot, XPtr xbase) {
   static_assert(NSQ >= 2 && NSQ <= 8, "an item's absmax block must fit one load per lane");
   static_assert(DEPTH >= 2 && DEPTH <= NSQ && NSQ % DEPTH == 0, "depth must divide NSQ");
   static_assert(!LA || DEPTH >= 3, "lookahead needs depth >= 3");
@@ -300,7 +321,7 @@ __device__ __forceinline__ void stream_aligned(GrabFn &&grab, PtrFn &&set_ptrs,
   uint4 xr[XREG ? NSQ : 1];
   if (XREG) {
 #pragma unroll
-    for (int sg = 0; sg < NSQ; ++sg) xr[sg] = ld_u4(xbase + sg * kStageVals);
+    for (int sg = 0; sg < NSQ; ++sg) xr[sg] = ld_x(xbase + sg * kStageVals);
   }
   load_abs();
   auto load = [&](StageQ<NP, NX> &st, int sg) {
@@ -570,13 +591,14 @@ __device__ __forceinline__ RouteSummary route_wave(RouteHead &rh, int32_t (&sl_e
   return RouteSummary{n_active, !multi, present};
 }
 
-template <int EMAX>
+template <int EMAX, bool NORM>
 __global__ void __launch_bounds__(kDecThreads, 1)
 decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
                      const uint16_t *__restrict__ gate, const float *__restrict__ bias, int T,
                      int H, int F, int E, int k, uint16_t *__restrict__ logits_out,
                      float *__restrict__ w_out, int64_t *__restrict__ idx_out,
-                     DecodeRoute *__restrict__ route_out, uint16_t *__restrict__ h_out) {
+                     DecodeRoute *__restrict__ route_out, uint16_t *__restrict__ h_out,
+                     const DecodeNorm nrm) {
   __shared__ __attribute__((aligned(16))) uint32_t s_tbl[kTableWords];
   __shared__ float s_part[kDecWaves][kDecMaxTokens][EMAX];
   // Codebooks of every expert: [0,16) w1, [16,32) w3, [32,48) w2 ([48,64) repeats w2).
@@ -591,12 +613,25 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
   // Single-token path: per item of the workgroup, the per-lane sums of w1 and w3 (row
   // j = lane % 4 of the tile, block lane / 4).
   __shared__ float s_raw[kRawSlots][2][kWave];
+  // NORM: the normalised token (gate products read it here) and the norm's wave sums.
+  __shared__ __attribute__((aligned(16))) uint16_t s_xn[NORM ? kDecNormMaxH : 8];
+  __shared__ float s_npart[kDecWaves];
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const bool wg0 = blockIdx.x == 0;
   if (tid == 0) s_ticket = 0;
+  // NORM: the norm's loads (x, residual, weight; L2-resident) go first, so that waiting
+  // for them does not wait for the gate rows issued after them.  Every wave loads (waves
+  // 4-7 duplicates, unused): no load behind a branch.
+  NormRegs<kDecNormChunks> ng;
+  if (NORM) {
+    norm_load<kDecNormChunks, true>(ng, x, nrm.res, nrm.w, H);
+    __builtin_amdgcn_sched_barrier(0);  // keep them ahead of the gate rows
+  }
+  // The token the expert stream reads: x, or this workgroup's row of normalised values.
+  const uint16_t *xt = NORM ? nrm.xs + (size_t)blockIdx.x * H : x;
 
   // ---- gate products on the 4x4x4 MFMA: wave w takes the 128-value chunks c = w, w + 8,
   // ... of H; lane (b = lane/4, j = lane%4) holds values 8b .. 8b+7 of a chunk of token j
@@ -608,12 +643,16 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
   const int lj = lane & 3;
   const int lb = lane >> 2;
   const int n_chunks = (H / 128 - wave + kDecWaves - 1) / kDecWaves;  // this wave's chunks
-  const gx_t xrow = (gx_t)x + (size_t)(lj < T ? lj : T - 1) * H + (size_t)wave * 128 + 8 * lb;
+  // A wave without chunks (H < 1024) still issues its first round, on chunk 0 (in bounds,
+  // unused): a load behind a branch would make every later wait count it as possibly
+  // missing, i.e. wait for the loads issued after it too.
+  const int wq = n_chunks > 0 ? wave : 0;
+  const gx_t xrow = (gx_t)x + (size_t)(lj < T ? lj : T - 1) * H + (size_t)wq * 128 + 8 * lb;
   gx_t grow[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     const int e = 4 * g + lj;
-    grow[g] = (gx_t)gate + (size_t)(e < E ? e : E - 1) * H + (size_t)wave * 128 + 8 * lb;
+    grow[g] = (gx_t)gate + (size_t)(e < E ? e : E - 1) * H + (size_t)wq * 128 + 8 * lb;
   }
   f32x4 gacc[G];
 #pragma unroll
@@ -623,12 +662,12 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
 #pragma unroll
     for (int c = 0; c < CPR; ++c) {
       const int cc = c0 + c < n_chunks ? c0 + c : 0;  // past the end: chunk 0 again, unused
-      xv[c] = ld_u4(xrow + (size_t)cc * (128 * kDecWaves));
+      if (!NORM) xv[c] = ld_u4(xrow + (size_t)cc * (128 * kDecWaves));
 #pragma unroll
       for (int g = 0; g < G; ++g) gv[c][g] = ld_u4(grow[g] + (size_t)cc * (128 * kDecWaves));
     }
   };
-  if (n_chunks > 0) load_round(0);
+  load_round(0);
   // Metadata of experts wave + 8q (wave-uniform, so the table entries are scalar loads):
   // lane l < 16 reads w1 code[l], 16..31 w3 code[l-16], 32..63 w2 code[l & 15]; lane f < 4
   // keeps stream pointer f (w1_packed, w1_absmax, w3_packed, w3_absmax).
@@ -658,10 +697,26 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
     build_table_regs<kDecThreads>(s_tbl, cst, cst);
   }
   __builtin_amdgcn_sched_barrier(0);
+  if (NORM) {
+    // r = x + res (workgroup 0 writes it), xn = rmsnorm(r) by threads 0..255 exactly as the
+    // norm kernel, into LDS (the single-token stream reads it there; other paths copy it to
+    // the workgroup's xs row first).
+    norm_finish<kDecNormChunks, true>(ng, nrm.eps, H, wg0 ? nrm.res_out : nullptr, s_xn, s_npart,
+                                      tid < kNormThreads);
+    lds_barrier();
+  }
   for (int c0 = 0; c0 < n_chunks; c0 += CPR) {
     if (c0 > 0) {
       load_round(c0);
       __builtin_amdgcn_sched_barrier(0);
+    }
+    if (NORM) {  // this round's x chunks from LDS (T = 1)
+#pragma unroll
+      for (int c = 0; c < CPR; ++c) {
+        const int cc = c0 + c < n_chunks ? c0 + c : 0;
+        xv[c] = *reinterpret_cast<const uint4 *>(s_xn + (size_t)wq * 128 + 8 * lb +
+                                                 (size_t)cc * (128 * kDecWaves));
+      }
     }
 #pragma unroll
     for (int c = 0; c < CPR; ++c) {
@@ -786,7 +841,7 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
     }
     const int jj = (!bc && lanej < s_rt.counts[a]) ? lanej : 0;
     const int tok = s_rt.perm_tok[s_rt.offsets[a] + jj];
-    P.ap = (gx_t)x + (size_t)tok * H + blk * 32 + (bc ? lanej * 8 : 0);
+    P.ap = (gx_t)xt + (size_t)tok * H + blk * 32 + (bc ? lanej * 8 : 0);
   };
   // nrows: MFMA result rows that hold tokens (1 on the single-token path, whose other rows
   // are never accumulated).
@@ -820,20 +875,29 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
       t = __builtin_amdgcn_readfirstlane(t) + wlo;
       return t < whi ? t : -1;
     };
-    const gx_t xb = (gx_t)x + blk * 32 + lanej * 8;
+    const gx_t xb = (gx_t)xt + blk * 32 + lanej * 8;
+    const uint16_t *xl = s_xn + blk * 32 + lanej * 8;
     const int nit = whi - wlo;
     if (nit > kRawSlots) {
       auto finish1 = [&](f32x4 (&ac)[2], int i) { finish_item(ac, i, 1); };
-      stream_aligned<2, 8, kGateUpDepth, true, true, kLookahead>(
-          grab, set_ptrs, finish1, hook, s_tbl, lane_const, row_blocks, s_aslot[wave], xb);
+      if (NORM)
+        stream_aligned<2, 8, kGateUpDepth, true, true, kLookahead>(
+            grab, set_ptrs, finish1, hook, s_tbl, lane_const, row_blocks, s_aslot[wave], xl);
+      else
+        stream_aligned<2, 8, kGateUpDepth, true, true, kLookahead>(
+            grab, set_ptrs, finish1, hook, s_tbl, lane_const, row_blocks, s_aslot[wave], xb);
       return;
     }
     auto finish_raw = [&](f32x4 (&ac)[2], int i) {
       s_raw[i - wlo][0][lane] = ac[0][0];
       s_raw[i - wlo][1][lane] = ac[1][0];
     };
-    stream_aligned<2, 8, kGateUpDepth, true, true, kLookahead>(
-        grab, set_ptrs, finish_raw, hook, s_tbl, lane_const, row_blocks, s_aslot[wave], xb);
+    if (NORM)
+      stream_aligned<2, 8, kGateUpDepth, true, true, kLookahead>(
+          grab, set_ptrs, finish_raw, hook, s_tbl, lane_const, row_blocks, s_aslot[wave], xl);
+    else
+      stream_aligned<2, 8, kGateUpDepth, true, true, kLookahead>(
+          grab, set_ptrs, finish_raw, hook, s_tbl, lane_const, row_blocks, s_aslot[wave], xb);
     __syncthreads();
     if (tid < 4 * nit) {
       const int slot = tid >> 2;
@@ -851,6 +915,12 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
     return;
   }
   // Other shapes: each wave takes a contiguous part of the workgroup's range.
+  if (NORM) {  // the stream reads the token from global memory: this workgroup's xs row
+    for (int c = tid * 8; c < H; c += kDecThreads * 8)
+      *reinterpret_cast<uint4 *>(const_cast<uint16_t *>(xt) + c) =
+          *reinterpret_cast<const uint4 *>(s_xn + c);
+    __syncthreads();
+  }
   const int nw = whi - wlo;
   const int i0 = wlo + wave * nw / kDecWaves;
   const int n_items = wlo + (wave + 1) * nw / kDecWaves - i0;
@@ -1013,7 +1083,7 @@ decode_down_kernel(const ExpertTable tab, const DecodeRoute *__restrict__ route,
     };
     const uint32_t lane_const2[2] = {(uint32_t)lane << 2, (uint32_t)lane << 2};
     stream_aligned<2, 4, 4, true, false, kLookahead>(grab, set_ptrs2, finish2, hook, s_tbl,
-                                                     lane_const2, row_blocks, s_aslot[wave], nullptr);
+                                                     lane_const2, row_blocks, s_aslot[wave], (gx_t)nullptr);
   } else {
     // Each wave takes a contiguous part of the units.
     const int i0 = wave * n_units / kDecWaves;
@@ -1096,6 +1166,7 @@ bool decode_layer_supported(int64_t T, int32_t k, int32_t E, int32_t H, int32_t 
 }
 
 int64_t decode_route_bytes() { return (int64_t)sizeof(DecodeRoute); }
+int64_t decode_norm_bytes() { return (int64_t)sizeof(DecodeNorm); }
 
 // Workgroups of the gate/up kernel: one per CU at most; each takes an even share of the
 // (routed expert, 4-row tile) items, which its waves then share through an LDS counter
@@ -1113,8 +1184,19 @@ int64_t decode_gateup_groups(int64_t T, int32_t k, int32_t E, int32_t F) {
 int launch_decode_layer(const moe_nf4_expert_t *experts, int32_t E, const void *gate,
                         const void *bias, const void *x, int64_t T, int32_t H, int32_t F,
                         int32_t k, void *out, void *logits, void *weights, void *idx64,
-                        void *route_ws, void *h_ws, hipStream_t s, hipEvent_t *ev) {
+                        void *route_ws, void *h_ws, hipStream_t s, hipEvent_t *ev,
+                        const void *norm) {
   MOE_REQUIRE(decode_layer_supported(T, k, E, H, F), "shape not supported by the decode layer");
+  DecodeNorm nrm{};
+  if (norm != nullptr) {
+    nrm = *static_cast<const DecodeNorm *>(norm);
+    MOE_REQUIRE(T == 1, "the fused norm takes one token (got %lld)", (long long)T);
+    MOE_REQUIRE(H <= kDecNormMaxH, "the fused norm takes H <= %d (got %d)", kDecNormMaxH, H);
+    MOE_REQUIRE(nrm.res && nrm.w && nrm.xs, "null norm pointer");
+    MOE_REQUIRE(((uintptr_t)nrm.res | (uintptr_t)nrm.w | (uintptr_t)nrm.res_out |
+                 (uintptr_t)nrm.xs) % 16 == 0,
+                "norm tensors must be 16-byte aligned");
+  }
   MOE_REQUIRE(((uintptr_t)x % 16) == 0 && ((uintptr_t)gate % 16) == 0,
               "x and gate must be 16-byte aligned");
   MOE_REQUIRE(((uintptr_t)route_ws % 16) == 0 && ((uintptr_t)h_ws % 16) == 0,
@@ -1137,12 +1219,12 @@ int launch_decode_layer(const moe_nf4_expert_t *experts, int32_t E, const void *
     hipLaunchKernelGGL(kern, dim3((unsigned)g1), dim3(kDecThreads), 0, s, tab,
                        (const uint16_t *)x, (const uint16_t *)gate, (const float *)bias, (int)T, H,
                        F, E, k, (uint16_t *)logits, (float *)weights, (int64_t *)idx64,
-                       (DecodeRoute *)route_ws, (uint16_t *)h_ws);
+                       (DecodeRoute *)route_ws, (uint16_t *)h_ws, nrm);
   };
-  if (E <= 8)
-    gateup(decode_gateup_kernel<8>);
+  if (norm != nullptr)
+    gateup(E <= 8 ? decode_gateup_kernel<8, true> : decode_gateup_kernel<16, true>);
   else
-    gateup(decode_gateup_kernel<16>);
+    gateup(E <= 8 ? decode_gateup_kernel<8, false> : decode_gateup_kernel<16, false>);
   MOE_LAUNCH_CHECK();
   if (ev) MOE_HIP_CHECK(hipEventRecord(ev[2], s));
   hipLaunchKernelGGL(decode_down_kernel, dim3((unsigned)g2), dim3(kDecThreads), 0, s, tab,

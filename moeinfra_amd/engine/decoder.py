@@ -139,6 +139,7 @@ class NativeDecoder:
         self.inv_freq = rope_inv_freq(s).to(self.dev)
         self.scaling = float(s.head_dim ** -0.5)
         self.moe = moe if moe is not None else self._moe_resident
+        self._resident = moe is None
         self._moe_bufs = {}
         self._sb = None  # single-token step buffers
 
@@ -226,6 +227,12 @@ class NativeDecoder:
         return (s.hidden % 512 == 0 and s.hidden <= 8192 and (s.n_heads * s.head_dim) % 512 == 0
                 and s.head_dim % 2 == 0)
 
+    def _decode_layer_shape(self) -> bool:
+        """Whether the MoE layer runs as the single-token decode form (T = 1)."""
+        s = self.s
+        return (s.top_k <= 8 and s.experts <= 16 and s.top_k <= s.experts and s.hidden % 512 == 0
+                and s.ffn % 512 == 0 and (s.hidden // 4 + 255) // 256 <= 8)
+
     def _step_buffers(self) -> dict:
         if self._sb is None:
             s, d = self.s, self.dev
@@ -240,7 +247,13 @@ class NativeDecoder:
                 "a": torch.empty((1, s.n_heads * s.head_dim), **bf),
                 "logits": torch.empty((1, s.vocab), **bf),
                 "cand": torch.empty((8 * 4 * cu,), dtype=torch.uint8, device=d),
+                "moe_w": torch.empty((1, s.top_k), dtype=torch.float32, device=d),
+                "moe_idx": torch.empty((1, s.top_k), dtype=torch.int64, device=d),
+                "moe_ws": None,
             }
+            nbytes = self.lib.moe_layer_norm_workspace_bytes(s.top_k, s.experts, s.hidden, s.ffn)
+            if self._resident and nbytes > 0 and s.hidden <= 8192 and self._decode_layer_shape():
+                self._sb["moe_ws"] = torch.empty((nbytes,), dtype=torch.uint8, device=d)
         return self._sb
 
     def decode_step(self, tok: torch.Tensor, gen: Optional[torch.Tensor] = None,
@@ -250,10 +263,13 @@ class NativeDecoder:
         ``gen_ctr`` (device int64) stored at gen[gen_ctr] before gen_ctr += 1; the position
         advances by one.  Returns the logits [1, V] (a buffer that the next step reuses).
 
-        Per layer four dense launches around the MoE block: norm + q/k/v + rotary + cache
-        write (moe_qkv_rope_bf16), attention, o_proj, residual + post-attention norm; then
-        the final norm, lm_head and argmax with the step's bookkeeping (moe_head_argmax_bf16,
-        two launches).  The results are bit-identical to forward() followed by argmax."""
+        Per layer three dense launches and the MoE layer's two: norm + q/k/v + rotary + cache
+        write (moe_qkv_rope_bf16), attention, o_proj, then the MoE layer with the residual
+        add and post-attention norm in its gate/up kernel (moe_layer_forward_nf4_norm; with
+        a caller-supplied MoE block, e.g. offload, a separate norm launch and that block);
+        then the final norm, lm_head and argmax with the step's bookkeeping
+        (moe_head_argmax_bf16, two launches).  The results are bit-identical to forward()
+        followed by argmax."""
         if not self.fused_step_supported():
             logits = self.forward(tok)
             nxt = logits.argmax(dim=-1)
@@ -264,6 +280,7 @@ class NativeDecoder:
             return logits
         s, b, st, lib = self.s, self._step_buffers(), self._stream(), self.lib
         nq, nkv, hd, H = s.n_heads, s.n_kv_heads, s.head_dim, s.hidden
+        fused_moe = self._resident and b["moe_ws"] is not None
         x, x_row, x_rows, res = self.w.embed, tok.data_ptr(), s.vocab, None
         m = None
         for l, lw in enumerate(self.w.layers):
@@ -278,11 +295,20 @@ class NativeDecoder:
                                               self.scaling, b["a"].data_ptr(), st), "attention")
             _lib.check(lib.moe_gemv_bf16(lw.o_proj.data_ptr(), b["a"].data_ptr(), 1, H, nq * hd,
                                          b["y"].data_ptr(), st), "o_proj")
-            _lib.check(lib.moe_add_rmsnorm_bf16(b["y"].data_ptr(), b["h"].data_ptr(),
-                                                lw.post_norm.data_ptr(), s.rms_eps, 1, H,
-                                                b["resid"].data_ptr(), b["x2"].data_ptr(), st),
-                       "post-attention norm")
-            m = self.moe(l, b["x2"])
+            if fused_moe:
+                # residual add + post-attention norm inside the MoE layer's gate/up kernel
+                m = torch.empty_like(b["y"])
+                _lib.check(lib.moe_layer_forward_nf4_norm(
+                    lw.table, s.experts, lw.gate.data_ptr(), b["y"].data_ptr(), b["h"].data_ptr(),
+                    lw.post_norm.data_ptr(), s.rms_eps, H, s.ffn, s.top_k, b["resid"].data_ptr(),
+                    m.data_ptr(), b["moe_w"].data_ptr(), b["moe_idx"].data_ptr(),
+                    b["moe_ws"].data_ptr(), b["moe_ws"].numel(), st), "moe layer + norm")
+            else:
+                _lib.check(lib.moe_add_rmsnorm_bf16(b["y"].data_ptr(), b["h"].data_ptr(),
+                                                    lw.post_norm.data_ptr(), s.rms_eps, 1, H,
+                                                    b["resid"].data_ptr(), b["x2"].data_ptr(), st),
+                           "post-attention norm")
+                m = self.moe(l, b["x2"])
             x, x_row, x_rows, res = m, None, 1, b["resid"].data_ptr()
         gen_p = gen.data_ptr() if gen is not None else None
         ctr_p = gen_ctr.data_ptr() if gen_ctr is not None else None

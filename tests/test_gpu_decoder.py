@@ -247,6 +247,54 @@ def test_head_argmax(cuda_device):
     assert gen.tolist() == [-1, 777, 777] and int(gctr.item()) == 4 and int(pos.item()) == 11
 
 
+@pytest.mark.parametrize("full", [True, False])
+def test_layer_norm_fused_matches_unfused(cuda_device, full):
+    """The single-token MoE layer with the post-attention residual add + norm in its gate/up
+    kernel == moe_add_rmsnorm_bf16 then moe_layer_forward_nf4, bit for bit (output,
+    residual, routing weights and ids), on two calls in a row."""
+    from moeinfra_amd import _lib
+    from moeinfra_amd.engine.decoder import MixtralShape, synthesize
+
+    lib = _lib.lib()
+    dev = cuda_device
+    shape = (MixtralShape(layers=1) if full else
+             MixtralShape(hidden=512, ffn=1024, layers=1, n_heads=8, n_kv_heads=2, head_dim=64,
+                          vocab=64))
+    w = synthesize(shape, seed=41, device=dev)
+    lw = w.layers[0]
+    H, F, E, k = shape.hidden, shape.ffn, shape.experts, shape.top_k
+    nw = _bf16((H,), 42, 0.5).to(dev)
+    ws_n = torch.empty((lib.moe_layer_norm_workspace_bytes(k, E, H, F),), dtype=torch.uint8, device=dev)
+    ws_u = torch.empty((lib.moe_layer_workspace_bytes(1, k, E, H, F),), dtype=torch.uint8, device=dev)
+    for seed in (43, 44):
+        y = _bf16((1, H), seed).to(dev)
+        h = _bf16((1, H), seed + 10).to(dev)
+        outs = {}
+        for fused in (True, False):
+            r = torch.empty((1, H), dtype=torch.bfloat16, device=dev)
+            out = torch.empty((1, H), dtype=torch.bfloat16, device=dev)
+            wt = torch.empty((1, k), dtype=torch.float32, device=dev)
+            idx = torch.empty((1, k), dtype=torch.int64, device=dev)
+            if fused:
+                _lib.check(lib.moe_layer_forward_nf4_norm(
+                    lw.table, E, lw.gate.data_ptr(), y.data_ptr(), h.data_ptr(), nw.data_ptr(), 1e-5,
+                    H, F, k, r.data_ptr(), out.data_ptr(), wt.data_ptr(), idx.data_ptr(),
+                    ws_n.data_ptr(), ws_n.numel(), _stream()), "fused")
+            else:
+                x2 = torch.empty_like(y)
+                _lib.check(lib.moe_add_rmsnorm_bf16(y.data_ptr(), h.data_ptr(), nw.data_ptr(), 1e-5, 1,
+                                                    H, r.data_ptr(), x2.data_ptr(), _stream()), "norm")
+                _lib.check(lib.moe_layer_forward_nf4(
+                    lw.table, E, lw.gate.data_ptr(), None, x2.data_ptr(), 1, H, F, k, out.data_ptr(),
+                    None, wt.data_ptr(), idx.data_ptr(), ws_u.data_ptr(), ws_u.numel(), _stream()),
+                    "layer")
+            torch.cuda.synchronize()
+            outs[fused] = (bits(r), bits(out), wt.cpu().numpy(), idx.cpu().numpy())
+        for a, b in zip(outs[True], outs[False]):
+            np.testing.assert_array_equal(a, b)
+        assert np.abs(outs[True][1].astype(np.int32)).sum() > 0
+
+
 def test_decode_step_matches_forward(cuda_device):
     """The fused decode step == forward() + argmax, bit for bit, over several positions."""
     from moeinfra_amd.engine.decoder import NativeDecoder
