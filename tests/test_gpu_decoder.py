@@ -398,6 +398,22 @@ def test_engine_offload_matches_reference(cuda_device):
         _check_against_reference(res, w, prompt)
 
 
+def test_engine_full_mixtral_layer_matches_reference(cuda_device):
+    """One decoder layer at the full Mixtral-8x7B shape (hidden 4096, 32/8 heads of 128,
+    8 NF4 experts of 14336, vocab 32000): prefill of 6 tokens and 4 graph-replayed decode
+    tokens against the CPU oracle decoder, teacher-forced on the engine's tokens."""
+    from moeinfra_amd.engine.decoder import MixtralShape, synthesize
+    from moeinfra_amd.engine.engine import InferenceEngine
+    from moeinfra_amd.engine.types import ForwardRequest
+
+    w = synthesize(MixtralShape(layers=1), seed=12, device=cuda_device)
+    prompt = torch.randint(0, w.shape.vocab, (1, 6), generator=torch.Generator().manual_seed(13))
+    eng = InferenceEngine(w, max_seq=32, device=cuda_device)
+    res = eng.generate(ForwardRequest(prompt, max_new_tokens=5))
+    assert len(res.token_ids) == 5
+    _check_against_reference(res, w, prompt)
+
+
 def test_engine_rejects_bad_requests(cuda_device):
     from moeinfra_amd.engine.engine import InferenceEngine
     from moeinfra_amd.engine.types import ForwardRequest
