@@ -74,6 +74,16 @@ int moe_version(void);
 int moe_nf4_dequant_bf16(const void *packed, const void *absmax, const void *code16,
                          void *out_bf16, int64_t numel, int32_t blocksize, void *stream);
 
+/* Nested (double-quantised) absmax of a bitsandbytes NF4 state (compress_statistics):
+ * out_f32[i] = code2[absmax_u8[i]] * absmax2[i / blocksize2] + offset, in fp32 (product and
+ * sum rounded separately), for i < n.  code2 has 256 entries.  The expanded absmax feeds
+ * K1 and the fused expert kernels, which take fp32 block scales.  Replaces the nested
+ * branch of the state that _build_quant_state assembles (transfer/nf4_reconstruct.py:22-43),
+ * which bitsandbytes resolves inside dequantize_4bit. */
+int moe_nf4_expand_absmax(const void *absmax_u8, const void *absmax2_f32, const void *code2_f32,
+                          float offset, int64_t n, int32_t blocksize2, void *out_f32,
+                          void *stream);
+
 /* ---------------------------------------------------------------- K0: NF4 quantise
  * Blockwise NF4 quantisation of bf16 values: absmax = max|w| per block, q = nearest
  * code value of w*(1/absmax) (midpoint thresholds, ties to the lower code).

@@ -70,6 +70,7 @@ SIGNATURES = {
     "moe_layer_norm_workspace_bytes": ([_i32, _i32, _i32, _i32], _i64),
     "moe_layer_forward_nf4_norm": ([ctypes.POINTER(MoeNf4Expert), _i32, _vp, _vp, _vp, _vp, ctypes.c_float, _i32, _i32, _i32,
                                     _vp, _vp, _vp, _vp, _vp, _i64, _vp], ctypes.c_int),
+    "moe_nf4_expand_absmax": ([_vp, _vp, _vp, ctypes.c_float, _i64, _i32, _vp, _vp], ctypes.c_int),
     "moe_qkv_rope_bf16": ([_vp, _vp, _vp, _i64, _vp, _vp, ctypes.c_float, _i32, _i32, _i32, _i32,
                            _vp, _vp, _i64, _vp, _vp, _vp, _vp, _vp], ctypes.c_int),
     "moe_head_argmax_bf16": ([_vp, _vp, _vp, _vp, ctypes.c_float, _i32, _i32, _vp, _vp, _i64, _vp,

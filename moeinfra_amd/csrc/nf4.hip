@@ -91,8 +91,43 @@ nf4_quantize_kernel(const uint16_t *__restrict__ w, int64_t numel, int32_t block
   }
 }
 
+constexpr int kExpandThreads = 256;
+
+// Nested (double-quantised) absmax: the fp32 block scales stored as 8-bit indices into a
+// 256-entry code, with one fp32 scale per group of blocksize2 indices and a common offset.
+// out[i] = code2[q[i]] * absmax2[i / blocksize2] + offset (a product, then a sum, each
+// rounded in fp32 -- bitsandbytes' dequantize_blockwise of the absmax, then += offset).
+__global__ void __launch_bounds__(kExpandThreads)
+expand_absmax_kernel(const uint8_t *__restrict__ q, const float *__restrict__ absmax2,
+                     const float *__restrict__ code2, float offset, int64_t n, int32_t blocksize2,
+                     float *__restrict__ out) {
+  __shared__ float s_code[256];
+  s_code[threadIdx.x] = code2[threadIdx.x];
+  __syncthreads();
+  const int64_t i = (int64_t)blockIdx.x * kExpandThreads + threadIdx.x;
+  if (i >= n) return;
+  const float v = s_code[q[i]] * absmax2[i / blocksize2];
+  out[i] = v + offset;
+}
+
 }  // namespace
 }  // namespace moe
+
+extern "C" int moe_nf4_expand_absmax(const void *absmax_u8, const void *absmax2_f32,
+                                     const void *code2_f32, float offset, int64_t n,
+                                     int32_t blocksize2, void *out_f32, void *stream) {
+  MOE_REQUIRE(n >= 0, "n must be non-negative (got %lld)", (long long)n);
+  MOE_REQUIRE(blocksize2 > 0, "blocksize2 must be positive (got %d)", blocksize2);
+  if (n == 0) return MOE_STATUS_OK;
+  MOE_REQUIRE(absmax_u8 && absmax2_f32 && code2_f32 && out_f32, "null device pointer");
+  const int64_t grid = (n + moe::kExpandThreads - 1) / moe::kExpandThreads;
+  MOE_REQUIRE(grid <= 0x7fffffff, "n too large");
+  hipLaunchKernelGGL(moe::expand_absmax_kernel, dim3((unsigned)grid), dim3(moe::kExpandThreads), 0,
+                     (hipStream_t)stream, (const uint8_t *)absmax_u8, (const float *)absmax2_f32,
+                     (const float *)code2_f32, offset, n, blocksize2, (float *)out_f32);
+  MOE_LAUNCH_CHECK();
+  return MOE_STATUS_OK;
+}
 
 extern "C" int moe_nf4_dequant_bf16(const void *packed, const void *absmax, const void *code16,
                                     void *out_bf16, int64_t numel, int32_t blocksize,

@@ -53,6 +53,21 @@ class NF4QuantState:
                                    offset=mv(self.offset),
                                    state2=None if self.state2 is None else self.state2.to(device))
 
+    def fp32_absmax(self) -> torch.Tensor:
+        """The fp32 block scales the kernels take: ``absmax`` itself, or for a nested state
+        its expansion on the GPU (moe_nf4_expand_absmax), computed once and kept."""
+        if not self.nested:
+            return self.absmax
+        cached = self.__dict__.get("_absmax_f32")
+        if cached is not None and cached.device == self.absmax.device:
+            return cached
+        if self.absmax.dtype != torch.uint8:
+            raise ValueError(f"nested absmax must be uint8 indices, got {self.absmax.dtype}")
+        out = ops.nf4_expand_absmax(self.absmax, self.state2.absmax, self.state2.code, self.offset,
+                                    self.state2.blocksize)
+        self.__dict__["_absmax_f32"] = out
+        return out
+
     def blob(self) -> torch.Tensor:
         meta = {"quant_type": self.quant_type, "blocksize": self.blocksize,
                 "dtype": str(self.dtype).replace("torch.", ""), "shape": list(self.shape)}
@@ -115,10 +130,8 @@ class NF4Linear(nn.Module):
         if not self.quantized:
             return self.weight
         qs = self.quant_state
-        if qs.nested:
-            raise NotImplementedError("nested (double-quantised) absmax is not supported")
-        return ops.nf4_dequant(self.weight, qs.absmax, qs.code, (self.out_features, self.in_features),
-                               qs.blocksize)
+        return ops.nf4_dequant(self.weight, qs.fp32_absmax(), qs.code,
+                               (self.out_features, self.in_features), qs.blocksize)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         # A lone projection is not on the expert fast path: dequantise with the HIP kernel
@@ -146,14 +159,13 @@ def expert_struct(w1: NF4Linear, w2: NF4Linear, w3: NF4Linear) -> MoeNf4Expert:
         if lin.weight.dtype != NF4_QUANT_STORAGE:
             raise ValueError(f"Expected packed NF4 weight dtype {NF4_QUANT_STORAGE}, "
                              f"got {lin.weight.dtype}")
-        if lin.quant_state.nested:
-            raise NotImplementedError("nested (double-quantised) absmax is not supported")
         if lin.quant_state.blocksize != NF4_BLOCKSIZE:
             raise ValueError(f"the fused expert kernels need blocksize {NF4_BLOCKSIZE}")
     p = lambda t: t.data_ptr()
-    return MoeNf4Expert(p(w1.weight), p(w1.quant_state.absmax), p(w1.quant_state.code),
-                        p(w3.weight), p(w3.quant_state.absmax), p(w3.quant_state.code),
-                        p(w2.weight), p(w2.quant_state.absmax), p(w2.quant_state.code))
+    a = lambda lin: lin.quant_state.fp32_absmax().data_ptr()  # nested states: expanded once
+    return MoeNf4Expert(p(w1.weight), a(w1), p(w1.quant_state.code),
+                        p(w3.weight), a(w3), p(w3.quant_state.code),
+                        p(w2.weight), a(w2), p(w2.quant_state.code))
 
 
 def swiglu_forward(expert, x: torch.Tensor) -> torch.Tensor:

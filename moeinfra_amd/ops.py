@@ -44,6 +44,30 @@ def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
 
 
 # ----------------------------------------------------------------------------- K1
+def nf4_expand_absmax(absmax_q: torch.Tensor, absmax2: torch.Tensor, code2: torch.Tensor,
+                      offset, blocksize2: int) -> torch.Tensor:
+    """fp32 block scales of a nested (double-quantised) NF4 state:
+    ``code2[absmax_q[i]] * absmax2[i // blocksize2] + offset`` (bitsandbytes'
+    dequantize_blockwise of the absmax, then ``+= offset``)."""
+    dev = absmax_q.device
+    _require(absmax_q, "absmax_q", torch.uint8, dev)
+    _require(absmax2, "absmax2", torch.float32, dev)
+    _require(code2, "code2", torch.float32, dev)
+    if code2.numel() != 256:
+        raise ValueError("the nested code must have 256 entries")
+    n = absmax_q.numel()
+    if absmax2.numel() * int(blocksize2) < n:
+        raise ValueError(f"absmax2 has {absmax2.numel()} groups, {n} values need "
+                         f"{(n + blocksize2 - 1) // blocksize2}")
+    off = 0.0 if offset is None else float(offset)
+    out = torch.empty(absmax_q.shape, dtype=torch.float32, device=dev)
+    check(lib().moe_nf4_expand_absmax(absmax_q.data_ptr(), absmax2.data_ptr(), code2.data_ptr(), off,
+                                      n, int(blocksize2), out.data_ptr(),
+                                      torch.cuda.current_stream(dev).cuda_stream),
+          "moe_nf4_expand_absmax")
+    return out
+
+
 def nf4_dequant(packed: torch.Tensor, absmax: torch.Tensor, code: torch.Tensor,
                 shape: Sequence[int], blocksize: int = NF4_BLOCKSIZE,
                 out: Optional[torch.Tensor] = None) -> torch.Tensor:

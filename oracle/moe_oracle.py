@@ -264,6 +264,40 @@ def dequant_expert(state: dict, hidden: int, inter: int, code: np.ndarray = NF4_
     return w1, w3, w2
 
 
+def expand_absmax(q: np.ndarray, absmax2: np.ndarray, code2: np.ndarray, offset: float,
+                  blocksize2: int) -> np.ndarray:
+    """fp32 block scales of a nested (double-quantised) NF4 state: ``code2[q[i]] *
+    absmax2[i // blocksize2]`` rounded to fp32, then ``+ offset`` rounded to fp32 -- the
+    nested branch of the state that transfer/nf4_reconstruct.py:22-43 assembles, which
+    bitsandbytes resolves as ``dequantize_blockwise(absmax, state2) + offset``.
+    Parity unpinned against bitsandbytes itself (absent here): pinned only by a hand case
+    and by the double-quantisation round trip in tests/test_host_store.py."""
+    q = np.asarray(q, dtype=np.uint8).reshape(-1)
+    grp = np.arange(q.size, dtype=np.int64) // int(blocksize2)
+    v = np.asarray(code2, dtype=np.float32)[q] * np.asarray(absmax2, dtype=np.float32)[grp]
+    return (v.astype(np.float32) + np.float32(offset)).astype(np.float32)
+
+
+def double_quantize_absmax(absmax: np.ndarray, blocksize2: int = 256):
+    """A nested state for fp32 block scales (test fixtures): offset = mean, then per group
+    of blocksize2 the largest |absmax - offset| as absmax2 and the nearest entry of a
+    256-entry signed code (uniform on [-1, 1]) as the 8-bit index.  Returns
+    (q uint8, absmax2 fp32, code2 fp32[256], offset float)."""
+    a = np.asarray(absmax, dtype=np.float32).reshape(-1)
+    offset = float(np.float32(a.mean(dtype=np.float64)))
+    c = (a - np.float32(offset)).astype(np.float32)
+    ngrp = -(-a.size // int(blocksize2))
+    pad = np.zeros(ngrp * int(blocksize2), dtype=np.float32)
+    pad[:a.size] = np.abs(c)
+    absmax2 = pad.reshape(ngrp, int(blocksize2)).max(axis=1).astype(np.float32)
+    absmax2 = np.where(absmax2 > 0, absmax2, np.float32(1.0)).astype(np.float32)
+    code2 = np.linspace(-1.0, 1.0, 256, dtype=np.float32)
+    grp = np.arange(a.size) // int(blocksize2)
+    x = c / absmax2[grp]
+    q = np.abs(x[:, None] - code2[None, :]).argmin(axis=1).astype(np.uint8)
+    return q, absmax2, code2, offset
+
+
 def rel_l2(a, b) -> float:
     a = np.asarray(a, dtype=np.float64)
     b = np.asarray(b, dtype=np.float64)

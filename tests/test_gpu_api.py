@@ -275,3 +275,78 @@ def test_full_size_layer_matches_oracle(cuda_device, T):
     err = _layer_err(bits(out), want, lg_o)
     print(f"full-size layer T={T}: rel-L2 {err:.2e}", flush=True)
     assert err < TOL
+
+
+# --------------------------------------------------------------------------- nested absmax
+def test_expand_absmax_kernel(cuda_device):
+    """moe_nf4_expand_absmax against the oracle, bit for bit (a Mixtral w1 absmax count plus
+    an odd tail; offsets zero and non-zero)."""
+    from moeinfra_amd import ops
+
+    rng = np.random.default_rng(11)
+    for n, off in ((14336 * 4096 // 64, 0.0), (1037, 0.0123)):
+        q = rng.integers(0, 256, n, dtype=np.uint8)
+        a2 = (rng.random(-(-n // 256), dtype=np.float32) * 0.05 + 1e-4).astype(np.float32)
+        c2 = np.sort(rng.standard_normal(256).astype(np.float32))
+        got = ops.nf4_expand_absmax(torch.from_numpy(q).to(cuda_device),
+                                    torch.from_numpy(a2).to(cuda_device),
+                                    torch.from_numpy(c2).to(cuda_device), off, 256)
+        want = orc.expand_absmax(q, a2, c2, off, 256)
+        np.testing.assert_array_equal(got.cpu().numpy().view(np.uint32), want.view(np.uint32))
+
+
+def test_nested_expert_from_store_to_gpu(cuda_device, tmp_path):
+    """A nested (double-quantised) expert written to the on-disk store, read back, staged and
+    transferred through the scheduler: each projection dequantises bit-exactly to the
+    oracle's dequant with the expanded absmax, and the expert's forward equals, bit for
+    bit, that of the same expert holding the expanded absmax as fp32."""
+    from moeinfra_amd.cache.manager import CacheManager
+    from moeinfra_amd.cache.types import EvictionPolicy
+    from moeinfra_amd.model.expert import NF4QuantState, PrequantizedNF4Expert
+    from moeinfra_amd.model.store import NF4ExpertStore, save_expert
+
+    H, F = 512, 1024
+    _gate, experts, x = build_layer(H, F, 1, 3, seed=9)
+    ex = experts[0]
+    shapes = {"w1": (F, H), "w3": (F, H), "w2": (H, F)}
+    nested, flat, expanded = {}, {}, {}
+    for n in ("w1", "w2", "w3"):
+        packed, absmax = ex.np[n]
+        q, a2, c2, off = orc.double_quantize_absmax(absmax, 256)
+        expanded[n] = orc.expand_absmax(q, a2, c2, off, 256)
+        code = torch.from_numpy(orc.NF4_CODE.copy())
+        qs = NF4QuantState(absmax=torch.from_numpy(q), code=code, shape=torch.Size(shapes[n]),
+                           offset=torch.tensor(off),
+                           state2=NF4QuantState(absmax=torch.from_numpy(a2), code=torch.from_numpy(c2),
+                                                shape=torch.Size((q.size,)), blocksize=256,
+                                                quant_type=None, dtype=torch.float32))
+        nested[n] = {"weight": torch.from_numpy(packed.copy()).reshape(-1, 1),
+                     "weight.absmax": qs.absmax, "weight.quant_map": code,
+                     "weight.nested_absmax": qs.state2.absmax,
+                     "weight.nested_quant_map": qs.state2.code,
+                     "weight.quant_state.bitsandbytes__nf4": qs.blob()}
+        flat[n] = _serialized(packed, expanded[n], shapes[n])
+    save_expert(tmp_path, 0, 0, PrequantizedNF4Expert.from_serialized(
+        nested["w1"], nested["w2"], nested["w3"], H, F))
+    back = NF4ExpertStore([tmp_path], H, F).load_expert(0, 0)
+    flat_ex = PrequantizedNF4Expert.from_serialized(flat["w1"], flat["w2"], flat["w3"], H, F)
+    gpu = []
+    # One staging rig each: a slot's pinned buffers are reused only for tensors of the same
+    # layout (the nested absmax is uint8, the flat one fp32).
+    for ex_cpu in (back, flat_ex):
+        cm = CacheManager(gpu_slots=1, cpu_slots=1, policy=EvictionPolicy.LRU)
+        cm.put(0, 0, ex_cpu, "cpu")
+        sch, _pool = _transfer_rig(cm, 1, ex_cpu.size_bytes)
+        assert sch.submit(_req(0, 0))
+        r = sch.execute_next()
+        assert r.success, r.error
+        gpu.append(cm.peek_gpu(0, 0))
+    gn, gf = gpu
+    for n in ("w1", "w2", "w3"):
+        lin = getattr(gn, n)
+        assert lin.quant_state.nested
+        got = bits(lin.dequantize())
+        want = orc.nf4_dequant(ex.np[n][0], expanded[n]).reshape(got.shape)
+        np.testing.assert_array_equal(got, want)
+    xd = x.to(cuda_device)
+    np.testing.assert_array_equal(bits(gn(xd)), bits(gf(xd)))
