@@ -49,7 +49,8 @@ def parse_args():
                    help="e2e mode with the NF4 store in pinned host memory and a bounded GPU cache")
     p.add_argument("--gpu-expert-slots", type=int, default=8,
                    help="GPU expert cache slots in offload mode (the reference's default: 8)")
-    p.add_argument("--prefetch", choices=["none", "next_layer", "lookahead"], default="next_layer")
+    p.add_argument("--prefetch", choices=["none", "next_layer", "lookahead"], default="none",
+                   help="offload mode's prefetch policy (the reference engine's default: none)")
     p.add_argument("--prefetch-depth", type=int, default=2)
     p.add_argument("--tokens", type=int, default=1, help="tokens per decode step (decode mode)")
     p.add_argument("--routing", choices=["uniform", "zipf"], default="uniform")
@@ -411,8 +412,9 @@ def _e2e(args) -> int:
                                     "note": "the 32 MoE layers alone on fixed N(0,1) inputs, T=1; "
                                             "roofline events are in this pass's timed region"}
     if args.offload:
-        result["offload_stats"] = {"cache_hits": st.hits, "cache_misses": st.misses,
-                                   "evictions": st.evictions, "hit_rate": round(st.hit_rate, 4)}
+        bw = eng.transfer_scheduler.bandwidth_monitor
+        result["offload_stats"] = {"cache_evictions": st.evictions,
+                                   "h2d_peak_gibps": round(bw.peak_gbps(), 2)}
     print(json.dumps(result), flush=True)
     return 0
 
