@@ -412,9 +412,8 @@ def _e2e(args) -> int:
                                     "note": "the 32 MoE layers alone on fixed N(0,1) inputs, T=1; "
                                             "roofline events are in this pass's timed region"}
     if args.offload:
-        bw = eng.transfer_scheduler.bandwidth_monitor
         result["offload_stats"] = {"cache_evictions": st.evictions,
-                                   "h2d_peak_gibps": round(bw.peak_gbps(), 2)}
+                                   "expert_bytes": int(nf4_expert_bytes(s.hidden, s.ffn))}
     print(json.dumps(result), flush=True)
     return 0
 

@@ -26,7 +26,7 @@ import torch
 
 from .. import ops
 from ..engine.router import ExpertRouter
-from ..transfer.types import TransferDirection, TransferPriority, TransferRequest
+from ..transfer.types import TransferDirection, TransferPriority, TransferRequest, TransferStatus
 
 
 def _is_hip_expert(expert) -> bool:
@@ -76,6 +76,28 @@ class MoELayer:
             raise RuntimeError(f"Expert layer={self.layer_id}, expert={expert_id} "
                                "was not resident on GPU after transfer")
         return expert
+
+    def _start_async_transfers(self, unique: list, was_resident: dict) -> None:
+        """Start the copies of every routed expert that is not GPU-resident at once
+        (submit_async: stage into a pinned slot, hipMemcpyAsync on the transfer stream), so
+        that staging one overlaps the copy of the previous; then finish them in order.
+        Experts that get no slot take the synchronous path in _ensure_expert_on_gpu."""
+        sched = self.transfer_scheduler
+        if not hasattr(sched, "submit_async") or not hasattr(sched, "poll_async"):
+            return
+        handles = {}
+        for e in unique:
+            if was_resident[e] or self.cache_manager.peek_cpu(self.layer_id, e) is None:
+                continue
+            request = TransferRequest(
+                request_id=f"layer-{self.layer_id}-expert-{e}-{id(self)}-async",
+                layer_id=self.layer_id, expert_id=e, direction=TransferDirection.CPU_TO_GPU,
+                priority=TransferPriority.HIGH, issued_at=time.monotonic())
+            handles[e] = sched.submit_async(request)
+        for e, h in handles.items():
+            if h.status == TransferStatus.IN_FLIGHT:
+                h.event.synchronize()
+                sched.poll_async(self.layer_id, e)
 
     # ------------------------------------------------------------------ forward
     @torch.no_grad()
@@ -142,6 +164,7 @@ class MoELayer:
         was_resident = {e: self.cache_manager.is_gpu_resident(self.layer_id, e) for e in unique}
         experts = {}
         try:
+            self._start_async_transfers(unique, was_resident)
             for e in unique:
                 experts[e] = self._ensure_expert_on_gpu(e)
             if not all(_is_hip_expert(ex) for ex in experts.values()):
