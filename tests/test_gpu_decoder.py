@@ -80,11 +80,12 @@ def test_rope_and_cache_write(cuda_device):
     assert not kc[:, :p0].any() and not kc[:, p0 + T:].any()              # other rows untouched
 
 
-@pytest.mark.parametrize("T,p0", [(1, 0), (1, 71), (40, 0), (7, 20)])
-def test_attention(cuda_device, T, p0):
+@pytest.mark.parametrize("T,p0,max_seq", [(1, 0, 256), (1, 71, 256), (40, 0, 256), (7, 20, 256),
+                                          (1, 3000, 4096), (16, 2040, 4096)])
+def test_attention(cuda_device, T, p0, max_seq):
     from moeinfra_amd import _lib
 
-    nq, nkv, hd, max_seq = 32, 8, 128, 256
+    nq, nkv, hd = 32, 8, 128
     S = p0 + T
     q = _bf16((T, nq, hd), 5)
     k = _bf16((nkv, S, hd), 6)
@@ -412,6 +413,24 @@ def test_engine_full_mixtral_layer_matches_reference(cuda_device):
     res = eng.generate(ForwardRequest(prompt, max_new_tokens=5))
     assert len(res.token_ids) == 5
     _check_against_reference(res, w, prompt)
+
+
+def test_engine_fills_max_seq_and_lookahead_offload(cuda_device):
+    """A prompt plus generated tokens that fill the KV cache exactly, graph-replayed; and the
+    offload engine with look-ahead prefetch, both against the oracle decoder."""
+    from moeinfra_amd.engine.engine import InferenceEngine
+    from moeinfra_amd.engine.types import ForwardRequest, PrefetchPolicy
+
+    w = _small_engine_weights(cuda_device)
+    prompt = torch.randint(0, w.shape.vocab, (1, 10), generator=torch.Generator().manual_seed(21))
+    eng = InferenceEngine(w, max_seq=16, device=cuda_device)
+    res = eng.generate(ForwardRequest(prompt, max_new_tokens=7))      # positions 0 .. 15
+    assert len(res.token_ids) == 7
+    _check_against_reference(res, w, prompt)
+    eng = InferenceEngine(w, max_seq=32, device=cuda_device, offload=True, gpu_expert_slots=3,
+                          prefetch=PrefetchPolicy.LOOKAHEAD, prefetch_depth=2)
+    res = eng.generate(ForwardRequest(prompt[:, :5], max_new_tokens=4))
+    _check_against_reference(res, w, prompt[:, :5])
 
 
 def test_engine_rejects_bad_requests(cuda_device):
