@@ -192,7 +192,19 @@ constexpr int kRouteThreads = 1024;
 constexpr int kRouteWaves = kRouteThreads / kWave;
 constexpr int kRouteMaxTokens = 16;
 
-template <int EMAX>
+constexpr int kRouteChunk = 256;  // values of H per wave and step in the chunked form
+
+// Orders one wave's LDS writes before its own lanes' reads of other lanes' data
+// (wavefront-scope fences around a wave barrier).
+__device__ __forceinline__ void route_wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// CHUNKED: E <= 8 and H a multiple of 256 (the gate products by H chunk, below); else one
+// group of 16/T waves per token streams its row and the gate.
+template <int EMAX, bool CHUNKED>
 __global__ void __launch_bounds__(kRouteThreads)
 route_small_kernel(const uint16_t *__restrict__ x, const uint16_t *__restrict__ gate,
                    const float *__restrict__ bias, int T, int H, int E, int k,
@@ -202,6 +214,8 @@ route_small_kernel(const uint16_t *__restrict__ x, const uint16_t *__restrict__ 
                    int32_t *__restrict__ perm_tok, int32_t *__restrict__ slot_pos,
                    int32_t *__restrict__ active, uint32_t *__restrict__ zero_word) {
   __shared__ float s_part[kRouteWaves][EMAX];
+  __shared__ float s_tpart[CHUNKED ? kRouteWaves : 1][kRouteMaxTokens][EMAX];
+  __shared__ __attribute__((aligned(16))) uint16_t s_g[CHUNKED ? kRouteWaves : 1][EMAX * kRouteChunk];
   __shared__ int32_t s_idx[kRouteMaxTokens * MOE_MAX_TOPK];
   __shared__ int32_t s_off[MOE_MAX_EXPERTS + 1];
   const int tid = threadIdx.x;
@@ -217,7 +231,51 @@ route_small_kernel(const uint16_t *__restrict__ x, const uint16_t *__restrict__ 
   float acc[EMAX];
 #pragma unroll
   for (int e = 0; e < EMAX; ++e) acc[e] = 0.0f;
-  if (t < T) {
+  if (CHUNKED) {
+    // Wave w takes the 256-value chunks w, w + 16, ... of H for every token, so each gate
+    // value is read once per workgroup: the chunk's gate rows go to the wave's LDS slot,
+    // lane (token tl = lane % 16, part p = lane / 16) multiplies its 64 values of the chunk
+    // by them; parts are summed with two butterflies, waves in order below.
+    const int tl = lane & 15, p = lane >> 4;
+    uint16_t *sg = s_g[CHUNKED ? wave : 0];
+    for (int ch = wave; ch < H / kRouteChunk; ch += kRouteWaves) {
+      const int c0 = ch * kRouteChunk;
+#pragma unroll
+      for (int i = 0; i < EMAX * kRouteChunk / (8 * kWave); ++i) {
+        const int v = (i * kWave + lane) * 8;  // value index within the EMAX x 256 block
+        const int e = v / kRouteChunk, o = v - e * kRouteChunk;
+        *reinterpret_cast<uint4 *>(sg + v) = *reinterpret_cast<const uint4 *>(
+            gate + (int64_t)(e < E ? e : E - 1) * H + c0 + o);
+      }
+      const uint16_t *xr = x + (int64_t)(tl < T ? tl : T - 1) * H + c0 + p * 64;
+      uint4 xv[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) xv[j] = *reinterpret_cast<const uint4 *>(xr + 8 * j);
+      route_wave_sync();
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const uint32_t xw[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
+#pragma unroll
+        for (int e = 0; e < EMAX; ++e) {
+          const uint4 gv = *reinterpret_cast<const uint4 *>(sg + e * kRouteChunk + p * 64 + 8 * j);
+          const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w};
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            acc[e] = fmaf(bf16lo_to_f32(xw[q]), bf16lo_to_f32(gw[q]), acc[e]);
+            acc[e] = fmaf(bf16hi_to_f32(xw[q]), bf16hi_to_f32(gw[q]), acc[e]);
+          }
+        }
+      }
+      route_wave_sync();  // the slot is rewritten by the next chunk
+    }
+#pragma unroll
+    for (int e = 0; e < EMAX; ++e) {
+      float v = acc[e];
+      v += __shfl_xor(v, 16, kWave);
+      v += __shfl_xor(v, 32, kWave);
+      if (lane < kRouteMaxTokens) s_tpart[CHUNKED ? wave : 0][lane][e] = v;
+    }
+  } else if (t < T) {
     const uint16_t *xr = x + (int64_t)t * H;
     for (int c = gtid * 8; c < H; c += gsize * 8) {
       const uint4 xv = *reinterpret_cast<const uint4 *>(xr + c);
@@ -231,10 +289,12 @@ route_small_kernel(const uint16_t *__restrict__ x, const uint16_t *__restrict__ 
       gate_step<EMAX>(gate, H, E, c, xf, acc);
     }
   }
+  if (!CHUNKED) {
 #pragma unroll
-  for (int e = 0; e < EMAX; ++e) {
-    const float v = wave_sum(acc[e]);
-    if (lane == 0) s_part[wave][e] = v;
+    for (int e = 0; e < EMAX; ++e) {
+      const float v = wave_sum(acc[e]);
+      if (lane == 0) s_part[wave][e] = v;
+    }
   }
   __syncthreads();
 
@@ -245,8 +305,14 @@ route_small_kernel(const uint16_t *__restrict__ x, const uint16_t *__restrict__ 
 #pragma unroll
     for (int e = 0; e < EMAX; ++e) {
       if (e < E) {
-        float v = s_part[tt * wpt][e];
-        for (int w = 1; w < wpt; ++w) v += s_part[tt * wpt + w][e];
+        float v;
+        if (CHUNKED) {
+          v = s_tpart[0][tt][e];
+          for (int w = 1; w < kRouteWaves; ++w) v += s_tpart[CHUNKED ? w : 0][tt][e];
+        } else {
+          v = s_part[tt * wpt][e];
+          for (int w = 1; w < wpt; ++w) v += s_part[tt * wpt + w][e];
+        }
         const uint16_t lb = f32_to_bf16(v);
         if (logits_out != nullptr) logits_out[(int64_t)tt * E + e] = lb;
         float l = bf16_to_f32(lb);
@@ -296,12 +362,20 @@ route_small_kernel(const uint16_t *__restrict__ x, const uint16_t *__restrict__ 
 
   // Grouping: same outputs as permute_kernel (ascending expert, then ascending slot).
   const int n_slots = T * k;
+  // Counts by one thread per expert (the slots read as a broadcast), then the running
+  // offsets and the active list by thread 0 over the E counts.
+  __shared__ int32_t s_cnt[MOE_MAX_EXPERTS];
+  if (tid < E) {
+    int c = 0;
+    for (int s = 0; s < n_slots; ++s) c += s_idx[s] == tid;
+    s_cnt[tid] = c;
+    counts[tid] = c;
+  }
+  __syncthreads();
   if (tid == 0) {
     int run = 0, na = 0;
     for (int e = 0; e < E; ++e) {
-      int c = 0;
-      for (int s = 0; s < n_slots; ++s) c += s_idx[s] == e;
-      counts[e] = c;
+      const int c = s_cnt[e];
       offsets[e] = run;
       s_off[e] = run;
       if (c > 0) active[1 + na++] = e;
@@ -344,12 +418,14 @@ int launch_route_small(const void *x, const void *gate, const void *bias, int64_
                        (int32_t *)counts, (int32_t *)offsets, (int32_t *)perm_tok,
                        (int32_t *)slot_pos, (int32_t *)active, (uint32_t *)zero_word);
   };
-  if (E <= 8)
-    go(route_small_kernel<8>);
+  if (E <= 8 && H % kRouteChunk == 0)
+    go(route_small_kernel<8, true>);
+  else if (E <= 8)
+    go(route_small_kernel<8, false>);
   else if (E <= 16)
-    go(route_small_kernel<16>);
+    go(route_small_kernel<16, false>);
   else
-    go(route_small_kernel<32>);
+    go(route_small_kernel<32, false>);
   MOE_LAUNCH_CHECK();
   return MOE_STATUS_OK;
 }
