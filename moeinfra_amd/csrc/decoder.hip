@@ -10,6 +10,11 @@
 //                 positions pos0 + t; k and v written to the KV cache
 //   attention     grouped-query causal attention of T query rows against the cache
 //   gemv          y = bf16(W x) for up to 4 tokens (the decode projections and lm_head)
+// and the fused single-token forms of a decode step:
+//   qkv_rope      input norm + q/k/v projection + rotary + KV-cache write
+//   head_logits   final norm + lm_head + per-workgroup argmax candidates, and
+//   argmax_finish the token, the generated-id buffer, its counter and the position
+// (the post-attention norm runs inside the MoE layer's gate/up kernel, decode_layer.hip).
 #include "norm_row.h"
 
 namespace moe {
@@ -367,7 +372,8 @@ gemv1_kernel(const uint16_t *__restrict__ W, const uint16_t *__restrict__ x, int
 // ---------------------------------------------------------------- fused decode-step kernels
 // One token.  Each removes a launch (about 4-5 us of dependent latency at batch 1) by doing
 // a neighbouring step inside the projection kernel, with the same arithmetic and summation
-// order as the separate kernels, so the results are bit-identical to them.
+// order as the separate kernels, so the results are bit-identical to them.  No kernel here
+// waits for another workgroup: device-scope fences cost more than a launch on this part.
 constexpr int kFusedMaxH = 8192;  // norm chunks per thread: up to 4
 static_assert(kNormThreads == kGemvThreads, "the fused kernels run the norm and the GEMV in one workgroup");
 
