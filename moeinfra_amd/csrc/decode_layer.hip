@@ -532,6 +532,28 @@ __device__ __forceinline__ RouteSummary route_wave(RouteHead &rh, int32_t (&sl_e
     sl_e[t * k + e] = my_win;
     sl_w[t * k + e] = my_wn;
   }
+  if (T == 1) {
+    // One token: its k slots have k distinct experts, so each active expert holds exactly
+    // one slot, at the rank of its id among the chosen ones -- the same descriptor as the
+    // general grouping below, without gathering the slots.
+    const uint32_t present = (uint32_t)(__ballot(valid && taken) & 0xffffull);
+    if (lane < k) {
+      const int a = __builtin_popcount(present & ((1u << my_win) - 1u));
+      rh.perm_tok[a] = 0;
+      rh.slot_a[lane] = a;
+      rh.slot_m[lane] = 0;
+      rh.slot_w[lane] = my_wn;
+      rh.active[a] = my_win;
+      rh.counts[a] = 1;
+      rh.offsets[a] = a;
+    }
+    if (lane == 0) {
+      rh.n_active = k;
+      rh.bc = 1;
+    }
+    wave_lds_sync();
+    return RouteSummary{k, true, present};
+  }
   // Grouping of the ns = T*k slots (slot s = t*k + j lives in lane 16*(s/k) + s%k): the
   // slot experts are gathered into scalars, then lane s < ns places its slot with a few
   // compares against them -- no loop over the experts, no LDS round trip.
