@@ -228,10 +228,13 @@ class NativeDecoder:
                 and s.head_dim % 2 == 0)
 
     def _decode_layer_shape(self) -> bool:
-        """Whether the MoE layer runs as the single-token decode form (T = 1)."""
+        """Whether the MoE layer runs as the single-token decode form (T = 1): top-k <= 8,
+        at most 16 experts, H and F multiples of 512, at most 8 four-row output tiles of
+        the down GEMV per CU."""
         s = self.s
+        cu = torch.cuda.get_device_properties(self.dev).multi_processor_count
         return (s.top_k <= 8 and s.experts <= 16 and s.top_k <= s.experts and s.hidden % 512 == 0
-                and s.ffn % 512 == 0 and (s.hidden // 4 + 255) // 256 <= 8)
+                and s.ffn % 512 == 0 and (s.hidden // 4 + cu - 1) // cu <= 8)
 
     def _step_buffers(self) -> dict:
         if self._sb is None:
