@@ -19,7 +19,6 @@ projections; longer prompts use the library GEMM.
 from __future__ import annotations
 
 import dataclasses
-import math
 from typing import List, Optional
 
 import torch

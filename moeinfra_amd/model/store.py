@@ -19,7 +19,6 @@ from __future__ import annotations
 from pathlib import Path
 from typing import Iterable, Optional, Union
 
-import torch
 
 from .expert import PrequantizedNF4Expert
 
