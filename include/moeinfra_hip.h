@@ -197,7 +197,8 @@ int moe_layer_forward_nf4_profiled(const moe_nf4_expert_t *experts, int32_t E,
  * moe_layer_forward_nf4 of xn at T = 1 -- bit-identical to that sequence, in the layer's
  * two launches (every gate/up workgroup normalises the token itself).  No bias, no logits
  * output.  workspace: moe_layer_norm_workspace_bytes(k, E, H, F) bytes, 256-byte aligned;
- * H up to 8192. */
+ * H up to 8192.  residual_out must not overlap x or residual (refused: one workgroup
+ * writes it while the others read them). */
 int64_t moe_layer_norm_workspace_bytes(int32_t k, int32_t E, int32_t H, int32_t F);
 int moe_layer_forward_nf4_norm(const moe_nf4_expert_t *experts, int32_t E, const void *gate_bf16,
                                const void *x_bf16, const void *residual_bf16,
@@ -246,7 +247,8 @@ int moe_gemv_bf16(const void *weight, const void *x, int64_t T, int32_t N, int32
  * moe_qkv_rope_bf16: r = x[*x_row] (+ residual) -> residual_out (x_row: device int64, null
  * for row 0; rows outside [0, x_rows) clamp), then moe_add_rmsnorm_bf16 of r, the q/k/v
  * projection (weight [(n_q + 2 n_kv) * head_dim, H]) and moe_rope_kv_bf16 at *pos0: q to
- * q_out, k and v to the cache row *pos0.  H a multiple of 512 up to 8192. */
+ * q_out, k and v to the cache row *pos0.  H a multiple of 512 up to 8192.  residual_out
+ * must not overlap x (all x_rows rows) or residual (refused). */
 int moe_qkv_rope_bf16(const void *weight, const void *x, const void *x_row_i64, int64_t x_rows,
                       const void *residual, const void *norm_weight, float eps, int32_t H,
                       int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,

@@ -298,9 +298,13 @@ extern "C" int moe_layer_forward_nf4_norm(const moe_nf4_expert_t *experts, int32
   MOE_REQUIRE(k >= 1 && E >= 1 && H >= 1 && F >= 1, "bad sizes");
   MOE_REQUIRE(moe::decode_layer_supported(1, k, E, H, F),
               "shape not supported by the single-token decode layer");
-  MOE_REQUIRE(x_bf16 && residual_bf16 && norm_weight_bf16 && residual_out_bf16 && out_bf16 &&
-                  weights_f32 && idx_i64 && gate_bf16,
+  MOE_REQUIRE(experts && x_bf16 && residual_bf16 && norm_weight_bf16 && residual_out_bf16 &&
+                  out_bf16 && weights_f32 && idx_i64 && gate_bf16,
               "null pointer");
+  // Workgroup 0 writes residual_out while the others still read x and residual.
+  MOE_REQUIRE(!moe::ranges_overlap(residual_out_bf16, 2 * (int64_t)H, x_bf16, 2 * (int64_t)H) &&
+                  !moe::ranges_overlap(residual_out_bf16, 2 * (int64_t)H, residual_bf16, 2 * (int64_t)H),
+              "residual_out must not overlap x or residual");
   const int64_t need = moe_layer_norm_workspace_bytes(k, E, H, F);
   MOE_REQUIRE(workspace != nullptr && workspace_bytes >= need,
               "workspace too small: need %lld bytes, got %lld", (long long)need,

@@ -57,6 +57,17 @@ __device__ __forceinline__ float wave_sum(float v) {
     }                                                                                              \
   } while (0)
 
+namespace moe {
+// Host-side: whether the byte ranges [a, a + na) and [b, b + nb) share a byte (a null
+// pointer is an empty range).  Kernels in which one workgroup writes an output that other
+// workgroups still read as an input reject such pairs.
+inline bool ranges_overlap(const void *a, int64_t na, const void *b, int64_t nb) {
+  if (a == nullptr || b == nullptr || na <= 0 || nb <= 0) return false;
+  const uintptr_t pa = (uintptr_t)a, pb = (uintptr_t)b;
+  return pa < pb + (uintptr_t)nb && pb < pa + (uintptr_t)na;
+}
+}  // namespace moe
+
 #define MOE_HIP_CHECK(expr)                                                                        \
   do {                                                                                             \
     hipError_t _moe_err = (expr);                                                                  \

@@ -1209,6 +1209,7 @@ int launch_decode_layer(const moe_nf4_expert_t *experts, int32_t E, const void *
                         void *route_ws, void *h_ws, hipStream_t s, hipEvent_t *ev,
                         const void *norm) {
   MOE_REQUIRE(decode_layer_supported(T, k, E, H, F), "shape not supported by the decode layer");
+  MOE_REQUIRE(experts != nullptr, "null expert table");
   DecodeNorm nrm{};
   if (norm != nullptr) {
     nrm = *static_cast<const DecodeNorm *>(norm);

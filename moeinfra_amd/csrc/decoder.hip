@@ -696,6 +696,10 @@ extern "C" int moe_qkv_rope_bf16(const void *weight, const void *x, const void *
               "bad sizes");
   MOE_REQUIRE(weight && x && norm_weight && inv_freq_f32 && pos0_i32 && q_out && k_cache && v_cache,
               "null pointer");
+  // Workgroup 0 writes residual_out while the others still read x and residual.
+  MOE_REQUIRE(!moe::ranges_overlap(residual_out, 2 * (int64_t)H, x, 2 * (int64_t)H * x_rows) &&
+                  !moe::ranges_overlap(residual_out, 2 * (int64_t)H, residual, 2 * (int64_t)H),
+              "residual_out must not overlap x or residual");
   MOE_REQUIRE(((uintptr_t)weight | (uintptr_t)x | (uintptr_t)residual | (uintptr_t)norm_weight |
                (uintptr_t)residual_out) % 16 == 0,
               "weight, x, residual and norm tensors must be 16-byte aligned");
