@@ -301,10 +301,16 @@ extern "C" int moe_layer_forward_nf4_norm(const moe_nf4_expert_t *experts, int32
   MOE_REQUIRE(experts && x_bf16 && residual_bf16 && norm_weight_bf16 && residual_out_bf16 &&
                   out_bf16 && weights_f32 && idx_i64 && gate_bf16,
               "null pointer");
-  // Workgroup 0 writes residual_out while the others still read x and residual.
-  MOE_REQUIRE(!moe::ranges_overlap(residual_out_bf16, 2 * (int64_t)H, x_bf16, 2 * (int64_t)H) &&
-                  !moe::ranges_overlap(residual_out_bf16, 2 * (int64_t)H, residual_bf16, 2 * (int64_t)H),
-              "residual_out must not overlap x or residual");
+  // Workgroup 0 writes residual_out while the others still read x, residual, the norm
+  // weight and the gate; the down kernel writes out, which must not clobber residual_out.
+  const int64_t hb = 2 * (int64_t)H;
+  MOE_REQUIRE(!moe::ranges_overlap(residual_out_bf16, hb, x_bf16, hb) &&
+                  !moe::ranges_overlap(residual_out_bf16, hb, residual_bf16, hb) &&
+                  !moe::ranges_overlap(residual_out_bf16, hb, norm_weight_bf16, hb) &&
+                  !moe::ranges_overlap(residual_out_bf16, hb, gate_bf16, hb * E),
+              "residual_out must not overlap x, residual, norm_weight or the gate");
+  MOE_REQUIRE(!moe::ranges_overlap(out_bf16, hb, residual_out_bf16, hb),
+              "out must not overlap residual_out");
   const int64_t need = moe_layer_norm_workspace_bytes(k, E, H, F);
   MOE_REQUIRE(workspace != nullptr && workspace_bytes >= need,
               "workspace too small: need %lld bytes, got %lld", (long long)need,

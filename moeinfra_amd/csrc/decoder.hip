@@ -696,10 +696,15 @@ extern "C" int moe_qkv_rope_bf16(const void *weight, const void *x, const void *
               "bad sizes");
   MOE_REQUIRE(weight && x && norm_weight && inv_freq_f32 && pos0_i32 && q_out && k_cache && v_cache,
               "null pointer");
-  // Workgroup 0 writes residual_out while the others still read x and residual.
-  MOE_REQUIRE(!moe::ranges_overlap(residual_out, 2 * (int64_t)H, x, 2 * (int64_t)H * x_rows) &&
-                  !moe::ranges_overlap(residual_out, 2 * (int64_t)H, residual, 2 * (int64_t)H),
-              "residual_out must not overlap x or residual");
+  // Workgroup 0 writes residual_out while the others still read x, residual, the norm
+  // weight and the projection weight.
+  const int64_t hb = 2 * (int64_t)H;
+  const int64_t wrows = (int64_t)(n_q_heads + 2 * n_kv_heads) * head_dim;
+  MOE_REQUIRE(!moe::ranges_overlap(residual_out, hb, x, hb * x_rows) &&
+                  !moe::ranges_overlap(residual_out, hb, residual, hb) &&
+                  !moe::ranges_overlap(residual_out, hb, norm_weight, hb) &&
+                  !moe::ranges_overlap(residual_out, hb, weight, hb * wrows),
+              "residual_out must not overlap x, residual, norm_weight or the weight");
   MOE_REQUIRE(((uintptr_t)weight | (uintptr_t)x | (uintptr_t)residual | (uintptr_t)norm_weight |
                (uintptr_t)residual_out) % 16 == 0,
               "weight, x, residual and norm tensors must be 16-byte aligned");

@@ -88,7 +88,8 @@ expert_gemm_kernel(const ExpertTable tab, const uint16_t *__restrict__ act, int 
     int e = 0, cnt = 0, items = 0;
     if (lane < n_active) {
       e = rt.active[1 + lane];
-      cnt = rt.counts[e];
+      // An absent expert (all-null table entry) has no items.
+      cnt = (GATEUP ? tab.e[e].w1_packed : tab.e[e].w2_packed) != nullptr ? rt.counts[e] : 0;
       items = ((cnt + kGemmM - 1) / kGemmM) * n_tiles;
     }
     int incl = items;  // inclusive prefix sum over the lanes
@@ -108,13 +109,21 @@ expert_gemm_kernel(const ExpertTable tab, const uint16_t *__restrict__ act, int 
   // Codebooks: when every active expert holds the codebooks of the first one (the usual
   // case: one NF4 codebook for all tensors), the table is built once for the launch;
   // otherwise it is checked per item.
+  // The first present active expert supplies the reference codebooks; with none present
+  // there is no item (uniform over the grid, before any barrier).
+  int e0 = -1;
+  for (int a = 0; a < n_active && e0 < 0; ++a) {
+    const int e = rt.active[1 + a];
+    if ((GATEUP ? tab.e[e].w1_packed : tab.e[e].w2_packed) != nullptr) e0 = e;
+  }
+  if (e0 < 0) return;
   int cb_diff = 0;
   {
-    const int e0 = rt.active[1];
     const float *lo0 = (const float *)(GATEUP ? tab.e[e0].w1_code : tab.e[e0].w2_code);
     const float *hi0 = (const float *)(GATEUP ? tab.e[e0].w3_code : tab.e[e0].w2_code);
     for (int i = tid; i < n_active * 32; i += kGemmThreads) {
       const int e = rt.active[1 + (i >> 5)], j = i & 15;
+      if ((GATEUP ? tab.e[e].w1_packed : tab.e[e].w2_packed) == nullptr) continue;
       const float *lo = (const float *)(GATEUP ? tab.e[e].w1_code : tab.e[e].w2_code);
       const float *hi = (const float *)(GATEUP ? tab.e[e].w3_code : tab.e[e].w2_code);
       const float *x = (i & 16) ? hi : lo;
@@ -124,7 +133,7 @@ expert_gemm_kernel(const ExpertTable tab, const uint16_t *__restrict__ act, int 
   }
   const bool per_item_table = __syncthreads_or(cb_diff) != 0;  // also publishes s_ex
   if (!per_item_table) {
-    const moe_nf4_expert_t &ex0 = tab.e[s_ex[0][0]];
+    const moe_nf4_expert_t &ex0 = tab.e[e0];
     if (GATEUP)
       ensure_table<kGemmThreads>(s_tbl, s_raw, s_code, (const float *)ex0.w1_code, (const float *)ex0.w3_code, built);
     else

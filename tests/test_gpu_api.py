@@ -354,31 +354,39 @@ def test_nested_expert_from_store_to_gpu(cuda_device, tmp_path):
 
 def test_fused_entries_reject_overlapping_residual_out(cuda_device):
     """The fused single-token entry points write residual_out from one workgroup while the
-    others still read x and residual: an overlapping residual_out, or a null expert table,
-    is refused before any launch."""
+    others still read x, residual, the norm weight and the gate (or projection weight), and
+    the MoE layer's down kernel writes out afterwards: a residual_out overlapping any of
+    them, an out overlapping residual_out, or a null expert table, is refused before any
+    launch."""
     from moeinfra_amd import _lib
     lib = _lib.lib()
     H, F, E, k = 4096, 14336, 8, 2
-    buf = torch.zeros((4, H), dtype=torch.bfloat16, device=cuda_device)
-    x, res, other = buf[0].data_ptr(), buf[1].data_ptr(), buf[2].data_ptr()
+    nq, nkv, hd = 32, 8, 128
+    buf = torch.zeros((6, H), dtype=torch.bfloat16, device=cuda_device)
+    x, res, nw, out, good, misc = (buf[i].data_ptr() for i in range(6))
+    gate = torch.zeros((E, H), dtype=torch.bfloat16, device=cuda_device)
+    wqkv = torch.zeros(((nq + 2 * nkv) * hd, H), dtype=torch.bfloat16, device=cuda_device)
     table = (_lib.MoeNf4Expert * E)()
     ws = torch.zeros((1 << 20,), dtype=torch.uint8, device=cuda_device)
 
-    def layer(experts, res_out):
-        return lib.moe_layer_forward_nf4_norm(experts, E, other, x, res, other, 1e-5, H, F, k,
-                                              res_out, other, other, other, ws.data_ptr(),
+    def layer(experts, res_out, out_ptr=out):
+        return lib.moe_layer_forward_nf4_norm(experts, E, gate.data_ptr(), x, res, nw, 1e-5, H, F,
+                                              k, res_out, out_ptr, misc, misc, ws.data_ptr(),
                                               ws.numel(), None)
 
-    for bad in (x, res, x + 2 * H - 2):
+    for bad in (x, res, x + 2 * H - 2, nw, gate.data_ptr() + 6 * H):
         with pytest.raises(ValueError, match="must not overlap"):
             _lib.check(layer(table, bad), "layer_norm")
+    with pytest.raises(ValueError, match="out must not overlap residual_out"):
+        _lib.check(layer(table, good, out_ptr=good + 2), "layer_norm")
     with pytest.raises(ValueError, match="null"):
-        _lib.check(layer(None, buf[3].data_ptr()), "layer_norm")
+        _lib.check(layer(None, good), "layer_norm")
 
     def qkv(res_out, residual):
-        return lib.moe_qkv_rope_bf16(other, x, None, 1, residual, other, 1e-5, H, 32, 8, 128,
-                                     other, other, 16, res_out, other, other, other, None)
+        return lib.moe_qkv_rope_bf16(wqkv.data_ptr(), x, None, 1, residual, nw, 1e-5, H, nq, nkv,
+                                     hd, misc, misc, 16, res_out, misc, misc, misc, None)
 
-    for bad, residual in ((x, res), (res, res), (x, None)):
+    for bad, residual in ((x, res), (res, res), (x, None), (nw, res),
+                          (wqkv.data_ptr() + 2 * H * 100, res)):
         with pytest.raises(ValueError, match="must not overlap"):
             _lib.check(qkv(bad, residual), "qkv_rope")

@@ -265,6 +265,37 @@ def test_layer_batched_gemm_mixed_codebooks(cuda_device, H, F, T):
     assert err <= 1e-2, err
 
 
+# A layer whose table has an absent expert (all nine pointers null) that the router never
+# selects (a -1e4 logit bias): every kernel family skips it.  T = 24 runs the mid-batch
+# kernels, T = 300 the batched GEMM.
+@pytest.mark.parametrize("T", [24, 300])
+def test_layer_absent_expert(cuda_device, T):
+    from moeinfra_amd import ops
+    from moeinfra_amd._lib import MoeNf4Expert
+
+    H, F, E, absent = 512, 1024, 8, 3
+    gate, experts, x = build_layer(H, F, E, T, 70 + T)
+    bias = torch.zeros(E, dtype=torch.float32)
+    bias[absent] = -1.0e4
+    want, (lg_w, w_w, i_w) = oracle_layer(gate, experts, x, bias=bias)
+    assert not (i_w == absent).any()
+    structs = []
+    for e, ex in enumerate(experts):
+        if e == absent:
+            structs.append(MoeNf4Expert())
+        else:
+            ex.to(cuda_device)
+            structs.append(ex.c_struct())
+    table = ops.expert_table(structs)
+    out, _, w, idx = ops.layer_forward(table, E, gate.to(cuda_device), x.to(cuda_device), 2, F,
+                                       bias=bias.to(cuda_device))
+    torch.cuda.synchronize()
+    ok = ~near_tie_rows(lg_w, bias=bias.numpy())
+    np.testing.assert_array_equal(idx.cpu().numpy()[ok], i_w[ok])
+    err = orc.rel_l2(orc.bf16_to_f32(bits(out)[ok]), orc.bf16_to_f32(want[ok]))
+    assert err <= 1e-2, err
+
+
 # ------------------------------------------------------------------------------ mid-size batches
 # Between the decode form (T <= 4) and the batched GEMM (>= 32 routed rows per expert on
 # average) the layer runs the mid-batch kernels (expert_skinny.hip): 32-token chunks per
