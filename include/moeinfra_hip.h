@@ -5,10 +5,11 @@
  * Every entry point takes raw device pointers, 64-bit sizes and a hipStream_t
  * (passed as void*), enqueues its kernels on that stream, performs no host<->device
  * synchronisation and allocates no memory: the caller owns every buffer, including the
- * workspace.  Calls return MOE_STATUS_OK (0) or a negative status; the message of the
- * last failure on the calling thread is returned by moe_last_error().  Calls on one
- * stream are ordered; the library keeps no mutable global state besides a per-device
- * cache of the compute-unit count.
+ * workspace (moe_layer_forward_nf4_noalloc uses the library's static scratch instead).
+ * Calls return MOE_STATUS_OK (0) or a negative status; the message of the last failure on
+ * the calling thread is returned by moe_last_error().  Calls on one stream are ordered;
+ * the library keeps no mutable global state besides per-device caches of the
+ * compute-unit count and of the static scratch's address.
  *
  * Data formats (bitsandbytes NF4, as the reference stores it):
  *   - a weight W[O][I] is the row-major flatten of O*I values quantised in blocks of
@@ -190,6 +191,22 @@ int moe_layer_forward_nf4_profiled(const moe_nf4_expert_t *experts, int32_t E,
                                    int32_t k, void *out_bf16, void *logits_bf16,
                                    void *weights_f32, void *idx_i64, void *workspace,
                                    int64_t workspace_bytes, void *const *events, void *stream);
+
+/* Allocation-free form of moe_layer_forward_nf4.  No counterpart in the reference: it is
+ * for callers that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  Same kernels and results as
+ * moe_layer_forward_nf4; the workspace is the library's static per-device scratch of
+ * MOE_NOALLOC_SCRATCH_BYTES (each device holds it until the process ends), and the call
+ * allocates nothing.  Layers whose workspace (moe_layer_workspace_bytes) exceeds the
+ * scratch are refused with MOE_STATUS_INVALID_ARGUMENT (Mixtral-8x7B shape: T <= 744 at
+ * k = 2).  Every call on a device shares that device's scratch: calls that overlap on one
+ * device (two streams, two threads) race. */
+#define MOE_NOALLOC_SCRATCH_BYTES (64ll << 20)
+int moe_layer_forward_nf4_noalloc(const moe_nf4_expert_t *experts, int32_t E,
+                                  const void *gate_bf16, const void *bias_f32,
+                                  const void *x_bf16, int64_t T, int32_t H, int32_t F,
+                                  int32_t k, void *out_bf16, void *logits_bf16,
+                                  void *weights_f32, void *idx_i64, void *stream);
 
 /* Single-token layer with the decoder's post-attention residual add and RMSNorm in front
  * (engine/decoder_layer.py:37-41 feeds the MoE block post_attention_layernorm(h + attn)):

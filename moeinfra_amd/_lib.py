@@ -18,6 +18,7 @@ MOE_STATUS_UNSUPPORTED = -3
 MOE_MAX_EXPERTS = 32
 MOE_MAX_TOPK = 8
 MOE_NF4_BLOCKSIZE = 64
+MOE_NOALLOC_SCRATCH_BYTES = 64 << 20
 
 _vp = ctypes.c_void_p
 _i32 = ctypes.c_int32
@@ -57,6 +58,8 @@ SIGNATURES = {
     "moe_layer_workspace_bytes": ([_i64, _i32, _i32, _i32, _i32], ctypes.c_int64),
     "moe_layer_forward_nf4": ([ctypes.POINTER(MoeNf4Expert), _i32, _vp, _vp, _vp, _i64, _i32,
                                _i32, _i32, _vp, _vp, _vp, _vp, _vp, _i64, _vp], ctypes.c_int),
+    "moe_layer_forward_nf4_noalloc": ([ctypes.POINTER(MoeNf4Expert), _i32, _vp, _vp, _vp, _i64,
+                                       _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp], ctypes.c_int),
     "moe_layer_forward_nf4_profiled": ([ctypes.POINTER(MoeNf4Expert), _i32, _vp, _vp, _vp, _i64,
                                         _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _i64,
                                         ctypes.POINTER(_vp), _vp], ctypes.c_int),

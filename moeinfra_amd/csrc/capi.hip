@@ -326,3 +326,56 @@ extern "C" int moe_layer_forward_nf4_norm(const moe_nf4_expert_t *experts, int32
                                   nullptr, weights_f32, idx_i64, moe::at<void>(workspace, w.droute),
                                   moe::at<void>(workspace, w.h), (hipStream_t)stream, nullptr, &nrm);
 }
+
+// ----------------------------------------------------------------- allocation-free layer
+namespace moe {
+namespace {
+// The workspace of moe_layer_forward_nf4_noalloc.  Every device the library runs on holds
+// its own copy, at its own address, until the process ends; in host code the name is a
+// stand-in, so kernels get the device address from scratch_address().
+static __device__ __align__(256) unsigned char scratch[MOE_NOALLOC_SCRATCH_BYTES];
+
+void *g_scratch_addr[kMaxDevices] = {};
+std::mutex g_scratch_mutex;
+
+// Device address of `scratch` on the current device, looked up once per device.
+int scratch_address(void **addr) {
+  int dev = 0;
+  MOE_HIP_CHECK(hipGetDevice(&dev));
+  MOE_REQUIRE(dev >= 0 && dev < kMaxDevices, "device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_addr[dev] == nullptr) {
+    void *p = nullptr;
+    MOE_HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    MOE_REQUIRE(p != nullptr && ((uintptr_t)p % 256) == 0, "scratch address lookup failed");
+    g_scratch_addr[dev] = p;
+  }
+  *addr = g_scratch_addr[dev];
+  return MOE_STATUS_OK;
+}
+}  // namespace
+}  // namespace moe
+
+// The layer's kernels write every workspace region they read (the descriptor, grouping
+// arrays and h before their consumers, the completion word through the routing kernel), so
+// nothing in the scratch has to start at zero and no memset is issued.
+extern "C" int moe_layer_forward_nf4_noalloc(const moe_nf4_expert_t *experts, int32_t E,
+                                             const void *gate_bf16, const void *bias_f32,
+                                             const void *x_bf16, int64_t T, int32_t H,
+                                             int32_t F, int32_t k, void *out_bf16,
+                                             void *logits_bf16, void *weights_f32,
+                                             void *idx_i64, void *stream) {
+  MOE_REQUIRE(T >= 0 && k >= 1 && E >= 1 && H >= 1 && F >= 1, "bad sizes");
+  if (T == 0) return MOE_STATUS_OK;
+  const int64_t need = moe::layer_ws(T, k, E, H, F).total;
+  MOE_REQUIRE(need <= MOE_NOALLOC_SCRATCH_BYTES,
+              "layer needs %lld bytes of workspace, above the %lld-byte static scratch; call "
+              "moe_layer_forward_nf4 with a workspace",
+              (long long)need, (long long)MOE_NOALLOC_SCRATCH_BYTES);
+  void *ws = nullptr;
+  const int rc = moe::scratch_address(&ws);
+  if (rc != MOE_STATUS_OK) return rc;
+  return moe::layer_forward(experts, E, gate_bf16, bias_f32, x_bf16, T, H, F, k, out_bf16,
+                            logits_bf16, weights_f32, idx_i64, ws, MOE_NOALLOC_SCRATCH_BYTES,
+                            (hipStream_t)stream, nullptr);
+}

@@ -1,0 +1,89 @@
+"""The allocation-free layer entry point (moe_layer_forward_nf4_noalloc), called through the
+C ABI, against moe_layer_forward_nf4 with a caller workspace: bit-identical outputs on
+consecutive calls that shrink (mid-batch T = 40, fused small-batch routing T = 16, decode
+form T = 3), so the static scratch's leftovers from a larger call change nothing; layers
+whose workspace exceeds the scratch are refused before any launch."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import bits
+
+pytestmark = pytest.mark.gpu
+
+
+def _experts(dev, H, F, E, seed):
+    from moeinfra_amd import ops
+    from moeinfra_amd._lib import MoeNf4Expert
+
+    g = torch.Generator(device=dev).manual_seed(seed)
+    keep = []
+    for _ in range(E):
+        st = {}
+        for name, shape in (("w1", (F, H)), ("w3", (F, H)), ("w2", (H, F))):
+            w = (torch.randn(shape, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+            st[name] = ops.nf4_quantize(w)
+        keep.append(st)
+    table = ops.expert_table([MoeNf4Expert(*(t.data_ptr() for n in ("w1", "w3", "w2")
+                                             for t in st[n])) for st in keep])
+    gate = (torch.randn((E, H), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    return keep, table, gate
+
+
+def _run(lib, table, E, gate, bias, x, F, k, noalloc):
+    from moeinfra_amd import _lib
+
+    dev = x.device
+    T, H = x.shape
+    out = torch.full((T, H), -1.0, dtype=torch.bfloat16, device=dev)
+    logits = torch.full((T, E), -1.0, dtype=torch.bfloat16, device=dev)
+    w = torch.full((T, k), -1.0, dtype=torch.float32, device=dev)
+    idx = torch.full((T, k), -1, dtype=torch.int64, device=dev)
+    bptr = None if bias is None else bias.data_ptr()
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    if noalloc:
+        rc = lib.moe_layer_forward_nf4_noalloc(table, E, gate.data_ptr(), bptr, x.data_ptr(), T, H,
+                                               F, k, out.data_ptr(), logits.data_ptr(),
+                                               w.data_ptr(), idx.data_ptr(), stream)
+    else:
+        ws_bytes = lib.moe_layer_workspace_bytes(T, k, E, H, F)
+        ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=dev)
+        rc = lib.moe_layer_forward_nf4(table, E, gate.data_ptr(), bptr, x.data_ptr(), T, H, F, k,
+                                       out.data_ptr(), logits.data_ptr(), w.data_ptr(),
+                                       idx.data_ptr(), ws.data_ptr(), ws_bytes, stream)
+    _lib.check(rc, "noalloc" if noalloc else "layer")
+    torch.cuda.synchronize(dev)
+    return bits(out), bits(logits), w.cpu().numpy(), idx.cpu().numpy()
+
+
+def test_noalloc_layer_matches_workspace_layer(cuda_device):
+    from moeinfra_amd import _lib, synth
+
+    lib = _lib.lib()
+    H, F, E, k = 1024, 3584, 8, 2
+    _keep, table, gate = _experts(cuda_device, H, F, E, seed=910)
+    g = torch.Generator(device=cuda_device).manual_seed(911)
+    for T, skew in ((40, True), (16, False), (3, False)):
+        print(f"noalloc layer T={T} skew={skew}", flush=True)
+        x = torch.randn((T, H), generator=g, device=cuda_device).to(torch.bfloat16)
+        bias = synth.zipf_bias(E, T).to(cuda_device) if skew else None
+        got = _run(lib, table, E, gate, bias, x, F, k, noalloc=True)
+        want = _run(lib, table, E, gate, bias, x, F, k, noalloc=False)
+        for a, b in zip(got, want):
+            np.testing.assert_array_equal(a, b)
+
+
+def test_noalloc_refuses_a_layer_above_the_scratch():
+    from moeinfra_amd import _lib
+
+    lib = _lib.lib()
+    H, F, E, k = 4096, 14336, 8, 2
+    assert lib.moe_layer_workspace_bytes(744, k, E, H, F) <= _lib.MOE_NOALLOC_SCRATCH_BYTES
+    assert lib.moe_layer_workspace_bytes(745, k, E, H, F) > _lib.MOE_NOALLOC_SCRATCH_BYTES
+    # Null outputs as well: a refusal happens before any launch either way.
+    rc = lib.moe_layer_forward_nf4_noalloc(None, E, None, None, None, 745, H, F, k, None, None,
+                                           None, None, None)
+    assert rc == _lib.MOE_STATUS_INVALID_ARGUMENT
+    assert "static scratch" in lib.moe_last_error().decode()
