@@ -143,6 +143,39 @@ class RefDecoder:
         return h + self._moe(L, rmsnorm(h, L["post"], s.rms_eps))
 
     @torch.no_grad()
+    def layer_parts(self, li: int, h: torch.Tensor, resid: torch.Tensor = None):
+        """Layer li split at its residual add, teacher-forced: the attention block's output
+        for input h [T, H] at the current position (keys/values appended), and the MoE
+        block's output (with its routing) on post_norm(resid), where resid is the caller's
+        post-attention residual stream (default bf16(h + attention)).  Does not advance the
+        position.  Returns (attention [T, H], moe [T, H] bf16, (logits, w, idx))."""
+        s, L = self.s, self.layers[li]
+        attn = self._attention(li, L, rmsnorm(h, L["inn"], s.rms_eps))
+        if resid is None:
+            resid = h + attn
+        x2 = rmsnorm(resid, L["post"], s.rms_eps)
+
+        wide = L.setdefault("cache_f32", {})
+
+        def expert_fn(e, rows):
+            if e not in wide:
+                wide[e] = tuple(orc.bf16_to_f32(w) for w in
+                                orc.dequant_expert(L["states"][e], s.hidden, s.ffn, threads=self.threads))
+            return orc.swiglu_f32(rows, *wide[e])
+
+        out, routing = orc.moe_layer(_bits(x2), _bits(L["gate"]), expert_fn, k=s.top_k)
+        return attn, _from_bits(out), routing
+
+    def advance(self, n: int) -> None:
+        """Moves the position on by n tokens (after layer_parts calls for them)."""
+        self.pos += int(n)
+
+    @torch.no_grad()
+    def head(self, h: torch.Tensor) -> torch.Tensor:
+        """Final norm + lm_head of the last row of the residual stream h: fp32 logits [1, V]."""
+        return (rmsnorm(h, self.final_norm, self.s.rms_eps)[-1:] @ self.lm_head.t()).float()
+
+    @torch.no_grad()
     def forward(self, ids) -> torch.Tensor:
         s = self.s
         h = self.embed[torch.as_tensor(ids, dtype=torch.long)]

@@ -246,12 +246,18 @@ def swiglu(x: np.ndarray, w1: np.ndarray, w3: np.ndarray, w2: np.ndarray) -> np.
     transfer/nf4_reconstruct.py:152-155: each linear returns the activation dtype (bf16),
     ``F.silu`` and ``*`` are bf16 ops computed in fp32 and rounded.
     """
+    return swiglu_f32(x, bf16_to_f32(w1), bf16_to_f32(w3), bf16_to_f32(w2))
+
+
+def swiglu_f32(x: np.ndarray, w1f: np.ndarray, w3f: np.ndarray, w2f: np.ndarray) -> np.ndarray:
+    """``swiglu`` with the dequantised weights already widened to float32 (each bf16 value
+    exactly), so that a caller running one expert many times converts them once."""
     xf = bf16_to_f32(x)
-    g = bf16_round(xf @ bf16_to_f32(w1).T)
-    u = bf16_round(xf @ bf16_to_f32(w3).T)
+    g = bf16_round(xf @ w1f.T)
+    u = bf16_round(xf @ w3f.T)
     s = bf16_round(silu_f32(bf16_to_f32(g)))
     h = bf16_round(bf16_to_f32(s) * bf16_to_f32(u))
-    return bf16_round(bf16_to_f32(h) @ bf16_to_f32(w2).T)
+    return bf16_round(bf16_to_f32(h) @ w2f.T)
 
 
 def dequant_expert(state: dict, hidden: int, inter: int, code: np.ndarray = NF4_CODE,

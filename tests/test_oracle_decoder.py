@@ -113,3 +113,59 @@ def test_attention_block_is_mixtral_attention_with_cache():
         got = dor.attention(q, kc, vc, pos, 32 ** -0.5) @ att.o_proj.weight.detach().t()
         _same(got, want[0])
         pos = S
+
+
+def _tiny_weights(seed=0):
+    """A 2-layer decoder weights object (the DecoderWeights fields the oracle reads) with
+    experts quantised by the oracle."""
+    import types
+
+    from oracle import moe_oracle as orc
+
+    s = types.SimpleNamespace(hidden=128, ffn=256, n_heads=4, n_kv_heads=2, head_dim=32, vocab=50,
+                              experts=4, top_k=2, rope_theta=1e6, rms_eps=1e-5)
+    g = lambda shape, i, std=0.02: _bf16(shape, seed * 100 + i, std)
+    u16 = lambda t: t.contiguous().view(torch.int16).numpy().view(np.uint16).reshape(-1)
+    layers = []
+    for li in range(2):
+        experts = []
+        for e in range(s.experts):
+            st = {}
+            for j, (name, shape) in enumerate((("w1", (s.ffn, s.hidden)), ("w3", (s.ffn, s.hidden)),
+                                              ("w2", (s.hidden, s.ffn)))):
+                p, a = orc.nf4_quantize(u16(g(shape, 10 + 10 * li + 3 * e + j)))
+                st[name] = (torch.from_numpy(p), torch.from_numpy(a), torch.from_numpy(orc.NF4_CODE.copy()))
+            experts.append(st)
+        qkv_rows = (s.n_heads + 2 * s.n_kv_heads) * s.head_dim
+        layers.append(types.SimpleNamespace(
+            input_norm=g((s.hidden,), 1 + li, 1.0), qkv=g((qkv_rows, s.hidden), 3 + li),
+            o_proj=g((s.hidden, s.n_heads * s.head_dim), 5 + li), post_norm=g((s.hidden,), 7 + li, 1.0),
+            gate=g((s.experts, s.hidden), 9 + li), experts=experts))
+    return types.SimpleNamespace(shape=s, embed=g((s.vocab, s.hidden), 90, 1.0), layers=layers,
+                                 final_norm=g((s.hidden,), 91, 1.0), lm_head=g((s.vocab, s.hidden), 92))
+
+
+def test_layer_parts_compose_to_the_layer_and_forward():
+    """layer_parts (attention, MoE at a given residual) and head() recompose forward(): the
+    two residual adds of each layer in bf16 give forward()'s logits bit for bit, over a
+    prompt and a decode token; an explicit residual equal to the default gives the same MoE
+    output, and a different one changes it (the residual is really used)."""
+    w = _tiny_weights()
+    whole, parts, forced = (dor.RefDecoder(w, threads=1) for _ in range(3))
+    for step in ([3, 17, 42, 8, 0], [11]):
+        want = whole.forward(step)
+        h = parts.embed[torch.as_tensor(step)]
+        for li in range(2):
+            attn, moe, (_lg, wts, idx) = parts.layer_parts(li, h)
+            assert idx.shape == (len(step), 2) and np.allclose(wts.sum(-1), 1.0, atol=1e-6)
+            attn_f, moe_f, _ = forced.layer_parts(li, h, resid=h + attn)
+            _same(attn_f, attn)
+            _same(moe_f, moe)
+            h = (h + attn) + moe
+        parts.advance(len(step))
+        forced.advance(len(step))
+        _same(parts.head(h).to(torch.bfloat16), want.to(torch.bfloat16))
+    other = dor.RefDecoder(w, threads=1)
+    h = other.embed[torch.as_tensor([5, 6])]
+    _a, moe0, _ = other.layer_parts(0, h, resid=h)
+    assert not torch.equal(moe0, dor.RefDecoder(w, threads=1).layer_parts(0, h)[1])
