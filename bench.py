@@ -48,8 +48,13 @@ def parse_args():
                    help="e2e mode with the NF4 store in pinned host memory and a bounded GPU cache")
     p.add_argument("--gpu-expert-slots", type=int, default=8,
                    help="GPU expert cache slots in offload mode (the reference's default: 8)")
-    p.add_argument("--prefetch", choices=["none", "next_layer", "lookahead"], default="none",
+    p.add_argument("--prefetch", choices=["none", "next_layer", "lookahead", "next_router"],
+                   default="none",
                    help="offload mode's prefetch policy (the reference engine's default: none)")
+    p.add_argument("--gpu-slots-per-layer", type=int, default=None,
+                   help="offload mode: partition the GPU expert tier by layer and keep the "
+                        "experts each layer transferred (default: the reference's contract, "
+                        "transferred experts are demoted after their layer)")
     p.add_argument("--prefetch-depth", type=int, default=2)
     p.add_argument("--tokens", type=int, default=1, help="tokens per decode step (decode mode)")
     p.add_argument("--routing", choices=["uniform", "zipf"], default="uniform")
@@ -321,12 +326,12 @@ def _e2e(args) -> int:
     t_setup = time.time()
     w = synthesize(s, seed=args.seed, device=dev, experts_on="cpu" if args.offload else None)
     prompt = torch.randint(0, s.vocab, (1, P), generator=torch.Generator().manual_seed(args.seed))
-    policy = {"none": PrefetchPolicy.NONE, "next_layer": PrefetchPolicy.NEXT_LAYER,
-              "lookahead": PrefetchPolicy.LOOKAHEAD}[args.prefetch]
+    policy = PrefetchPolicy(args.prefetch)
     eng = InferenceEngine(w, max_seq=P + max(Ksteps, W) + 8, device=dev, offload=args.offload,
                           gpu_expert_slots=args.gpu_expert_slots if args.offload else None,
                           prefetch=policy if args.offload else PrefetchPolicy.NONE,
-                          prefetch_depth=args.prefetch_depth)
+                          prefetch_depth=args.prefetch_depth,
+                          gpu_slots_per_layer=args.gpu_slots_per_layer if args.offload else None)
     _log(f"weights synthesized, engine built ({time.time() - t_setup:.1f} s)")
     eng.prepare(Ksteps + 1)
     torch.cuda.synchronize()
@@ -339,6 +344,7 @@ def _e2e(args) -> int:
     torch.cuda.synchronize()
     warm_s = time.time() - t_w
     # Timed: prefill (ttft), then exactly Ksteps decode steps between two synchronizations.
+    copies0 = dict(eng.transfer_scheduler.copies) if args.offload else None
     res = eng.generate(ForwardRequest(prompt, max_new_tokens=Ksteps + 1))
     decode_ms = res.stage_timings["decode"]
     ms_per_step = decode_ms / Ksteps
@@ -378,7 +384,8 @@ def _e2e(args) -> int:
     if args.offload:
         st = eng.cache_manager.stats()
         config.update({"gpu_expert_slots": args.gpu_expert_slots, "prefetch": args.prefetch,
-                       "prefetch_depth": args.prefetch_depth})
+                       "prefetch_depth": args.prefetch_depth,
+                       "gpu_slots_per_layer": args.gpu_slots_per_layer})
     result = {
         "metric": METRIC,
         "value": round(res.tps, 3),
@@ -411,8 +418,22 @@ def _e2e(args) -> int:
                                     "note": "the 32 MoE layers alone on fixed N(0,1) inputs, T=1; "
                                             "roofline events are in this pass's timed region"}
     if args.offload:
-        result["offload_stats"] = {"cache_evictions": st.evictions,
-                                   "expert_bytes": int(nf4_expert_bytes(s.hidden, s.ffn))}
+        c1 = eng.transfer_scheduler.copies
+        moved = c1["bytes"] - copies0["bytes"]
+        from moeinfra_amd.transfer import scheduler as sched_mod
+        staging = [p.get("staging_ms", 0.0) for p in sched_mod.EXECUTE_NEXT_PROFILE]
+        pe = eng.prefetch_engine
+        result["offload_stats"] = {
+            "cache_evictions": st.evictions,
+            "expert_bytes": int(nf4_expert_bytes(s.hidden, s.ffn)),
+            "pinned_store_bytes": eng.pinned_store.pinned_bytes,
+            "copies_in_timed_run": {k: c1[k] - copies0[k] for k in ("image", "staged")},
+            "copies_per_decode_step": round((c1["image"] + c1["staged"] - copies0["image"]
+                                             - copies0["staged"]) / (Ksteps + 1), 2),
+            "host_link_gbps_timed_run": round(moved / ((res.ttft_ms + decode_ms) * 1e-3) / 1e9, 2),
+            "execute_next_staging_ms_max": round(max(staging), 4) if staging else None,
+            "prefetch": None if pe is None else dict(pe.counts),
+        }
     print(json.dumps(result), flush=True)
     return 0
 

@@ -10,11 +10,12 @@ Two expert modes, as in the reference:
   is one call of the layer entry point, and the whole decode step (embedding, 32 decoder
   layers, final norm, lm_head, argmax, position advance) is captured once as a HIP graph
   and replayed per token.  Generated ids stay on the device until the end.
-* offload: the NF4 store lives in pinned host memory (CacheManager CPU tier) with a bounded
-  GPU tier; each layer's MoE block is the reference's MoELayer (route, make the routed
-  experts resident through the transfer scheduler's staged H2D, compute, demote the ones
-  that were not resident), optionally with the PrefetchEngine starting the next layer's
-  copies on the side stream.
+* offload: the NF4 store is pinned once in host memory (CacheManager CPU tier) with a
+  bounded GPU tier in a device-slot arena; each layer's MoE block is the reference's
+  MoELayer (route, start the copies of the routed experts that are not resident as single
+  hipMemcpyAsync calls on a side stream, run the kernels behind stream waits on their
+  events, demote the ones that were not resident), optionally with a per-layer GPU tier
+  that keeps transferred experts and with the PrefetchEngine starting later layers' copies.
 """
 from __future__ import annotations
 
@@ -35,7 +36,8 @@ class InferenceEngine:
     def __init__(self, weights: DecoderWeights, max_seq: int = 1024, device="cuda:0",
                  offload: bool = False, gpu_expert_slots: Optional[int] = None,
                  prefetch: PrefetchPolicy = PrefetchPolicy.NONE, prefetch_depth: int = 1,
-                 use_graph: bool = True, logger: Optional[logging.Logger] = None) -> None:
+                 use_graph: bool = True, logger: Optional[logging.Logger] = None,
+                 gpu_slots_per_layer: Optional[int] = None) -> None:
         self._logger = logger or logging.getLogger(__name__)
         self.device = torch.device(device)
         self.weights = weights
@@ -45,59 +47,77 @@ class InferenceEngine:
         self.cache_manager = None
         self.transfer_scheduler = None
         self.prefetch_engine = None
+        self.pinned_store = None
         moe = None
         if offload:
-            moe = self._build_offload(gpu_expert_slots, prefetch, prefetch_depth)
+            moe = self._build_offload(gpu_expert_slots, prefetch, prefetch_depth,
+                                      gpu_slots_per_layer)
         self.decoder = NativeDecoder(weights, max_seq, self.device, moe=moe)
         self._graph = None
         self._last_logits = None
 
     # ------------------------------------------------------------------ offload wiring
-    def _build_offload(self, gpu_slots, policy, depth):
+    def _build_offload(self, gpu_slots, policy, depth, slots_per_layer):
+        """The host-authoritative offload mode: every expert pinned once in host memory
+        (one arena per layer) as the CacheManager's CPU tier; a bounded GPU tier of
+        `gpu_slots` experts (default: all) in a preallocated device-slot arena, filled by
+        single-copy host-to-device transfers on a side stream that the compute stream waits
+        for with events.  With `slots_per_layer` the GPU tier is partitioned by layer and
+        layers keep the experts they transferred (otherwise they are demoted after the
+        layer, the reference's contract)."""
         from ..cache.manager import CacheManager
         from ..cache.types import EvictionPolicy
         from ..model.expert import PrequantizedNF4Expert
         from ..model.moe_layer import MoELayer
-        from ..transfer.pinned_memory import PinnedMemoryBudget
-        from ..transfer.reusable_staging import ReusablePinnedStagingPool
+        from ..transfer.device_slots import DeviceExpertSlots
+        from ..transfer.host_store import PinnedExpertStore
         from ..transfer.scheduler import TransferScheduler
         from .router import ExpertRouter
 
         s = self.weights.shape
         n_experts = s.layers * s.experts
-        gpu_slots = n_experts if gpu_slots is None else int(gpu_slots)
-        cm = CacheManager(gpu_slots=max(gpu_slots, 1), cpu_slots=n_experts, policy=EvictionPolicy.LRU)
+        gpu_slots = n_experts if gpu_slots is None else max(1, int(gpu_slots))
+        if slots_per_layer is not None:
+            gpu_slots = min(gpu_slots, slots_per_layer * s.layers)
+        cm = CacheManager(gpu_slots=gpu_slots, cpu_slots=n_experts, policy=EvictionPolicy.LRU,
+                          gpu_slots_per_layer=slots_per_layer)
+        store = PinnedExpertStore()
         for l, lw in enumerate(self.weights.layers):
-            for e, st in enumerate(lw.experts):
-                ex = PrequantizedNF4Expert.from_nf4_tensors(
-                    {n: (p.cpu(), a.cpu(), c.cpu()) for n, (p, a, c) in st.items()}, s.hidden, s.ffn)
+            src = [PrequantizedNF4Expert.from_nf4_tensors(st, s.hidden, s.ffn) for st in lw.experts]
+            for e, ex in enumerate(store.add_layer(src)):
                 cm.put(l, e, ex, device="cpu")
-        slot_bytes = cm.get_size_bytes(0, 0)
-        n_slots = 2 * s.experts
-        pool = ReusablePinnedStagingPool(PinnedMemoryBudget(n_slots * slot_bytes), slot_bytes)
+        self.pinned_store = store
+        image_bytes = cm.peek_cpu(0, 0).image_layout.nbytes
         self._transfer_stream = torch.cuda.Stream(self.device)
-        sched = TransferScheduler(cm, 24.0, n_slots, staging_pool=pool,
-                                  transfer_stream=self._transfer_stream)
+        slots = DeviceExpertSlots(gpu_slots, image_bytes, self.device)
+        sched = TransferScheduler(cm, 24.0, max(2 * s.experts, 2 * s.top_k * max(depth, 1)),
+                                  transfer_stream=self._transfer_stream, device_slots=slots)
         self.cache_manager, self.transfer_scheduler = cm, sched
         if policy != PrefetchPolicy.NONE:
             self.prefetch_engine = PrefetchEngine(cm, sched, policy, depth, logger=self._logger)
+        retain = slots_per_layer is not None
         self._moe_layers = [MoELayer(l, ExpertRouter(lw.gate, s.top_k), cm, None, sched,
-                                     logger=self._logger)
+                                     logger=self._logger, retain_transferred=retain)
                             for l, lw in enumerate(self.weights.layers)]
         return self._moe_offload
 
     def _moe_offload(self, l: int, x: torch.Tensor) -> torch.Tensor:
         pe = self.prefetch_engine
-        if pe is not None:
-            # This layer's prefetched copies finish before it routes (their events are on
-            # the side stream); the compute stream waits for the side stream's work.
-            torch.cuda.current_stream(self.device).wait_stream(self._transfer_stream)
-            self._transfer_stream.synchronize()
-            pe.poll()
+        if pe is None:
+            return self._moe_layers[l].forward(x)
+        pe.poll()
+        nxt = None
+        if pe.policy == PrefetchPolicy.NEXT_ROUTER and l + 1 < len(self._moe_layers):
+            # Enqueued before this layer's routing: the layer's own read-back of its routed
+            # set covers it, so the guess costs no extra host synchronisation.
+            nxt, _ = self._moe_layers[l + 1].router.route(x)
         out = self._moe_layers[l].forward(x)
-        if pe is not None:
-            idx, _ = self._moe_layers[l].router.route(x)
-            pe.on_layer_complete(l, idx)
+        if nxt is not None:
+            pe.poll()
+            pe.cancel_stale(l + 1)
+            pe.prefetch(l + 1, nxt.reshape(-1).tolist())
+        elif pe.policy != PrefetchPolicy.NEXT_ROUTER:
+            pe.on_layer_complete(l, self._moe_layers[l].last_expert_indices)
         return out
 
     # ------------------------------------------------------------------ generate

@@ -1,17 +1,33 @@
-"""Expert prefetch ahead of the compute (mirrors engine/prefetch.py:53-309 of the reference).
+"""Expert prefetch: the PrefetchEngine API of the reference's engine/prefetch.py:53-309
+(schedule_prefetch / on_layer_complete / cancel_stale, policies NONE / NEXT_LAYER /
+LOOKAHEAD), plus NEXT_ROUTER.
 
-After a layer completes, the experts it routed to are taken as the prediction for the next
-layer (NEXT_LAYER) or the next ``depth`` layers (LOOKAHEAD) and their CPU->GPU copies are
-started on the transfer scheduler's side stream (``submit_async``), so that the H2D of
-layer l+1 overlaps the compute of layer l.  Requests for layers already passed are cancelled.
-Same policy names, method names, return values and bookkeeping as the reference.
+A prefetch is a low-priority ``submit_async`` on the transfer scheduler: the expert's copy
+starts on the transfer stream and the expert joins the GPU tier behind the copy's event,
+so a layer that routes to it later finds it resident and only orders its kernels after the
+copy.  What differs between the policies is the prediction of which (layer, expert) pairs
+to start:
+
+* NONE: nothing.
+* NEXT_LAYER / LOOKAHEAD (the reference's heuristic, prefetch.py:177-192): the experts the
+  completed layer routed to, for the next layer or the next ``depth`` layers.
+* NEXT_ROUTER: the caller supplies the prediction through ``prefetch(layer, experts)`` --
+  the engine runs the next layer's router on the current layer's MoE input.
+
+On a host link that is already saturated by demand copies (the offload decode loop moves
+two 99 MB experts per layer over PCIe) a wrong guess costs a whole copy while a right one
+saves only the gap between two layers' copies; DESIGN.md's offload section has the numbers.
+
+``_in_flight`` maps (layer_id, expert_id) to the request id of each prefetch still in
+flight, as in the reference (its tests inspect it); ``poll`` retires finished ones and
+``cancel_stale`` cancels those for layers already passed.
 """
 from __future__ import annotations
 
+import itertools
 import logging
 import time
-import uuid
-from typing import List, Optional
+from typing import Iterable, List, Optional
 
 import torch
 
@@ -20,79 +36,77 @@ from .types import PrefetchPolicy
 
 
 class PrefetchEngine:
-    """Lookahead expert prefetch scheduler (engine/prefetch.py:53)."""
+    """Starts expert copies ahead of the layers that will need them."""
 
     def __init__(self, cache_manager, transfer_scheduler, policy: PrefetchPolicy, depth: int,
                  logger: Optional[logging.Logger] = None) -> None:
         self._cache_manager = cache_manager
         self._transfer_scheduler = transfer_scheduler
-        self.policy: PrefetchPolicy = policy
-        self.depth: int = depth
+        self.policy = policy
+        self.depth = depth
         self._logger = logger or logging.getLogger(__name__)
-        # (layer_id, expert_id) -> request_id of the prefetches in flight.
         self._in_flight: dict[tuple[int, int], str] = {}
+        self._ids = itertools.count()
+        self.counts = {"started": 0, "refused": 0, "cancelled": 0}
 
-    def _is_gpu_resident(self, layer_id: int, expert_id: int) -> bool:
-        return self._cache_manager.is_gpu_resident(layer_id, expert_id)
-
-    def _submit_if_needed(self, layer_id: int, expert_id: int) -> Optional[str]:
-        """Start a CPU->GPU prefetch unless it is in flight or resident (prefetch.py:128-181)."""
+    # ------------------------------------------------------------------ starting copies
+    def _start(self, layer_id: int, expert_id: int) -> Optional[str]:
         key = (layer_id, expert_id)
-        if key in self._in_flight:
+        if key in self._in_flight or self._cache_manager.is_gpu_resident(layer_id, expert_id):
             return None
-        if self._is_gpu_resident(layer_id, expert_id):
-            return None
-        request_id = str(uuid.uuid4())
-        request = TransferRequest(request_id=request_id, layer_id=layer_id, expert_id=expert_id,
-                                  direction=TransferDirection.CPU_TO_GPU,
-                                  priority=TransferPriority.LOW, issued_at=time.monotonic())
-        handle = self._transfer_scheduler.submit_async(request)
+        rid = f"prefetch-{layer_id}-{expert_id}-{next(self._ids)}"
+        handle = self._transfer_scheduler.submit_async(TransferRequest(
+            request_id=rid, layer_id=layer_id, expert_id=expert_id,
+            direction=TransferDirection.CPU_TO_GPU, priority=TransferPriority.LOW,
+            issued_at=time.monotonic()))
         if handle.status != TransferStatus.IN_FLIGHT:
-            self._logger.debug("prefetch not accepted: layer=%d expert=%d status=%s", layer_id,
-                               expert_id, handle.status.value)
+            self.counts["refused"] += 1
             return None
-        self._in_flight[key] = request_id
-        return request_id
+        self._in_flight[key] = rid
+        self.counts["started"] += 1
+        return rid
 
-    def _predict_experts(self, expert_indices: torch.Tensor) -> List[int]:
-        """Sorted distinct expert ids of a routing result (prefetch.py:183-194)."""
-        return sorted(int(x) for x in expert_indices.reshape(-1).unique().tolist())
+    def prefetch(self, layer_id: int, expert_ids: Iterable[int]) -> List[str]:
+        """Start the copies of the given experts of `layer_id` (ascending, each once)."""
+        started = (self._start(layer_id, e) for e in sorted({int(e) for e in expert_ids}))
+        return [rid for rid in started if rid is not None]
+
+    # ------------------------------------------------------------------ policies
+    def _target_layers(self, current_layer: int) -> range:
+        if self.policy == PrefetchPolicy.NEXT_LAYER:
+            return range(current_layer + 1, current_layer + 2)
+        if self.policy == PrefetchPolicy.LOOKAHEAD:
+            return range(current_layer + 1, current_layer + 1 + self.depth)
+        return range(0)                      # NONE, and NEXT_ROUTER (caller-driven)
 
     def schedule_prefetch(self, current_layer: int, expert_indices: torch.Tensor) -> List[str]:
-        """Submit prefetches for the layers after ``current_layer`` (prefetch.py:200-250)."""
-        if self.policy == PrefetchPolicy.NONE:
+        """Prefetch what the policy predicts from the current layer's routing; the request
+        ids of the copies started."""
+        layers = self._target_layers(current_layer)
+        if not layers:
             return []
-        predicted = self._predict_experts(expert_indices)
-        if self.policy == PrefetchPolicy.NEXT_LAYER:
-            targets = [current_layer + 1]
-        else:
-            targets = list(range(current_layer + 1, current_layer + self.depth + 1))
-        submitted: List[str] = []
-        for target in targets:
-            for expert_id in predicted:
-                req_id = self._submit_if_needed(target, expert_id)
-                if req_id is not None:
-                    submitted.append(req_id)
-        return submitted
+        experts = sorted({int(v) for v in expert_indices.reshape(-1).tolist()})
+        return [rid for layer in layers for rid in self.prefetch(layer, experts)]
 
     def on_layer_complete(self, layer_id: int, expert_indices: torch.Tensor) -> None:
-        """Cancel stale prefetches, then schedule the next ones (prefetch.py:252-277)."""
-        self.cancel_stale(current_layer=layer_id + 1)
-        self.schedule_prefetch(current_layer=layer_id, expert_indices=expert_indices)
+        """After layer `layer_id`: cancel what is now stale, then prefetch ahead."""
+        self.cancel_stale(layer_id + 1)
+        self.schedule_prefetch(layer_id, expert_indices)
 
+    # ------------------------------------------------------------------ retiring
     def cancel_stale(self, current_layer: int) -> int:
-        """Cancel in-flight prefetches for layers below ``current_layer`` (prefetch.py:279-309)."""
-        stale = [key for key in self._in_flight if key[0] < current_layer]
-        cancelled = 0
+        """Cancel the prefetches still in flight for layers below `current_layer`; drop
+        their bookkeeping either way.  Returns how many the scheduler cancelled."""
+        stale = [k for k in self._in_flight if k[0] < current_layer]
+        n = 0
         for key in stale:
-            request_id = self._in_flight.pop(key)
-            if self._transfer_scheduler.cancel(request_id):
-                cancelled += 1
-        return cancelled
+            if self._transfer_scheduler.cancel(self._in_flight.pop(key)):
+                n += 1
+        self.counts["cancelled"] += n
+        return n
 
     def poll(self) -> None:
-        """Finish the prefetches whose copies have completed (makes them GPU-resident)."""
+        """Retire the prefetches whose copies have finished."""
         for key in list(self._in_flight):
-            status = self._transfer_scheduler.poll_async(*key)
-            if status in (TransferStatus.READY, TransferStatus.CANCELLED, TransferStatus.REJECTED):
-                self._in_flight.pop(key, None)
+            if self._transfer_scheduler.poll_async(*key) != TransferStatus.IN_FLIGHT:
+                del self._in_flight[key]

@@ -10,11 +10,13 @@ import torch
 
 
 class PrefetchPolicy(enum.Enum):
-    """Expert prefetch strategy (engine/types.py:15-28)."""
+    """Expert prefetch strategy (engine/types.py:15-28), plus NEXT_ROUTER: the next layer's
+    router applied to the current layer's MoE input predicts the next layer's experts."""
 
     NONE = "none"
     NEXT_LAYER = "next_layer"
     LOOKAHEAD = "lookahead"
+    NEXT_ROUTER = "next_router"
 
 
 @dataclasses.dataclass

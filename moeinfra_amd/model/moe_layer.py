@@ -9,8 +9,14 @@ HIP kernels:
   groups, runs the fused NF4 SwiGLU of every routed expert and combines, without any
   host synchronisation;
 * offload: the routing runs on the device, the routed set is read back (the reference's
-  ``unique().tolist()``), missing experts arrive through ``_ensure_expert_on_gpu`` and the
-  transfer scheduler, then grouping / expert FFN / combine run on the device.
+  ``unique().tolist()``), the copies of every missing routed expert are started at once on
+  the transfer stream (``submit_async``; each expert is GPU-resident from then on, ordered
+  behind its copy's event), ``_ensure_expert_on_gpu`` returns them (or runs the synchronous
+  transfer for one that found no slot), and grouping / expert FFN / combine are enqueued
+  behind stream waits on those events -- the host never waits for a copy.  Experts that
+  were not resident before the layer are demoted after it, as in the reference
+  (model/moe_layer.py:200-209), unless the layer was built with ``retain_transferred`` (the
+  engine's offload mode with a per-layer GPU cache keeps them for the next token).
 
 Expert objects that are not NF4 HIP experts (the fakes the reference's tests install by
 monkeypatching ``_ensure_expert_on_gpu``) are called one by one, in the reference's order,
@@ -26,7 +32,7 @@ import torch
 
 from .. import ops
 from ..engine.router import ExpertRouter
-from ..transfer.types import TransferDirection, TransferPriority, TransferRequest, TransferStatus
+from ..transfer.types import TransferDirection, TransferPriority, TransferRequest
 
 
 def _is_hip_expert(expert) -> bool:
@@ -37,7 +43,9 @@ class MoELayer:
     """Single Mixtral MoE layer with expert offloading."""
 
     def __init__(self, layer_id: int, router, cache_manager, model_loader, transfer_scheduler,
-                 logger: Optional[logging.Logger] = None) -> None:
+                 logger: Optional[logging.Logger] = None, *,
+                 retain_transferred: bool = False) -> None:
+        self.retain_transferred = retain_transferred
         self.layer_id = layer_id
         self.router = router
         self.cache_manager = cache_manager
@@ -47,6 +55,8 @@ class MoELayer:
         self._table_key = None
         self._table = None
         self._workspace: Optional[torch.Tensor] = None
+        #: The expert indices [T, k] (device int64) of the last forward on the device path.
+        self.last_expert_indices: Optional[torch.Tensor] = None
 
     # ------------------------------------------------------------------ residency
     def _ensure_expert_on_gpu(self, expert_id: int):
@@ -77,27 +87,27 @@ class MoELayer:
                                "was not resident on GPU after transfer")
         return expert
 
-    def _start_async_transfers(self, unique: list, was_resident: dict) -> None:
-        """Start the copies of every routed expert that is not GPU-resident at once
-        (submit_async: stage into a pinned slot, hipMemcpyAsync on the transfer stream), so
-        that staging one overlaps the copy of the previous; then finish them in order.
-        Experts that get no slot take the synchronous path in _ensure_expert_on_gpu."""
+    def _start_async_transfers(self, unique: list, was_resident: dict) -> dict:
+        """Start the copies of every routed expert that is not GPU-resident, back to back on
+        the transfer stream, without waiting for any (submit_async publishes each expert in
+        the GPU tier behind its copy's event).  Returns {expert id: the arriving expert} --
+        held by the layer, so that an expert the GPU tier evicts again before the layer runs
+        (more routed experts than the tier keeps for a layer) stays usable.  Experts that
+        find no slot are left to the synchronous path of _ensure_expert_on_gpu."""
         sched = self.transfer_scheduler
-        if not hasattr(sched, "submit_async") or not hasattr(sched, "poll_async"):
-            return
-        handles = {}
+        started = {}
+        if not hasattr(sched, "submit_async"):
+            return started
         for e in unique:
             if was_resident[e] or self.cache_manager.peek_cpu(self.layer_id, e) is None:
                 continue
-            request = TransferRequest(
+            h = sched.submit_async(TransferRequest(
                 request_id=f"layer-{self.layer_id}-expert-{e}-{id(self)}-async",
                 layer_id=self.layer_id, expert_id=e, direction=TransferDirection.CPU_TO_GPU,
-                priority=TransferPriority.HIGH, issued_at=time.monotonic())
-            handles[e] = sched.submit_async(request)
-        for e, h in handles.items():
-            if h.status == TransferStatus.IN_FLIGHT:
-                h.event.synchronize()
-                sched.poll_async(self.layer_id, e)
+                priority=TransferPriority.HIGH, issued_at=time.monotonic()))
+            if getattr(h, "gpu_state", None) is not None:
+                started[e] = h.gpu_state
+        return started
 
     # ------------------------------------------------------------------ forward
     @torch.no_grad()
@@ -142,14 +152,18 @@ class MoELayer:
         x = x.contiguous()
         resident = [self.cache_manager.peek_gpu(self.layer_id, e) for e in range(E)]
         if all(r is not None and _is_hip_expert(r) for r in resident):
+            for r in resident:                 # experts still arriving: order after their copies
+                if getattr(r, "ready_event", None) is not None:
+                    r.wait_ready()
             table = self._resident_table(resident)
             inter = resident[0].intermediate_size
             need = ops.lib().moe_layer_workspace_bytes(x.shape[0], k, E, x.shape[1], inter)
             if self._workspace is None or self._workspace.numel() < need or \
                     self._workspace.device != x.device:
                 self._workspace = torch.empty((need,), dtype=torch.uint8, device=x.device)
-            out, _, _, _ = ops.layer_forward(table, E, router.gate_weight.contiguous(), x, k,
-                                             inter, bias=router.bias, workspace=self._workspace)
+            out, _, _, idx = ops.layer_forward(table, E, router.gate_weight.contiguous(), x, k,
+                                               inter, bias=router.bias, workspace=self._workspace)
+            self.last_expert_indices = idx
             return out
         return self._forward_offload(x)
 
@@ -160,13 +174,14 @@ class MoELayer:
         idx32 = torch.empty((T, k), dtype=torch.int32, device=x.device)
         _, w, idx = ops.router_topk(x, router.gate_weight.contiguous(), k, bias=router.bias,
                                     want_logits=False, idx32_out=idx32)
+        self.last_expert_indices = idx
         unique = sorted(int(e) for e in idx.reshape(-1).unique().tolist())   # host sync
         was_resident = {e: self.cache_manager.is_gpu_resident(self.layer_id, e) for e in unique}
         experts = {}
         try:
-            self._start_async_transfers(unique, was_resident)
+            started = self._start_async_transfers(unique, was_resident)
             for e in unique:
-                experts[e] = self._ensure_expert_on_gpu(e)
+                experts[e] = started[e] if e in started else self._ensure_expert_on_gpu(e)
             if not all(_is_hip_expert(ex) for ex in experts.values()):
                 return self._combine_with_callables(x, idx, w, experts)
             first = next(iter(experts.values()))
@@ -176,9 +191,10 @@ class MoELayer:
             _, ypart = ops.expert_ffn(table, E, x, k, x.shape[1], first.intermediate_size, route)
             return ops.combine(ypart, w, idx32, route["slot_pos"])
         finally:
-            for e in unique:
-                if not was_resident[e]:
-                    self.cache_manager.demote_to_cpu(self.layer_id, e)
+            if not self.retain_transferred:
+                for e in unique:
+                    if not was_resident[e]:
+                        self.cache_manager.demote_to_cpu(self.layer_id, e)
             experts.clear()
 
     # ------------------------------------------------------------------ expert callables

@@ -67,14 +67,34 @@ class ReconstructedNF4Expert(nn.Module):
         self.w3 = _reconstruct_linear(gpu_state["w3"], in_features=hidden_size,
                                       out_features=intermediate_size)
         self._struct: Optional[MoeNf4Expert] = None
+        # Completion event of the copy that brings the tensors in (None: already there);
+        # kernels that read them are ordered after it by wait_ready().
+        self.ready_event: Optional[torch.cuda.Event] = None
+        # Whatever keeps the tensors' device memory reserved for this expert (a slot lease
+        # of the transfer scheduler's arena); dropped with the expert.
+        self.device_lease = None
+
+    def wait_ready(self) -> None:
+        """Order the current stream's later work after the expert's arrival (a stream wait,
+        no host synchronisation)."""
+        ev = self.ready_event
+        if ev is None:
+            return
+        if ev.query():
+            self.ready_event = None
+        else:
+            torch.cuda.current_stream(self.device).wait_event(ev)
 
     def c_struct(self) -> MoeNf4Expert:
-        """Device pointers of the three projections (moe_nf4_expert_t)."""
+        """Device pointers of the three projections (moe_nf4_expert_t); the current stream
+        first waits for the expert's arrival."""
+        self.wait_ready()
         if self._struct is None:
             self._struct = expert_struct(self.w1, self.w2, self.w3)
         return self._struct
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
+        self.wait_ready()
         return swiglu_forward(self, x)
 
     @property

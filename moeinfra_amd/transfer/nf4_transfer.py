@@ -1,10 +1,12 @@
-"""Asynchronous host-to-device copy of a staged NF4 expert (mirrors
-transfer/nf4_transfer.py:8-40 of the reference).
+"""Host-to-device copy of a staged NF4 expert: transfer_staged_expert_to_gpu, the API of the
+reference's transfer/nf4_transfer.py:8-40.
 
-Each tensor of the pinned slot is copied with a non-blocking copy (hipMemcpyAsync from
-pinned memory) on the given side stream, so the transfer can overlap expert compute on
-the default stream.  The caller orders the consumer after the copies (stream sync or the
-event of mark_transfer_complete) and keeps the slot until they complete.
+Every tensor of the staging slot is copied with a non-blocking copy (hipMemcpyAsync from
+pinned memory) enqueued on `stream`; the returned device tensors are allocated on that
+stream.  The caller orders consumers after the copies (an event recorded on `stream`) and
+keeps the slot until they have run.  The transfer scheduler itself copies into preallocated
+device slots instead (scheduler.py); this function is the per-tensor form for callers of
+the reference's API.
 """
 from __future__ import annotations
 
@@ -15,10 +17,8 @@ from .reusable_staging import StagingSlot
 
 def transfer_staged_expert_to_gpu(slot: StagingSlot, stream, device="cuda") -> dict:
     if not slot.in_use:
-        raise RuntimeError("Slot must be acquired before transfer")
-    gpu_state: dict = {}
+        raise RuntimeError(f"staging slot {slot.slot_id} must be acquired before its transfer")
     with torch.cuda.stream(stream):
-        for name in ("w1", "w2", "w3"):
-            gpu_state[name] = {key: (None if t is None else t.to(device=device, non_blocking=True))
-                               for key, t in slot.tensors[name].items()}
-    return gpu_state
+        return {name: {key: None if t is None else t.to(device, non_blocking=True)
+                       for key, t in state.items()}
+                for name, state in slot.tensors.items()}

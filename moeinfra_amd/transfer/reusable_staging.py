@@ -1,27 +1,30 @@
-"""Bounded, reusable pinned-memory staging slots for expert H2D transfers (mirrors
-transfer/reusable_staging.py:20-284 of the reference).
+"""Pinned host staging for expert transfers: the ReusablePinnedStagingPool / StagingSlot API
+of the reference's transfer/reusable_staging.py:20-284.
 
-A slot is not handed out again until the event recorded after its last DMA has completed
-(:72-93), so a host buffer is never overwritten while a copy still reads it.  Experts are
-staged in the canonical per-projection representation
-``weight, absmax, code, offset [, state2_absmax, state2_code, state2_offset]`` (:126-222),
-accepting either that form or bitsandbytes' serialized Linear4bit.state_dict() keys; the
-serialized metadata blob is decoded here without bitsandbytes.
+A slot is a pinned host buffer set that one transfer reads from.  Its ``ready_event`` is
+recorded on the transfer stream behind the copies that read it; ``acquire`` hands a slot
+out again only once that event has completed, so a host buffer is never rewritten under a
+DMA.  Slots are created lazily within a PinnedMemoryBudget and never shrink.
+
+Staging an expert fills ``slot.tensors`` with its canonical per-projection tensors
+(expert_image.canonical_projection).  Tensors that already live in pinned memory -- the
+offload store is pinned once, see host_store.py -- are referenced as they are: nothing is
+copied and the DMA reads the store directly.  Pageable tensors are copied into buffers the
+slot owns, which later stagings of the same shapes reuse in place, so the slot's addresses
+stay fixed; the source expert is never modified or pinned.
 """
 from __future__ import annotations
 
-from dataclasses import dataclass
+import dataclasses
 from typing import Optional
 
 import torch
 
-from ..model.expert import parse_blob
+from .expert_image import PROJECTIONS, canonical_projection
 from .pinned_memory import PinnedMemoryBudget
 
-_BLOB = "weight.quant_state.bitsandbytes__nf4"
 
-
-@dataclass
+@dataclasses.dataclass
 class StagingSlot:
     slot_id: int
     size_bytes: int
@@ -29,12 +32,16 @@ class StagingSlot:
     in_use: bool = False
     ready_event: Optional[torch.cuda.Event] = None
     expert_key: Optional[tuple[int, int]] = None
+    # pinned buffers owned by the slot, per (projection, key)
+    owned: dict = dataclasses.field(default_factory=dict)
+    # bytes of the last staging that had to be copied (0 when everything was pinned)
+    copied_bytes: int = 0
 
 
 class ReusablePinnedStagingPool:
-    """Pinned slots reused once the event of their previous transfer has completed."""
+    """Bounded set of reusable pinned staging slots."""
 
-    _PROJECTIONS = ("w1", "w2", "w3")
+    _PROJECTIONS = PROJECTIONS
 
     def __init__(self, budget: PinnedMemoryBudget, slot_size_bytes: int):
         if slot_size_bytes <= 0:
@@ -49,122 +56,81 @@ class ReusablePinnedStagingPool:
 
     @property
     def active_slots(self) -> int:
-        return sum(slot.in_use for slot in self._slots.values())
+        return sum(1 for s in self._slots.values() if s.in_use)
 
-    def _create_slot(self, slot_id: int) -> Optional[StagingSlot]:
-        if not self.budget.reserve(self.slot_size_bytes):
-            return None
-        slot = StagingSlot(slot_id=slot_id, size_bytes=self.slot_size_bytes, tensors={})
-        self._slots[slot_id] = slot
-        return slot
+    @staticmethod
+    def _reusable(slot: StagingSlot) -> bool:
+        if slot.in_use:
+            return False
+        ev = slot.ready_event
+        if ev is not None and not ev.query():
+            return False
+        slot.ready_event = None
+        return True
 
     def acquire(self) -> Optional[StagingSlot]:
-        """A free slot whose last transfer has finished, a new one within budget, or None."""
-        for slot in self._slots.values():
-            if slot.in_use:
-                continue
-            if slot.ready_event is not None:
-                if not slot.ready_event.query():
-                    continue
-                slot.ready_event = None
-            slot.in_use = True
-            return slot
-        slot = self._create_slot(len(self._slots))
-        if slot is not None:
-            slot.in_use = True
+        """An idle slot whose last DMA has finished, else a new slot if the budget allows,
+        else None."""
+        slot = next((s for s in self._slots.values() if self._reusable(s)), None)
+        if slot is None:
+            if not self.budget.reserve(self.slot_size_bytes):
+                return None
+            slot = StagingSlot(slot_id=len(self._slots), size_bytes=self.slot_size_bytes,
+                               tensors={})
+            self._slots[slot.slot_id] = slot
+        slot.in_use = True
         return slot
 
     def mark_transfer_complete(self, slot: StagingSlot, stream) -> None:
-        """Record the event that gates the slot's reuse on `stream` (after its DMA)."""
+        """Gate the slot's reuse on everything issued to `stream` so far (its copies)."""
         if not slot.in_use:
-            raise RuntimeError("Cannot mark an inactive slot")
-        event = torch.cuda.Event()
-        event.record(stream)
-        slot.ready_event = event
+            raise RuntimeError(f"staging slot {slot.slot_id} is not acquired")
+        ev = torch.cuda.Event()
+        ev.record(stream)
+        slot.ready_event = ev
 
     def release(self, slot: StagingSlot) -> None:
         if not slot.in_use:
-            raise RuntimeError("Slot is not in use")
+            raise RuntimeError(f"staging slot {slot.slot_id} is not acquired")
         slot.in_use = False
 
     def destroy(self) -> None:
         self._slots.clear()
         self.budget.used_bytes = 0
 
-    @staticmethod
-    def _tensor_bytes(tensor: Optional[torch.Tensor]) -> int:
-        return 0 if tensor is None else tensor.numel() * tensor.element_size()
-
     @classmethod
     def _projection_state(cls, expert, name: str) -> dict:
-        """One projection in the canonical staging representation."""
-        projection = getattr(expert, name)
-        if isinstance(projection, dict):
-            raw = projection
-        else:
-            raw = getattr(projection, "state", None)
-            if raw is None and hasattr(projection, "serialized"):
-                raw = projection.serialized()
-        if not isinstance(raw, dict):
-            raise TypeError(f"Expert projection {name!r} does not expose serialized NF4 state")
-        if "weight" not in raw:
-            raise ValueError(f"Projection {name!r} is missing 'weight'")
-
-        if "absmax" in raw and ("code" in raw or "quant_map" in raw):
-            canonical = {"weight": raw["weight"], "absmax": raw["absmax"],
-                         "code": raw.get("code", raw.get("quant_map")),
-                         "offset": raw.get("offset")}
-            for key in ("state2_absmax", "state2_code", "state2_offset"):
-                if key in raw:
-                    canonical[key] = raw[key]
-            if canonical["code"] is None:
-                raise ValueError(f"Projection {name!r} is missing NF4 code/quant_map")
-            return canonical
-
-        required = {"weight.absmax", "weight.quant_map", _BLOB}
-        missing = required - raw.keys()
-        if missing:
-            raise ValueError(f"Projection {name!r} is missing serialized NF4 state tensors: "
-                             f"{sorted(missing)}")
-        meta = parse_blob(raw[_BLOB])
-        canonical = {"weight": raw["weight"], "absmax": raw["weight.absmax"],
-                     "code": raw["weight.quant_map"], "offset": None}
-        if "weight.nested_absmax" in raw:
-            canonical["state2_absmax"] = raw["weight.nested_absmax"]
-            canonical["state2_code"] = raw.get("weight.nested_quant_map")
-            off = meta.get("nested_offset")
-            canonical["state2_offset"] = None
-            canonical["offset"] = None if off is None else torch.tensor(off, dtype=torch.float32)
-        return canonical
+        return canonical_projection(expert, name)
 
     @classmethod
     def _expert_staging_size(cls, expert) -> int:
-        return sum(cls._tensor_bytes(t) for name in cls._PROJECTIONS
-                   for t in cls._projection_state(expert, name).values())
+        return sum(t.numel() * t.element_size() for name in PROJECTIONS
+                   for t in canonical_projection(expert, name).values() if t is not None)
+
+    def _pinned_copy(self, slot: StagingSlot, where: tuple, src: torch.Tensor) -> torch.Tensor:
+        buf = slot.owned.get(where)
+        if buf is None or buf.shape != src.shape or buf.dtype != src.dtype:
+            buf = torch.empty(src.shape, dtype=src.dtype, pin_memory=True)
+            slot.owned[where] = buf
+        buf.copy_(src)
+        slot.copied_bytes += buf.numel() * buf.element_size()
+        return buf
 
     def stage_expert(self, slot: StagingSlot, expert, layer_id: int, expert_id: int) -> None:
-        """Copy the expert's NF4 tensors into the slot's pinned buffers (reused in place
-        when shapes match)."""
+        """Point the slot at the expert's device tensors, copying only what is pageable."""
         if not slot.in_use:
-            raise RuntimeError("Slot must be acquired before staging")
-        old = slot.tensors
+            raise RuntimeError(f"staging slot {slot.slot_id} must be acquired before staging")
+        slot.copied_bytes = 0
         staged = {}
-        for name in self._PROJECTIONS:
-            source = self._projection_state(expert, name)
-            prev = old.get(name, {})
-            staged[name] = {key: self._copy_into_pinned(t, prev.get(key))
-                            for key, t in source.items()}
+        for name in PROJECTIONS:
+            state = {}
+            for key, t in canonical_projection(expert, name).items():
+                if t is None:
+                    state[key] = None
+                elif t.device.type == "cpu" and t.is_pinned():
+                    state[key] = t
+                else:
+                    state[key] = self._pinned_copy(slot, (name, key), t)
+            staged[name] = state
         slot.tensors = staged
         slot.expert_key = (layer_id, expert_id)
-
-    @staticmethod
-    def _copy_into_pinned(source: Optional[torch.Tensor],
-                          existing: Optional[torch.Tensor] = None) -> Optional[torch.Tensor]:
-        if source is None:
-            return None
-        if existing is None:
-            existing = torch.empty_like(source, device="cpu", pin_memory=True)
-        if existing.shape != source.shape or existing.dtype != source.dtype:
-            raise ValueError("Existing staging buffer does not match source tensor")
-        existing.copy_(source)
-        return existing

@@ -143,32 +143,87 @@ def test_staged_transfer_reconstructs_the_expert(cuda_device):
     assert not cm.is_gpu_resident(0, 0) and cm.is_gpu_resident(0, 1)
 
 
-def test_async_transfer_then_layer(cuda_device):
+def _pinned(experts, device):
+    """helpers.NF4Expert list -> PinnedNF4Expert list (one pinned arena)."""
+    from moeinfra_amd.transfer.host_store import PinnedExpertStore
+
+    store = PinnedExpertStore()
+    return store, store.add_layer([_prequantized(e) for e in experts])
+
+
+def test_async_transfers_publish_at_once_and_order_the_compute(cuda_device):
+    """submit_async makes each expert GPU-resident immediately, behind its copy's event; a
+    layer launched right away (no host synchronisation) must see the copied weights, which
+    only the stream waits guarantee.  Experts come from the pinned store (one copy each, no
+    staging); cancellation drops an in-flight expert."""
     from moeinfra_amd.cache.manager import CacheManager
     from moeinfra_amd.cache.types import EvictionPolicy
+    from moeinfra_amd.transfer.scheduler import TransferScheduler
     from moeinfra_amd.transfer.types import TransferStatus
 
-    H, F = 256, 512
-    _, experts, _ = build_layer(H, F, 3, 1, seed=6)
-    cm = CacheManager(gpu_slots=4, cpu_slots=4, policy=EvictionPolicy.LRU)
-    for e, ex in enumerate(experts):
-        cm.put(0, e, _prequantized(ex), "cpu")
-    sch, pool = _transfer_rig(cm, 2, cm.get_size_bytes(0, 0))
-    handles = [sch.submit_async(_req(0, e)) for e in range(3)]
-    assert [h.status for h in handles] == [TransferStatus.IN_FLIGHT] * 2 + [TransferStatus.REJECTED]
-    assert sch.submit_async(_req(0, 0)) is handles[0]          # the in-flight handle again
-    torch.cuda.synchronize()
-    assert sch.poll_async(0, 0) == TransferStatus.READY
-    assert sch.poll_async(0, 1) == TransferStatus.READY
-    assert cm.is_gpu_resident(0, 0) and cm.is_gpu_resident(0, 1)
-    assert sch.submit_async(_req(0, 0)).status == TransferStatus.READY
-    assert pool.active_slots == 0
-    torch.cuda.synchronize()                                   # the slots' reuse events
-    h = sch.submit_async(_req(0, 2))                           # a slot is free again
+    H, F, E, T = 1024, 3584, 8, 12
+    gate, experts, x = build_layer(H, F, E, T, seed=61)
+    store, pinned = _pinned(experts, cuda_device)
+    assert all(t.is_pinned() for a in store.arenas for t in (a,))
+    cm = CacheManager(gpu_slots=E, cpu_slots=2 * E, policy=EvictionPolicy.LRU)
+    for e, ex in enumerate(pinned):
+        cm.put(0, e, ex, "cpu")
+    cm.put(1, 0, pinned[0], "cpu")
+    sch = TransferScheduler(cm, 24.0, 2 * E, transfer_stream=torch.cuda.Stream())
+    handles = [sch.submit_async(_req(0, e)) for e in range(E)]
+    # Every copy started (a handle turns READY once its copy has finished).
+    assert all(h.event is not None and h.status in (TransferStatus.IN_FLIGHT, TransferStatus.READY)
+               for h in handles)
+    assert all(cm.is_gpu_resident(0, e) for e in range(E))
+    again = sch.submit_async(_req(0, 0))
+    assert again is handles[0] or again.status == TransferStatus.READY
+    layer = _layer(cm, gate, cuda_device, scheduler=sch)
+    out = layer.forward(x.to(cuda_device))                     # all-resident path, no sync
+    want, (lg, _, _) = oracle_layer(gate, experts, x)
+    assert _layer_err(bits(out), want, lg) < TOL
+    h = sch.submit_async(_req(1, 0))
     assert h.status == TransferStatus.IN_FLIGHT and sch.cancel(h.request_id)
+    assert not cm.is_gpu_resident(1, 0)
     torch.cuda.synchronize()
-    assert sch.poll_async(0, 2) == TransferStatus.CANCELLED and not cm.is_gpu_resident(0, 2)
-    assert pool.active_slots == 0
+    assert sch.poll_async(1, 0) == TransferStatus.CANCELLED
+    assert sch.poll_async(0, 3) == TransferStatus.READY
+    assert sch.poll_async(0, 3) == TransferStatus.REJECTED      # retired
+
+
+def test_device_slots_are_leased_to_live_experts(cuda_device):
+    """With two device slots, a third transferred expert that is still referenced elsewhere
+    gets a buffer of its own; dropped experts give their slots back (fenced), and every
+    expert dequantises bit-exactly whichever memory it landed in."""
+    from moeinfra_amd.cache.manager import CacheManager
+    from moeinfra_amd.cache.types import EvictionPolicy
+    from moeinfra_amd.transfer.device_slots import DeviceExpertSlots
+    from moeinfra_amd.transfer.scheduler import TransferScheduler
+
+    H, F = 256, 512
+    _, experts, _ = build_layer(H, F, 3, 1, seed=62)
+    _store, pinned = _pinned(experts, cuda_device)
+    cm = CacheManager(gpu_slots=2, cpu_slots=3, policy=EvictionPolicy.LRU)
+    for e, ex in enumerate(pinned):
+        cm.put(0, e, ex, "cpu")
+    slots = DeviceExpertSlots(2, pinned[0].image_layout.nbytes, cuda_device)
+    sch = TransferScheduler(cm, 24.0, 4, transfer_stream=torch.cuda.Stream(), device_slots=slots)
+    held = []
+    for e in range(3):
+        assert sch.submit(_req(0, e)) and sch.execute_next().success
+        held.append(cm.peek_gpu(0, e))
+    assert slots.free_count == 0 and not cm.is_gpu_resident(0, 0)   # (0, 0) evicted, still held
+    inside = [slots._mem.data_ptr() <= g.w1.weight.data_ptr() < slots._mem.data_ptr() + slots._mem.numel()
+              for g in held]
+    assert inside == [True, True, False]
+    for e, g in enumerate(held):
+        for n in ("w1", "w2", "w3"):
+            want = orc.nf4_dequant(*experts[e].np[n])
+            np.testing.assert_array_equal(bits(getattr(g, n).dequantize()).reshape(-1), want)
+    sch._async.clear()
+    held.clear()
+    cm.demote_to_cpu(0, 1)
+    cm.demote_to_cpu(0, 2)
+    assert slots.free_count == 2 and all(slots.fence(i) is not None for i in range(2))
 
 
 def _layer(cm, gate, device, layer_id=0, scheduler=None):

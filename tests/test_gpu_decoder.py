@@ -385,18 +385,34 @@ def test_engine_graph_replays_match_eager(cuda_device):
         np.testing.assert_array_equal(lg, outs[0][1])
 
 
-def test_engine_offload_matches_reference(cuda_device):
-    """Offload mode: the NF4 store on the host, 4 GPU expert slots, next-layer prefetch."""
+@pytest.mark.parametrize("policy,slots,per_layer", [
+    ("NONE", 4, None), ("NEXT_LAYER", 4, None), ("NEXT_ROUTER", 4, None),
+    ("NONE", 3, 1), ("NEXT_ROUTER", 6, 3)])
+def test_engine_offload_matches_reference(cuda_device, policy, slots, per_layer):
+    """Offload mode: the NF4 store pinned on the host, a few GPU expert slots (fewer than a
+    40-token prefill routes to per layer), the prefetch policies, and the per-layer GPU tier
+    that keeps transferred experts across tokens."""
     from moeinfra_amd.engine.engine import InferenceEngine
     from moeinfra_amd.engine.types import ForwardRequest, PrefetchPolicy
+    from moeinfra_amd.transfer import scheduler as sched_mod
 
     w = _small_engine_weights(cuda_device)
     prompt = torch.randint(0, w.shape.vocab, (1, 6), generator=torch.Generator().manual_seed(6))
-    for policy in (PrefetchPolicy.NONE, PrefetchPolicy.NEXT_LAYER):
-        eng = InferenceEngine(w, max_seq=64, device=cuda_device, offload=True, gpu_expert_slots=4,
-                              prefetch=policy)
-        res = eng.generate(ForwardRequest(prompt, max_new_tokens=5))
-        _check_against_reference(res, w, prompt)
+    eng = InferenceEngine(w, max_seq=64, device=cuda_device, offload=True, gpu_expert_slots=slots,
+                          prefetch=PrefetchPolicy[policy], gpu_slots_per_layer=per_layer)
+    n_prof = len(sched_mod.EXECUTE_NEXT_PROFILE)
+    res = eng.generate(ForwardRequest(prompt, max_new_tokens=5))
+    _check_against_reference(res, w, prompt)
+    assert eng.pinned_store.pinned_bytes > 0
+    assert all(p.get("source", "image") == "image"                 # never staged
+               for p in sched_mod.EXECUTE_NEXT_PROFILE[n_prof:])
+    used = eng.cache_manager.stats().gpu_slots_used
+    if per_layer is not None:                # transferred experts are kept, per layer
+        assert 0 < used <= per_layer * w.shape.layers
+        assert all(sum(1 for k in eng.cache_manager._gpu_cache if k[0] == l) <= per_layer
+                   for l in range(w.shape.layers))
+    elif policy == "NONE":                   # the reference's contract: demoted after use
+        assert used == 0
 
 
 def test_engine_full_mixtral_layer_matches_reference(cuda_device):

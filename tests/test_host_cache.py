@@ -100,9 +100,9 @@ def test_arc_ghost_hit_adapts_target():
     c.put(0, 1, Fake(), "cpu")
     c.put(0, 2, Fake(), "cpu")                 # evicts 0 into the T1 ghost list
     assert c.peek_cpu(0, 0) is None
-    p0 = c._arc_cpu.p
+    p0 = c._rank[False].p
     c.put(0, 0, Fake(), "cpu")                 # ghost hit grows T1's target
-    assert c._arc_cpu.p > p0
+    assert c._rank[False].p > p0
     assert c.stats().cpu_slots_used == 2
 
 
@@ -155,3 +155,81 @@ def test_residency_epoch_changes_only_with_gpu_tier():
     assert e2 > e1
     c.demote_to_cpu(0, 1)
     assert c.residency_epoch > e2
+
+
+def _decode_trace(layers, experts, tokens, seed=0, k=2):
+    """(layer, expert) GPU-tier accesses of layer-by-layer decoding with random top-k
+    routing: every token visits layers 0..L-1 in order."""
+    import random
+
+    rng = random.Random(seed)
+    return [(l, e) for _ in range(tokens) for l in range(layers)
+            for e in sorted(rng.sample(range(experts), k))]
+
+
+def _hits(c, trace):
+    hits = 0
+    for key in trace:
+        if c.is_gpu_resident(*key):
+            hits += 1
+            c.get(*key)
+        else:
+            c.put(*key, Fake(device="cuda"), "cuda")
+    return hits
+
+
+def test_global_lru_never_hits_a_cyclic_decode_while_a_per_layer_tier_does():
+    """Layer-by-layer decoding visits (layer, expert) keys cyclically.  A global LRU tier
+    with fewer slots (12) than one token's keys (8 layers x 2 routed) has flushed every key
+    before its layer comes round again: no hit at all.  One slot per layer (8 of the 12
+    used) keeps each layer's last expert, which the next token's first routed expert
+    sometimes is."""
+    trace = _decode_trace(layers=8, experts=8, tokens=400)
+    glob = CacheManager(gpu_slots=12, cpu_slots=64, policy=EvictionPolicy.LRU)
+    part = CacheManager(gpu_slots=12, cpu_slots=64, policy=EvictionPolicy.LRU,
+                        gpu_slots_per_layer=1)
+    assert _hits(glob, trace) == 0
+    rate = _hits(part, trace) / len(trace)
+    assert rate > 0.02, rate
+    assert part.stats().gpu_slots_used == 8
+    assert all(sum(1 for k in part._gpu_cache if k[0] == l) == 1 for l in range(8))
+
+
+def test_per_layer_partition_evicts_within_the_layer():
+    c = CacheManager(gpu_slots=6, cpu_slots=8, policy=EvictionPolicy.LRU, gpu_slots_per_layer=2)
+    for key in ((0, 0), (1, 0), (0, 1), (1, 1)):
+        c.put(*key, Fake(device="cuda"), "cuda")
+    c.get(0, 0)
+    c.put(0, 2, Fake(device="cuda"), "cuda")   # layer 0 is full: its LRU entry (0, 1) goes
+    assert set(c._gpu_cache) == {(0, 0), (0, 2), (1, 0), (1, 1)}
+    with pytest.raises(ValueError):
+        CacheManager(gpu_slots=1, cpu_slots=1, policy=EvictionPolicy.LRU, gpu_slots_per_layer=0)
+
+
+@pytest.mark.parametrize("policy", list(EvictionPolicy))
+def test_make_room_evicts_ahead_of_the_put(policy):
+    c = CacheManager(gpu_slots=2, cpu_slots=4, policy=policy)
+    c.put(0, 0, Fake(device="cuda"), "cuda")
+    c.put(0, 1, Fake(device="cuda"), "cuda")
+    c.make_room_gpu(0, 1)                      # already resident: nothing to do
+    assert c.stats().evictions == 0
+    c.make_room_gpu(0, 2)
+    assert c.stats().gpu_slots_used == 1 and c.stats().evictions == 1
+    c.put(0, 2, Fake(device="cuda"), "cuda")   # fits without another eviction
+    assert c.stats().evictions == 1 and c.is_gpu_resident(0, 2)
+
+
+def test_arc_matches_the_paper_on_a_small_trace():
+    """ARC with capacity 2: a key seen twice moves to T2; a miss on a T1 ghost raises p and
+    re-enters in T2; with T1 under its target the victim comes from T2."""
+    c = cm(EvictionPolicy.ARC, cpu=2)
+    arc = c._rank[False]
+    c.put(0, 0, Fake(), "cpu")
+    c.get(0, 0)                                # (0,0) -> T2
+    c.put(0, 1, Fake(), "cpu")                 # T1 = [(0,1)], T2 = [(0,0)]
+    assert list(arc.t1) == [(0, 1)] and list(arc.t2) == [(0, 0)]
+    c.put(0, 2, Fake(), "cpu")                 # |T1| = 1 > p = 0: T1's LRU (0,1) -> B1
+    assert list(arc.b1) == [(0, 1)] and c.peek_cpu(0, 0) is not None
+    c.put(0, 1, Fake(), "cpu")                 # B1 ghost hit: p -> 1, victim from T2? |T1|=1==p
+    assert arc.p == 1 and (0, 1) in arc.t2
+    assert c.stats().cpu_slots_used == 2

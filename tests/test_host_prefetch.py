@@ -112,4 +112,4 @@ def test_request_and_result_types():
     res = ForwardResult(logits=torch.zeros(1), token_ids=[1, 2], ttft_ms=1.0, tps=2.0,
                         stage_timings={"prefill": 1.0})
     assert res.token_ids == [1, 2]
-    assert [p.value for p in PrefetchPolicy] == ["none", "next_layer", "lookahead"]
+    assert [p.value for p in PrefetchPolicy] == ["none", "next_layer", "lookahead", "next_router"]

@@ -51,8 +51,11 @@ class FakeCM:
     def is_gpu_resident(self, layer, expert):
         return (layer, expert) in self.gpu
 
-    def peek_cpu(self, layer, expert):
+    def peek_gpu(self, layer, expert):
         return None
+
+    def peek_cpu(self, layer, expert):
+        return self.cpu_objs.get((layer, expert)) if hasattr(self, "cpu_objs") else None
 
 
 # --------------------------------------------------------------------------- budget
@@ -240,9 +243,14 @@ def test_failures_are_reported_in_the_result():
     s.submit(req(1, 1, TransferDirection.GPU_TO_CPU))       # present but not GPU-resident
     r = s.execute_next()
     assert not r.success and "Transfer failed" in r.error
-    s.submit(req(1, 1, TransferDirection.CPU_TO_GPU))       # no staging pool / stream
+    s.submit(req(1, 1, TransferDirection.CPU_TO_GPU))       # sized, but no CPU copy
     r = s.execute_next()
-    assert not r.success and "staging_pool" in r.error
+    assert not r.success and "CPU expert not found" in r.error
+    cm.cpu_objs = {(1, 2): object()}
+    cm.cpu[(1, 2)] = 99
+    s.submit(req(1, 2, TransferDirection.CPU_TO_GPU))       # a CPU copy, but no stream
+    r = s.execute_next()
+    assert not r.success and "transfer_stream" in r.error
     assert EXECUTE_NEXT_PROFILE[-1]["success"] is False
     assert s.pending_count() == 0
 
@@ -253,6 +261,8 @@ def test_submit_async_rejections_without_gpu():
         s.submit_async(req(0, 0, TransferDirection.GPU_TO_CPU))
     cm.gpu[(0, 0)] = 1
     assert s.submit_async(req(0, 0)).status.value == "ready"
-    with pytest.raises(RuntimeError, match="staging_pool"):
+    assert s.submit_async(req(0, 1)).status.value == "rejected"   # no CPU copy to send
+    cm.cpu_objs = {(0, 1): object()}
+    with pytest.raises(RuntimeError, match="transfer_stream"):
         s.submit_async(req(0, 1))
     assert s.poll_async(0, 1).value == "rejected"
