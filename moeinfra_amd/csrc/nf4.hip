@@ -1,5 +1,8 @@
 // K0 (NF4 blockwise quantise) and K1 (standalone NF4 -> bf16 dequant) for gfx950.
 //
+// K0 moves 2 B in and 0.5625 B out per value; with blocksize 64 (the expert path) eight
+// lanes share a block and every wave reads and writes contiguous runs.
+//
 // K1 is HBM-bound: 0.5 B read + 2 B written per value (plus 4 B of absmax per 64
 // values).  Each thread owns 32 consecutive values: one 16-byte load of packed nibbles,
 // one absmax, four 16-byte stores of bf16.  The 16-entry codebook sits in LDS; 16
@@ -60,7 +63,58 @@ nf4_dequant_kernel(const uint8_t *__restrict__ packed, const float *__restrict__
 
 constexpr int kQuantThreads = 256;
 
-// One thread per quantisation block.  Not on the timed path (fixture creation).
+// Blocksize-64 quantisation, eight lanes per block: lane l of a wave loads the 8 bf16 values
+// at 8*l of the wave's 512-value chunk (one contiguous 1 KB load per wave), the block's
+// absmax is the max over its 8 lanes (xor shuffles), and each lane packs its 8 values into
+// 4 bytes (one contiguous 256-byte store per wave).  Same arithmetic as the per-block kernel
+// below: q = number of codebook midpoints strictly below w * (1 / absmax), in fp32.
+constexpr int kQuant64Chunk = 512;
+
+__global__ void __launch_bounds__(kQuantThreads)
+nf4_quantize64_kernel(const uint16_t *__restrict__ w, int64_t nchunk,
+                      const float *__restrict__ code, uint8_t *__restrict__ packed,
+                      float *__restrict__ absmax) {
+  __shared__ float s_mid[16];
+  if (threadIdx.x < 15) s_mid[threadIdx.x] = (code[threadIdx.x] + code[threadIdx.x + 1]) * 0.5f;
+  __syncthreads();
+  float mid[15];
+#pragma unroll
+  for (int m = 0; m < 15; ++m) mid[m] = s_mid[m];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t waves = (int64_t)gridDim.x * (kQuantThreads / kWave);
+  for (int64_t c = (int64_t)blockIdx.x * (kQuantThreads / kWave) + (threadIdx.x >> 6); c < nchunk;
+       c += waves) {
+    const int64_t v0 = c * kQuant64Chunk + 8 * lane;
+    const u32x4 raw = *reinterpret_cast<const u32x4 *>(w + v0);
+    float x[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t word = raw[i];
+      x[2 * i] = bf16lo_to_f32(word);
+      x[2 * i + 1] = bf16hi_to_f32(word);
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(x[i]));
+#pragma unroll
+    for (int off = 1; off < 8; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off, kWave));
+    if ((lane & 7) == 0) absmax[v0 / 64] = amax;
+    const float r = amax > 0.0f ? 1.0f / amax : 0.0f;
+    uint32_t out = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float y = x[i] * r;
+      uint32_t q = 0;
+#pragma unroll
+      for (int m = 0; m < 15; ++m) q += y > mid[m] ? 1u : 0u;
+      // value 2j in the high nibble of byte j
+      out |= q << (8 * (i >> 1) + ((i & 1) ? 0 : 4));
+    }
+    *reinterpret_cast<uint32_t *>(packed + v0 / 2) = out;
+  }
+}
+
+// One thread per quantisation block: any blocksize, partial last block.
 __global__ void __launch_bounds__(kQuantThreads)
 nf4_quantize_kernel(const uint16_t *__restrict__ w, int64_t numel, int32_t blocksize,
                     const float *__restrict__ code, uint8_t *__restrict__ packed,
@@ -161,6 +215,18 @@ extern "C" int moe_nf4_quantize_bf16(const void *w_bf16, int64_t numel, int32_t 
               "blocksize must be even and in [2, 4096] (got %d)", blocksize);
   if (numel == 0) return MOE_STATUS_OK;
   MOE_REQUIRE(w_bf16 && code16 && packed_out && absmax_out, "null device pointer");
+  if (blocksize == 64 && numel % moe::kQuant64Chunk == 0 && ((uintptr_t)w_bf16 % 16) == 0 &&
+      ((uintptr_t)packed_out % 4) == 0 && ((uintptr_t)absmax_out % 4) == 0) {
+    const int64_t nchunk = numel / moe::kQuant64Chunk;
+    int64_t blocks = (nchunk + (moe::kQuantThreads / moe::kWave) - 1) / (moe::kQuantThreads / moe::kWave);
+    const int64_t cap = (int64_t)moe::device_cu_count() * 8;
+    blocks = blocks > cap ? cap : blocks;
+    hipLaunchKernelGGL(moe::nf4_quantize64_kernel, dim3((unsigned)blocks), dim3(moe::kQuantThreads),
+                       0, (hipStream_t)stream, (const uint16_t *)w_bf16, nchunk,
+                       (const float *)code16, (uint8_t *)packed_out, (float *)absmax_out);
+    MOE_LAUNCH_CHECK();
+    return MOE_STATUS_OK;
+  }
   const int64_t nblocks = (numel + blocksize - 1) / blocksize;
   const int64_t grid = (nblocks + moe::kQuantThreads - 1) / moe::kQuantThreads;
   MOE_REQUIRE(grid <= 0x7fffffff, "numel too large");

@@ -45,13 +45,22 @@ def test_dequant_full_expert_projection(cuda_device):
 
 
 # ------------------------------------------------------------------------------ K0
-@pytest.mark.parametrize("shape", [(64, 64), (256, 1024), (3, 130)])
+@pytest.mark.parametrize("shape", [(64, 64), (256, 1024), (3, 130), (14336, 4096)])
 def test_quantize_bitexact(cuda_device, shape):
+    """Blocksize 64 over whole 512-value chunks takes the eight-lanes-per-block kernel, other
+    sizes the per-block one; both bit-exact, including an all-zero block, signed zeros and
+    a block whose maximum is negative."""
     from moeinfra_amd import ops, synth
 
     gen = synth.make_generator(11)
     w = synth._normal(shape, gen, "cpu", 0.02)
-    w.view(-1)[5] = 0.0
+    flat = w.view(-1)
+    flat[5] = 0.0
+    if flat.numel() >= 256:
+        flat[64:128] = 0.0                       # absmax 0: every value maps to code 7
+        flat[130] = -0.0
+        flat[192:256] = -flat[192:256].abs()
+        flat[200] = -0.5                         # a negative maximum magnitude
     p_want, a_want = orc.nf4_quantize(bits(w).reshape(-1))
     p_got, a_got, _ = ops.nf4_quantize(w.to(cuda_device))
     np.testing.assert_array_equal(p_got.cpu().numpy().reshape(-1), p_want)
