@@ -9,7 +9,7 @@
 
 namespace moe {
 
-int choose_nsplit(int64_t T, int32_t k, int32_t E, int32_t H);
+int choose_nsplit(int64_t T, int32_t k, int32_t E, int32_t H, int32_t F);
 int launch_expert_ffn(const moe_nf4_expert_t *experts, int32_t E, const void *x, int64_t T,
                       int32_t k, int32_t H, int32_t F, const int32_t *counts,
                       const int32_t *offsets, const int32_t *perm_tok, const int32_t *active,
@@ -64,7 +64,7 @@ struct LayerWs {
 LayerWs layer_ws(int64_t T, int32_t k, int32_t E, int32_t H, int32_t F) {
   LayerWs w{};
   const int64_t rows = T * k;
-  w.nsplit = choose_nsplit(T, k, E, H);
+  w.nsplit = choose_nsplit(T, k, E, H, F);
   int64_t o = 0;
   w.idx32 = o;    o = align_up(o + rows * 4);
   w.counts = o;   o = align_up(o + (int64_t)E * 4);
@@ -87,7 +87,7 @@ struct ExpertWs {
 
 ExpertWs expert_ws(int64_t T, int32_t H, int32_t F) {
   ExpertWs w{};
-  w.nsplit = choose_nsplit(T, 1, 1, H);
+  w.nsplit = choose_nsplit(T, 1, 1, H, F);
   int64_t o = 0;
   w.counts = o;   o = align_up(o + 4);
   w.offsets = o;  o = align_up(o + 8);

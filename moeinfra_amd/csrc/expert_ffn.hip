@@ -428,13 +428,6 @@ int token_tiles_for(int64_t max_tokens_per_expert) { return max_tokens_per_exper
 // Default number of cross-workgroup K splits of the down projection.  Inside a workgroup
 // four waves already split each w2 tile's K range, which fills the chip at batch 1, so a
 // single split (no partial sums to add in the combine) is the default.
-int choose_nsplit(int64_t T, int32_t k, int32_t E, int32_t H) {
-  (void)T;
-  (void)k;
-  (void)E;
-  (void)H;
-  return 1;
-}
 
 bool gemv4_supported(int64_t max_tokens_per_expert, int32_t H, int32_t F);
 bool expert_gemm_supported(int32_t H, int32_t F);
@@ -450,6 +443,25 @@ bool skinny_supported(int32_t H, int32_t F);
 int launch_skinny(const void *tab, const void *x, int64_t T, int64_t rows_total, int32_t H,
                   int32_t F, const void *route, void *h_ws, void *ypart, int phases,
                   hipStream_t stream);
+bool midbatch_supported(int32_t H, int32_t F, int32_t nsplit);
+bool midbatch_rows_ok(int64_t T, int64_t rows_total, int32_t H, int32_t F);
+int midbatch_splits(int64_t active_max, int32_t H, int32_t F);
+int launch_midbatch(const void *tab, const void *x, int64_t T, int64_t rows_total, int32_t H,
+                    int32_t F, const void *route, void *h_ws, void *ypart, int32_t nsplit,
+                    int phases, hipStream_t stream);
+
+// ypart planes a layer's down projection writes (the combine adds them): the streamed
+// mid-batch kernels split K of the down projection over workgroups when few experts would
+// leave CUs idle; every other path writes one plane.  Follows the path choice of
+// launch_expert_ffn for a layer (T tokens, k slots, E experts).
+int choose_nsplit(int64_t T, int32_t k, int32_t E, int32_t H, int32_t F) {
+  const int64_t rows = T * k;
+  const int64_t active_max = rows < E ? rows : E;
+  if (T <= 0 || gemv4_supported(T, H, F)) return 1;
+  if (rows >= kGemmMinRowsPerExpert * active_max && expert_gemm_supported(H, F)) return 1;
+  if (!midbatch_supported(H, F, 1) || !midbatch_rows_ok(T, rows, H, F)) return 1;
+  return midbatch_splits(active_max, H, F);
+}
 
 // phases: bit 0 = gate/up (x -> h), bit 1 = down (h -> ypart).  Up to 4 tokens per expert
 // use the 4x4x4 MFMA GEMV (expert_gemv4.hip); more use the 16x16x32 tiles below.
@@ -496,7 +508,11 @@ int launch_expert_ffn(const moe_nf4_expert_t *experts, int32_t E, const void *x,
       expert_gemm_supported(H, F))
     return launch_expert_gemm(&tab, x, H, F, &rt, h_ws, ypart, phases, stream);
   // Fewer: the mid-batch kernels stream each weight tile once per 32 tokens of its expert
-  // at the HBM rate (32x32x16 MFMA, 16-byte weight loads, activations from L2).
+  // (32x32x16 MFMA, 16-byte weight loads): the streamed form (whole-K waves, activations
+  // through LDS, `nsplit` K splits of the down projection) where the shape allows, else the
+  // K-split form with activations from L2.
+  if (fused == nullptr && midbatch_supported(H, F, nsplit) && midbatch_rows_ok(T, rows_total, H, F))
+    return launch_midbatch(&tab, x, T, rows_total, H, F, &rt, h_ws, ypart, nsplit, phases, stream);
   if (nsplit == 1 && fused == nullptr && skinny_supported(H, F) && rows_total <= 2048 &&
       T * (int64_t)H * 2 < ((int64_t)1 << 31) && rows_total * (int64_t)F * 2 < ((int64_t)1 << 31))
     return launch_skinny(&tab, x, T, rows_total, H, F, &rt, h_ws, ypart, phases, stream);

@@ -307,9 +307,11 @@ def test_layer_absent_expert(cuda_device, T):
 
 # ------------------------------------------------------------------------------ mid-size batches
 # Between the decode form (T <= 4) and the batched GEMM (>= 32 routed rows per expert on
-# average) the layer runs the mid-batch kernels (expert_skinny.hip): 32-token chunks per
-# expert (a hot expert under skewed routing takes several), uniform and skewed routing,
-# shapes whose K does not split evenly over the eight waves (F = 768: 12 blocks).
+# average) the layer runs the mid-batch kernels: the streamed form (expert_midbatch.hip;
+# H and F multiples of 512, K splits of the down projection when few experts are active)
+# or, for other shapes, the K-split form (expert_skinny.hip; F = 768 here).  32-token
+# chunks per expert (a hot expert under skewed routing takes several), uniform and skewed
+# routing.
 @pytest.mark.parametrize("H,F,E,T,seed,skew", [
     (512, 1024, 8, 6, 51, False),
     (512, 768, 8, 9, 52, True),
@@ -323,6 +325,29 @@ def test_layer_mid_batch(cuda_device, H, F, E, T, seed, skew):
     np.testing.assert_array_equal(i_got[~tie], i_want[~tie])
     ok = ~tie
     err = orc.rel_l2(orc.bf16_to_f32(got[ok]), orc.bf16_to_f32(want[ok]))
+    assert err <= 1e-2, err
+
+
+# One expert takes every token (a +1e4 selection bias): 120 rows, four 32-token chunks of
+# the streamed kernels, with the down projection split over K (H = 1024, F = 2048).
+def test_layer_mid_batch_hot_expert(cuda_device):
+    from moeinfra_amd import ops
+
+    H, F, E, T, hot = 1024, 2048, 8, 120, 5
+    gate, experts, x = build_layer(H, F, E, T, 56)
+    bias = torch.zeros(E, dtype=torch.float32)
+    bias[hot] = 1.0e4
+    want, (lg_w, w_w, i_w) = oracle_layer(gate, experts, x, bias=bias)
+    assert (i_w == hot).any(axis=1).all()
+    for ex in experts:
+        ex.to(cuda_device)
+    table = ops.expert_table([ex.c_struct() for ex in experts])
+    out, _, w, idx = ops.layer_forward(table, E, gate.to(cuda_device), x.to(cuda_device), 2, F,
+                                       bias=bias.to(cuda_device))
+    torch.cuda.synchronize()
+    ok = ~near_tie_rows(lg_w, bias=bias.numpy())
+    np.testing.assert_array_equal(idx.cpu().numpy()[ok], i_w[ok])
+    err = orc.rel_l2(orc.bf16_to_f32(bits(out)[ok]), orc.bf16_to_f32(want[ok]))
     assert err <= 1e-2, err
 
 
