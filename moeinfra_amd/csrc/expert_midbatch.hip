@@ -300,11 +300,13 @@ midbatch_kernel(const ExpertTable tab, const uint16_t *__restrict__ act, uint32_
   f32x4 abs_cur[2], abs_nxt[2];
   auto load_fill = [&](const MbPtr<NP> &Q, int c) {
     const uint32_t adv = (uint32_t)c * (kMbChunk * 128u);
+    // All lanes of a wave share row wave + 8j of piece set j, so a row past the chunk is a
+    // wave-uniform skip: no load is issued for it (its LDS row keeps stale values, which
+    // only reach MFMA rows that are never written out).
 #pragma unroll
-    for (int j = 0; j < kMbFill; ++j) {
-      const uint32_t o = Q.fo[j] == kMbOob ? kMbOob : Q.fo[j] + adv;
-      fbuf[j] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, (int)o, 0, 0);
-    }
+    for (int j = 0; j < kMbFill; ++j)
+      if (__builtin_amdgcn_readfirstlane((int)(Q.fo[j] != kMbOob)))
+        fbuf[j] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, (int)(Q.fo[j] + adv), 0, 0);
 #pragma unroll
     for (int h = 0; h < 2; ++h)
       abs_nxt[h] = *reinterpret_cast<const MB_GLOBAL f32x4 *>(Q.ab + (c * kMbChunk + 4 * h));
