@@ -19,7 +19,8 @@ layer per step (layer s mod 32 at step s), so its average covers every layer.
 numpy fp32 SwiGLU) on a bounded sample of layers of one decode token, scaled to the model.
 
 ``--mode decode`` keeps the MoE-layer pass alone at any batch (``--tokens``, ``--routing``)
-as the headline; ``--mode reconstruct`` times one expert's NF4 -> bf16 reconstruction.
+as the headline; ``--mode reconstruct`` times one expert's NF4 -> bf16 reconstruction;
+``--mode prefill`` times the prompt prefill alone (time to first token).
 Weights are synthetic bf16 N(0, 0.02) drawn on the GPU from a seed, experts NF4-quantised
 by the library's quantiser.  Prints ONE JSON line (two for reconstruct).
 """
@@ -55,6 +56,8 @@ def parse_args():
                    help="offload mode: partition the GPU expert tier by layer and keep the "
                         "experts each layer transferred (default: the reference's contract, "
                         "transferred experts are demoted after their layer)")
+    p.add_argument("--cache-policy", choices=["lru", "lfu", "arc"], default="lru",
+                   help="offload mode's GPU-tier eviction policy (the reference's default: lru)")
     p.add_argument("--prefetch-depth", type=int, default=2)
     p.add_argument("--tokens", type=int, default=1, help="tokens per decode step (decode mode)")
     p.add_argument("--routing", choices=["uniform", "zipf"], default="uniform")
@@ -67,11 +70,13 @@ def parse_args():
                         "scales the FETCH_SIZE / WRITE_SIZE counters) and exit")
     p.add_argument("--no-kernel-events", action="store_true",
                    help="do not bracket kernels with HIP events (headline timing only)")
-    p.add_argument("--mode", choices=["e2e", "decode", "reconstruct"], default="e2e",
+    p.add_argument("--mode", choices=["e2e", "decode", "reconstruct", "prefill"], default="e2e",
                    help="e2e (default): the end-to-end model's decode plus the MoE-layer pass; "
                         "decode: the MoE-layer pass alone at --tokens per step; reconstruct: one "
                         "Mixtral expert's NF4 -> bf16 reconstruction from HBM (K1) and from a "
-                        "pinned host staging slot (H2D + K1), one JSON line each")
+                        "pinned host staging slot (H2D + K1), one JSON line each; prefill: the "
+                        "end-to-end model's prompt prefill alone (time to first token), --steps "
+                        "timed prompts of --prompt tokens")
     return p.parse_args()
 
 
@@ -84,6 +89,19 @@ def decode_form(t: int, k: int, e: int, h: int, f: int) -> bool:
     """Whether the layer call runs as the two-launch decode form (routing fused into the
     gate/up kernel, combine into the down kernel)."""
     return t <= 4 and t * k <= 8 and e <= 16 and h % 512 == 0 and f % 512 == 0
+
+
+def gemm_form(t: int, k: int, e: int, h: int, f: int) -> bool:
+    """Whether the layer call runs the LDS-staged batched GEMM (32 or more rows per routed
+    expert on average)."""
+    return not decode_form(t, k, e, h, f) and t * k >= 32 * min(t * k, e)
+
+
+def midbatch_form(t: int, k: int, e: int, h: int, f: int) -> bool:
+    """Whether the layer call runs the streamed mid-batch kernels (more than 4 and fewer
+    than 32 rows per routed expert, shapes with whole 512-wide tiles)."""
+    return (not decode_form(t, k, e, h, f) and not gemm_form(t, k, e, h, f) and t > 4
+            and h % 512 == 0 and f % 512 == 0 and (f // 64) % 8 == 0 and t * k <= 2048)
 
 
 def gateup_bytes(u: int, h: int, f: int, t: int, k: int, e: int) -> int:
@@ -133,11 +151,46 @@ def main() -> int:
         return _reconstruct(args)
     if args.mode == "e2e":
         return _e2e(args)
+    if args.mode == "prefill":
+        return _prefill(args)
     return _decode_layers(args)
 
 
+def _prefill(args) -> int:
+    """``--mode prefill``: the prompt prefill of the all-resident 32-layer model alone (the
+    reference's ttft, engine/engine.py:478-484): W untimed prompts, then ``--steps`` timed
+    ones, each the whole prefill through the last token's logits."""
+    import torch
+
+    from moeinfra_amd.engine.decoder import MixtralShape, synthesize
+    from moeinfra_amd.engine.engine import InferenceEngine
+    from moeinfra_amd.engine.types import ForwardRequest
+
+    s = MixtralShape(layers=args.layers)
+    P, K, W = args.prompt, max(args.steps, 1), args.warmup
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    w = synthesize(s, seed=args.seed, device=dev)
+    eng = InferenceEngine(w, max_seq=P + 8, device=dev)
+    prompt = torch.randint(0, s.vocab, (1, P), generator=torch.Generator().manual_seed(args.seed))
+    for _ in range(W):
+        eng.generate(ForwardRequest(prompt, max_new_tokens=1))
+    torch.cuda.synchronize()
+    ttft = [eng.generate(ForwardRequest(prompt, max_new_tokens=1)).ttft_ms for _ in range(K)]
+    ms = sorted(ttft)[len(ttft) // 2]
+    print(json.dumps({
+        "metric": "time to first token, Mixtral-8x7B-shape NF4, all-resident", "value": round(ms, 3),
+        "unit": "ms", "n_gpus": 1, "steps": K, "warmup": W, "higher_is_better": False,
+        "dtype": "bf16", "data": "synthetic (seeded weights, random prompt ids)",
+        "config": {"workload": f"{P}-token random-id prompt through the {s.layers}-layer "
+                               "Mixtral-8x7B-shaped model (prefill to the last token's logits)",
+                   "prompt_tokens": P, "layers": s.layers},
+        "ttft_ms_all": [round(t, 3) for t in ttft]}), flush=True)
+    return 0
+
+
 # ---------------------------------------------------------------------------- MoE-layer pass
-def _moe_pass(lib, layers, xs, bias, T, H, F, E, K, steps, warmup, events=True):
+def _moe_pass(lib, layers, xs, bias, T, H, F, E, K, steps, warmup, events=True, routing="uniform"):
     """Times ``steps`` passes over the MoE layers (one call of the whole-layer entry point
     each), with one layer per step through the profiled entry when ``events`` is set.
     ``layers``: [{"gate": [E, H] bf16, "table": expert table}]; ``xs``: per-layer [T, H]."""
@@ -203,18 +256,23 @@ def _moe_pass(lib, layers, xs, bias, T, H, F, E, K, steps, warmup, events=True):
     layer_us = ms_per_step * 1e3 / L
     layer_gbps = ly_bytes / (layer_us * 1e-6) / 1e9
 
+    streamed = midbatch_form(T, K, E, H, F)
     if decode_form(T, K, E, H, F):
         gu_kernel = "decode_gateup_kernel (routing + NF4 w1/w3 GEMV + SwiGLU)"
-    elif T * K >= 32 * min(T * K, E):  # the library's choice of the batched GEMM
+    elif gemm_form(T, K, E, H, F):
         gu_kernel = "expert_gemm_kernel<gate/up> (LDS-staged NF4 GEMM + SwiGLU)"
+    elif streamed:
+        gu_kernel = "midbatch_kernel<2> (streamed NF4 w1/w3 + SwiGLU, 32x32x16 MFMA)"
     else:
         gu_kernel = "skinny_kernel / gemv4_kernel (NF4 w1/w3 + SwiGLU)"
     roofline = None
-    if gu_us and decode_form(T, K, E, H, F):
+    if gu_us and (decode_form(T, K, E, H, F) or streamed):
+        # Weight streaming: the routed experts' w1/w3 NF4 bytes per launch on the HBM roofline.
         ach = gu_bytes / (gu_us * 1e-6) / 1e9
         roofline = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBPS,
                     "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBPS, 4),
-                    "traffic": _traffic("gateup_nf4_decode_t%d" % T), "kernel": gu_kernel,
+                    "traffic": _traffic("gateup_nf4_midbatch_t%d_%s" % (T, routing) if streamed
+                                        else "gateup_nf4_decode_t%d" % T), "kernel": gu_kernel,
                     "bytes_per_launch": int(gu_bytes), "avg_launch_us": round(gu_us, 2)}
     elif gu_us:
         # Batches (prefill): the w1/w3 GEMMs, 2 x 2 * (T*k) * H * F flops per launch, on the
@@ -266,7 +324,7 @@ def _decode_layers(args) -> int:
     setup_s = time.time() - t_setup
 
     r = _moe_pass(lib, layers, xs, bias, T, H, F, E, K, args.steps, args.warmup,
-                  events=not args.no_kernel_events)
+                  events=not args.no_kernel_events, routing=args.routing)
     cpu = None
     if not args.no_cpu_baseline:
         cpu = _cpu_baseline(layers, xs, bias, T, H, F, E, K, L, args.cpu_seconds)
@@ -331,7 +389,8 @@ def _e2e(args) -> int:
                           gpu_expert_slots=args.gpu_expert_slots if args.offload else None,
                           prefetch=policy if args.offload else PrefetchPolicy.NONE,
                           prefetch_depth=args.prefetch_depth,
-                          gpu_slots_per_layer=args.gpu_slots_per_layer if args.offload else None)
+                          gpu_slots_per_layer=args.gpu_slots_per_layer if args.offload else None,
+                          cache_policy=args.cache_policy)
     _log(f"weights synthesized, engine built ({time.time() - t_setup:.1f} s)")
     eng.prepare(Ksteps + 1)
     torch.cuda.synchronize()
@@ -385,7 +444,8 @@ def _e2e(args) -> int:
         st = eng.cache_manager.stats()
         config.update({"gpu_expert_slots": args.gpu_expert_slots, "prefetch": args.prefetch,
                        "prefetch_depth": args.prefetch_depth,
-                       "gpu_slots_per_layer": args.gpu_slots_per_layer})
+                       "gpu_slots_per_layer": args.gpu_slots_per_layer,
+                       "cache_policy": args.cache_policy})
     result = {
         "metric": METRIC,
         "value": round(res.tps, 3),

@@ -37,7 +37,7 @@ class InferenceEngine:
                  offload: bool = False, gpu_expert_slots: Optional[int] = None,
                  prefetch: PrefetchPolicy = PrefetchPolicy.NONE, prefetch_depth: int = 1,
                  use_graph: bool = True, logger: Optional[logging.Logger] = None,
-                 gpu_slots_per_layer: Optional[int] = None) -> None:
+                 gpu_slots_per_layer: Optional[int] = None, cache_policy="lru") -> None:
         self._logger = logger or logging.getLogger(__name__)
         self.device = torch.device(device)
         self.weights = weights
@@ -51,20 +51,21 @@ class InferenceEngine:
         moe = None
         if offload:
             moe = self._build_offload(gpu_expert_slots, prefetch, prefetch_depth,
-                                      gpu_slots_per_layer)
+                                      gpu_slots_per_layer, cache_policy)
         self.decoder = NativeDecoder(weights, max_seq, self.device, moe=moe)
         self._graph = None
         self._last_logits = None
 
     # ------------------------------------------------------------------ offload wiring
-    def _build_offload(self, gpu_slots, policy, depth, slots_per_layer):
+    def _build_offload(self, gpu_slots, policy, depth, slots_per_layer, cache_policy):
         """The host-authoritative offload mode: every expert pinned once in host memory
         (one arena per layer) as the CacheManager's CPU tier; a bounded GPU tier of
         `gpu_slots` experts (default: all) in a preallocated device-slot arena, filled by
         single-copy host-to-device transfers on a side stream that the compute stream waits
         for with events.  With `slots_per_layer` the GPU tier is partitioned by layer and
         layers keep the experts they transferred (otherwise they are demoted after the
-        layer, the reference's contract)."""
+        layer, the reference's contract).  `cache_policy` ("lru", "lfu", "arc" or an
+        EvictionPolicy) picks the GPU tier's victims."""
         from ..cache.manager import CacheManager
         from ..cache.types import EvictionPolicy
         from ..model.expert import PrequantizedNF4Expert
@@ -79,7 +80,8 @@ class InferenceEngine:
         gpu_slots = n_experts if gpu_slots is None else max(1, int(gpu_slots))
         if slots_per_layer is not None:
             gpu_slots = min(gpu_slots, slots_per_layer * s.layers)
-        cm = CacheManager(gpu_slots=gpu_slots, cpu_slots=n_experts, policy=EvictionPolicy.LRU,
+        cm = CacheManager(gpu_slots=gpu_slots, cpu_slots=n_experts,
+                          policy=EvictionPolicy(cache_policy),
                           gpu_slots_per_layer=slots_per_layer)
         store = PinnedExpertStore()
         for l, lw in enumerate(self.weights.layers):

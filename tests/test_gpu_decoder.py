@@ -385,13 +385,15 @@ def test_engine_graph_replays_match_eager(cuda_device):
         np.testing.assert_array_equal(lg, outs[0][1])
 
 
-@pytest.mark.parametrize("policy,slots,per_layer", [
-    ("NONE", 4, None), ("NEXT_LAYER", 4, None), ("NEXT_ROUTER", 4, None),
-    ("NONE", 3, 1), ("NEXT_ROUTER", 6, 3)])
-def test_engine_offload_matches_reference(cuda_device, policy, slots, per_layer):
+@pytest.mark.parametrize("policy,slots,per_layer,evict", [
+    ("NONE", 4, None, "lru"), ("NEXT_LAYER", 4, None, "lru"), ("NEXT_ROUTER", 4, None, "lru"),
+    ("NONE", 3, 1, "lru"), ("NEXT_ROUTER", 6, 3, "lru"),
+    ("NEXT_ROUTER", 4, None, "lfu"), ("NONE", 4, 2, "lfu"),
+    ("NEXT_ROUTER", 4, None, "arc"), ("NONE", 4, 2, "arc")])
+def test_engine_offload_matches_reference(cuda_device, policy, slots, per_layer, evict):
     """Offload mode: the NF4 store pinned on the host, a few GPU expert slots (fewer than a
-    40-token prefill routes to per layer), the prefetch policies, and the per-layer GPU tier
-    that keeps transferred experts across tokens."""
+    40-token prefill routes to per layer), the prefetch policies, the per-layer GPU tier
+    that keeps transferred experts across tokens, and the LRU / LFU / ARC GPU tiers."""
     from moeinfra_amd.engine.engine import InferenceEngine
     from moeinfra_amd.engine.types import ForwardRequest, PrefetchPolicy
     from moeinfra_amd.transfer import scheduler as sched_mod
@@ -399,7 +401,9 @@ def test_engine_offload_matches_reference(cuda_device, policy, slots, per_layer)
     w = _small_engine_weights(cuda_device)
     prompt = torch.randint(0, w.shape.vocab, (1, 6), generator=torch.Generator().manual_seed(6))
     eng = InferenceEngine(w, max_seq=64, device=cuda_device, offload=True, gpu_expert_slots=slots,
-                          prefetch=PrefetchPolicy[policy], gpu_slots_per_layer=per_layer)
+                          prefetch=PrefetchPolicy[policy], gpu_slots_per_layer=per_layer,
+                          cache_policy=evict)
+    assert eng.cache_manager.policy.value == evict
     n_prof = len(sched_mod.EXECUTE_NEXT_PROFILE)
     res = eng.generate(ForwardRequest(prompt, max_new_tokens=5))
     _check_against_reference(res, w, prompt)
