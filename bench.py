@@ -59,6 +59,9 @@ def parse_args():
     p.add_argument("--cache-policy", choices=["lru", "lfu", "arc"], default="lru",
                    help="offload mode's GPU-tier eviction policy (the reference's default: lru)")
     p.add_argument("--prefetch-depth", type=int, default=2)
+    p.add_argument("--prefetch-prefix-mib", type=float, default=8.0,
+                   help="offload mode with --prefetch next_router: copy only this many MiB of "
+                        "each guessed expert ahead (a bounded prefix); 0: the whole image")
     p.add_argument("--tokens", type=int, default=1, help="tokens per decode step (decode mode)")
     p.add_argument("--routing", choices=["uniform", "zipf"], default="uniform")
     p.add_argument("--seed", type=int, default=0)
@@ -390,7 +393,8 @@ def _e2e(args) -> int:
                           prefetch=policy if args.offload else PrefetchPolicy.NONE,
                           prefetch_depth=args.prefetch_depth,
                           gpu_slots_per_layer=args.gpu_slots_per_layer if args.offload else None,
-                          cache_policy=args.cache_policy)
+                          cache_policy=args.cache_policy,
+                          prefetch_prefix_bytes=int(args.prefetch_prefix_mib * 2**20))
     _log(f"weights synthesized, engine built ({time.time() - t_setup:.1f} s)")
     eng.prepare(Ksteps + 1)
     torch.cuda.synchronize()
@@ -444,6 +448,7 @@ def _e2e(args) -> int:
         st = eng.cache_manager.stats()
         config.update({"gpu_expert_slots": args.gpu_expert_slots, "prefetch": args.prefetch,
                        "prefetch_depth": args.prefetch_depth,
+                       "prefetch_prefix_mib": args.prefetch_prefix_mib,
                        "gpu_slots_per_layer": args.gpu_slots_per_layer,
                        "cache_policy": args.cache_policy})
     result = {
@@ -487,7 +492,7 @@ def _e2e(args) -> int:
             "cache_evictions": st.evictions,
             "expert_bytes": int(nf4_expert_bytes(s.hidden, s.ffn)),
             "pinned_store_bytes": eng.pinned_store.pinned_bytes,
-            "copies_in_timed_run": {k: c1[k] - copies0[k] for k in ("image", "staged")},
+            "copies_in_timed_run": {k: c1[k] - copies0[k] for k in ("image", "staged", "prefix")},
             "copies_per_decode_step": round((c1["image"] + c1["staged"] - copies0["image"]
                                              - copies0["staged"]) / (Ksteps + 1), 2),
             "host_link_gbps_timed_run": round(moved / ((res.ttft_ms + decode_ms) * 1e-3) / 1e9, 2),

@@ -15,7 +15,8 @@ Two expert modes, as in the reference:
   MoELayer (route, start the copies of the routed experts that are not resident as single
   hipMemcpyAsync calls on a side stream, run the kernels behind stream waits on their
   events, demote the ones that were not resident), optionally with a per-layer GPU tier
-  that keeps transferred experts and with the PrefetchEngine starting later layers' copies.
+  that keeps transferred experts and with the PrefetchEngine starting later layers' copies
+  (whole copies, or with NEXT_ROUTER bounded prefixes sized to the host link's idle gap).
 """
 from __future__ import annotations
 
@@ -30,6 +31,11 @@ from .prefetch import PrefetchEngine
 from .types import ForwardRequest, ForwardResult, PrefetchPolicy
 
 
+#: NEXT_ROUTER's bounded prefix per guessed expert: about the host link's idle time between
+#: two layers' copies in the offload decode loop (8 MiB at ~54 GB/s is ~0.15 ms).
+NEXT_ROUTER_PREFIX_BYTES = 8 << 20
+
+
 class InferenceEngine:
     """Native Mixtral-shaped NF4 MoE inference engine on one GPU."""
 
@@ -37,7 +43,8 @@ class InferenceEngine:
                  offload: bool = False, gpu_expert_slots: Optional[int] = None,
                  prefetch: PrefetchPolicy = PrefetchPolicy.NONE, prefetch_depth: int = 1,
                  use_graph: bool = True, logger: Optional[logging.Logger] = None,
-                 gpu_slots_per_layer: Optional[int] = None, cache_policy="lru") -> None:
+                 gpu_slots_per_layer: Optional[int] = None, cache_policy="lru",
+                 prefetch_prefix_bytes: Optional[int] = NEXT_ROUTER_PREFIX_BYTES) -> None:
         self._logger = logger or logging.getLogger(__name__)
         self.device = torch.device(device)
         self.weights = weights
@@ -48,6 +55,9 @@ class InferenceEngine:
         self.transfer_scheduler = None
         self.prefetch_engine = None
         self.pinned_store = None
+        self._prefix_bytes = None            # None: NEXT_ROUTER copies whole experts ahead
+        if prefetch_prefix_bytes and prefetch == PrefetchPolicy.NEXT_ROUTER:
+            self._prefix_bytes = int(prefetch_prefix_bytes)
         moe = None
         if offload:
             moe = self._build_offload(gpu_expert_slots, prefetch, prefetch_depth,
@@ -65,7 +75,8 @@ class InferenceEngine:
         for with events.  With `slots_per_layer` the GPU tier is partitioned by layer and
         layers keep the experts they transferred (otherwise they are demoted after the
         layer, the reference's contract).  `cache_policy` ("lru", "lfu", "arc" or an
-        EvictionPolicy) picks the GPU tier's victims."""
+        EvictionPolicy) picks the GPU tier's victims.  With NEXT_ROUTER bounded prefixes
+        the arena holds one more slot per expert of a layer for the prefixes in flight."""
         from ..cache.manager import CacheManager
         from ..cache.types import EvictionPolicy
         from ..model.expert import PrequantizedNF4Expert
@@ -91,7 +102,8 @@ class InferenceEngine:
         self.pinned_store = store
         image_bytes = cm.peek_cpu(0, 0).image_layout.nbytes
         self._transfer_stream = torch.cuda.Stream(self.device)
-        slots = DeviceExpertSlots(gpu_slots, image_bytes, self.device)
+        extra = s.experts if self._prefix_bytes else 0
+        slots = DeviceExpertSlots(gpu_slots + extra, image_bytes, self.device)
         sched = TransferScheduler(cm, 24.0, max(2 * s.experts, 2 * s.top_k * max(depth, 1)),
                                   transfer_stream=self._transfer_stream, device_slots=slots)
         self.cache_manager, self.transfer_scheduler = cm, sched
@@ -114,11 +126,16 @@ class InferenceEngine:
             # set covers it, so the guess costs no extra host synchronisation.
             nxt, _ = self._moe_layers[l + 1].router.route(x)
         out = self._moe_layers[l].forward(x)
-        if nxt is not None:
+        if pe.policy == PrefetchPolicy.NEXT_ROUTER:
             pe.poll()
-            pe.cancel_stale(l + 1)
-            pe.prefetch(l + 1, nxt.reshape(-1).tolist())
-        elif pe.policy != PrefetchPolicy.NEXT_ROUTER:
+            pe.cancel_stale(l + 1)           # also settles this layer's prefixes
+            if nxt is not None:
+                guess = nxt.reshape(-1).tolist()
+                if self._prefix_bytes:
+                    pe.prefetch_prefix(l + 1, guess, self._prefix_bytes)
+                else:
+                    pe.prefetch(l + 1, guess)
+        else:
             pe.on_layer_complete(l, self._moe_layers[l].last_expert_indices)
         return out
 

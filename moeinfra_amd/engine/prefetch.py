@@ -11,16 +11,20 @@ to start:
 * NONE: nothing.
 * NEXT_LAYER / LOOKAHEAD (the reference's heuristic, prefetch.py:177-192): the experts the
   completed layer routed to, for the next layer or the next ``depth`` layers.
-* NEXT_ROUTER: the caller supplies the prediction through ``prefetch(layer, experts)`` --
-  the engine runs the next layer's router on the current layer's MoE input.
+* NEXT_ROUTER: the caller supplies the prediction through ``prefetch(layer, experts)`` or
+  ``prefetch_prefix(layer, experts, nbytes)`` -- the engine runs the next layer's router on
+  the current layer's MoE input.
 
-On a host link that is already saturated by demand copies (the offload decode loop moves
-two 99 MB experts per layer over PCIe) a wrong guess costs a whole copy while a right one
-saves only the gap between two layers' copies; DESIGN.md's offload section has the numbers.
+On a host link that demand copies already keep busy (the offload decode loop moves two
+99 MB experts per layer over PCIe) a wrong full-copy guess costs a whole copy, while a right
+one saves at most the link's idle gap between two layers' copies.  A bounded prefix
+(``prefetch_prefix``) copies only the first bytes of each guessed expert, sized to that gap:
+a right guess leaves only the rest of the image to copy once the layer routes, a wrong one
+costs no more than the gap.
 
 ``_in_flight`` maps (layer_id, expert_id) to the request id of each prefetch still in
 flight, as in the reference (its tests inspect it); ``poll`` retires finished ones and
-``cancel_stale`` cancels those for layers already passed.
+``cancel_stale`` cancels those for layers already passed, and drops their unused prefixes.
 """
 from __future__ import annotations
 
@@ -46,8 +50,10 @@ class PrefetchEngine:
         self.depth = depth
         self._logger = logger or logging.getLogger(__name__)
         self._in_flight: dict[tuple[int, int], str] = {}
+        self._prefixes: set[tuple[int, int]] = set()
         self._ids = itertools.count()
-        self.counts = {"started": 0, "refused": 0, "cancelled": 0}
+        self.counts = {"started": 0, "refused": 0, "cancelled": 0,
+                       "prefixes": 0, "prefixes_used": 0, "prefixes_dropped": 0}
 
     # ------------------------------------------------------------------ starting copies
     def _start(self, layer_id: int, expert_id: int) -> Optional[str]:
@@ -70,6 +76,17 @@ class PrefetchEngine:
         """Start the copies of the given experts of `layer_id` (ascending, each once)."""
         started = (self._start(layer_id, e) for e in sorted({int(e) for e in expert_ids}))
         return [rid for rid in started if rid is not None]
+
+    def prefetch_prefix(self, layer_id: int, expert_ids: Iterable[int], nbytes: int) -> List[int]:
+        """Start bounded prefix copies (the first `nbytes` of each image) of the given
+        experts of `layer_id`; the experts whose prefix was started."""
+        started = []
+        for e in sorted({int(e) for e in expert_ids}):
+            if self._transfer_scheduler.start_prefix(layer_id, e, nbytes):
+                self._prefixes.add((layer_id, e))
+                started.append(e)
+        self.counts["prefixes"] += len(started)
+        return started
 
     # ------------------------------------------------------------------ policies
     def _target_layers(self, current_layer: int) -> range:
@@ -103,6 +120,12 @@ class PrefetchEngine:
             if self._transfer_scheduler.cancel(self._in_flight.pop(key)):
                 n += 1
         self.counts["cancelled"] += n
+        for key in [k for k in self._prefixes if k[0] < current_layer]:
+            self._prefixes.discard(key)
+            if self._transfer_scheduler.drop_prefix(*key):
+                self.counts["prefixes_dropped"] += 1
+            else:                              # the layer's transfer completed it
+                self.counts["prefixes_used"] += 1
         return n
 
     def poll(self) -> None:

@@ -80,8 +80,12 @@ class TransferScheduler:
         self._queued: dict[str, TransferRequest] = {}
         self._busy: dict[tuple, str] = {}          # (layer, expert, direction) -> request id
         self._async: dict[tuple[int, int], TransferHandle] = {}
-        #: Copies issued so far, by source, and the bytes they moved over the host link.
-        self.copies = {"image": 0, "staged": 0, "bytes": 0}
+        #: Copies issued so far, by source, and the bytes they moved over the host link
+        #: ("prefix": bounded prefix copies, see start_prefix).
+        self.copies = {"image": 0, "staged": 0, "prefix": 0, "bytes": 0}
+        #: (layer, expert) -> (device region, slot lease, bytes already copied) of the
+        #: bounded prefixes started and not yet completed or dropped.
+        self._prefixes: dict[tuple[int, int], tuple] = {}
 
     # ------------------------------------------------------------------ queue
     def _is_duplicate(self, request: TransferRequest) -> bool:
@@ -189,10 +193,17 @@ class TransferScheduler:
             layout = ImageLayout.of(staging.tensors)
         profile["staging_ms"] = (time.perf_counter() - t0) * 1e3
         profile["source"] = "staged" if staging is not None else "image"
+        key = (request.layer_id, request.expert_id)
+        prefix = self._prefixes.pop(key, None) if staging is None else None
         try:
             self._cache_manager.make_room_gpu(request.layer_id, request.expert_id)
             self._in_flight_count()           # retire finished handles (they hold experts)
-            region, fence, lease = self._destination(layout.nbytes)
+            if prefix is not None:            # the slot already holds the image's first bytes
+                region, lease, done_bytes = prefix
+                fence = None                  # honoured when the prefix was issued
+            else:
+                region, fence, lease = self._destination(layout.nbytes)
+                done_bytes = 0
         except Exception:
             if staging is not None:
                 self._staging_pool.release(staging)
@@ -205,7 +216,7 @@ class TransferScheduler:
             if timing:
                 timing[0].record(stream)
             if staging is None:                # the copy goes out before any host bookkeeping
-                region.copy_(image, non_blocking=True)
+                region[done_bytes:].copy_(image[done_bytes:], non_blocking=True)
             else:
                 staged = layout.views(region)
                 for f in layout.fields:
@@ -218,12 +229,54 @@ class TransferScheduler:
             self._staging_pool.mark_transfer_complete(staging, stream)
             self._staging_pool.release(staging)
         self.copies[profile["source"]] += 1
-        self.copies["bytes"] += layout.nbytes
+        self.copies["bytes"] += layout.nbytes - done_bytes
         expert = ReconstructedNF4Expert(cpu_expert, views)
         expert.ready_event = done
         expert.device_lease = lease            # the slot is reused once the expert is gone
         self._cache_manager.put(request.layer_id, request.expert_id, expert, device="cuda:0")
         return expert, done
+
+    # ------------------------------------------------------------------ bounded prefixes
+    def start_prefix(self, layer_id: int, expert_id: int, nbytes: int) -> bool:
+        """Copy the first `nbytes` of the pinned image of (layer_id, expert_id) into a free
+        slot of the device arena, on the transfer stream, without publishing the expert: a
+        later transfer of the expert copies only the rest into the same slot.  A prefix
+        costs the host link `nbytes` whether or not the expert is routed, so a caller sizes
+        it to the link's idle time between two layers' copies.  False (nothing started) when
+        the expert is resident, in flight or already has a prefix, has no pinned image, or
+        no arena slot is free (a prefix never allocates)."""
+        key = (layer_id, expert_id)
+        if self._transfer_stream is None or key in self._prefixes or \
+                self._live_handle(*key) is not None or self._cache_manager.is_gpu_resident(*key):
+            return False
+        cpu_expert = self._cache_manager.peek_cpu(*key)
+        image = getattr(cpu_expert, "image", None)
+        layout = getattr(cpu_expert, "image_layout", None)
+        if image is None or layout is None:
+            return False
+        nbytes = min(int(nbytes), layout.nbytes)
+        slots = self._slots_for(layout.nbytes)
+        if nbytes <= 0 or layout.nbytes > slots.slot_bytes:
+            return False
+        slot = slots.take()
+        if slot is None:
+            return False
+        region, fence, lease = slots.region(slot, layout.nbytes), slots.fence(slot), slots.lease(slot)
+        stream = self._transfer_stream
+        with torch.cuda.stream(stream):
+            if fence is not None:
+                stream.wait_event(fence)
+            region[:nbytes].copy_(image[:nbytes], non_blocking=True)
+        self._prefixes[key] = (region, lease, nbytes)
+        self.copies["prefix"] += 1
+        self.copies["bytes"] += nbytes
+        return True
+
+    def drop_prefix(self, layer_id: int, expert_id: int) -> bool:
+        """Give back the slot of an unused prefix (fenced like any slot: the transfer stream
+        orders a later copy into it after the prefix copy).  False if there is none -- the
+        expert's transfer consumed it, or none was started."""
+        return self._prefixes.pop((layer_id, expert_id), None) is not None
 
     # ------------------------------------------------------------------ synchronous path
     def execute_next(self) -> Optional[TransferResult]:

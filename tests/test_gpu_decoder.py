@@ -402,7 +402,7 @@ def test_engine_offload_matches_reference(cuda_device, policy, slots, per_layer,
     prompt = torch.randint(0, w.shape.vocab, (1, 6), generator=torch.Generator().manual_seed(6))
     eng = InferenceEngine(w, max_seq=64, device=cuda_device, offload=True, gpu_expert_slots=slots,
                           prefetch=PrefetchPolicy[policy], gpu_slots_per_layer=per_layer,
-                          cache_policy=evict)
+                          cache_policy=evict, prefetch_prefix_bytes=None)  # whole copies
     assert eng.cache_manager.policy.value == evict
     n_prof = len(sched_mod.EXECUTE_NEXT_PROFILE)
     res = eng.generate(ForwardRequest(prompt, max_new_tokens=5))
@@ -417,6 +417,33 @@ def test_engine_offload_matches_reference(cuda_device, policy, slots, per_layer,
                    for l in range(w.shape.layers))
     elif policy == "NONE":                   # the reference's contract: demoted after use
         assert used == 0
+
+
+@pytest.mark.parametrize("prefix,slots,per_layer", [
+    (4096, 4, None), ("half", 4, None), ("whole", 4, None), ("half", 6, 3)])
+def test_engine_offload_prefix_prefetch_matches_reference(cuda_device, prefix, slots, per_layer):
+    """NEXT_ROUTER with bounded prefixes: the first bytes of each guessed expert's image go
+    ahead into a spare slot; the layer's transfer copies the rest into the same slot (a
+    prefix of a few KB, half the image, the whole image), or the unused prefix is dropped."""
+    from moeinfra_amd.engine.engine import InferenceEngine
+    from moeinfra_amd.engine.types import ForwardRequest, PrefetchPolicy
+
+    w = _small_engine_weights(cuda_device)
+    prompt = torch.randint(0, w.shape.vocab, (1, 6), generator=torch.Generator().manual_seed(7))
+    probe = InferenceEngine(w, max_seq=64, device=cuda_device, offload=True, gpu_expert_slots=slots)
+    image = probe.cache_manager.peek_cpu(0, 0).image_layout.nbytes
+    del probe
+    nbytes = {"half": image // 2 + 3, "whole": image}.get(prefix, prefix)
+    eng = InferenceEngine(w, max_seq=64, device=cuda_device, offload=True, gpu_expert_slots=slots,
+                          prefetch=PrefetchPolicy.NEXT_ROUTER, gpu_slots_per_layer=per_layer,
+                          prefetch_prefix_bytes=nbytes)
+    res = eng.generate(ForwardRequest(prompt, max_new_tokens=6))
+    _check_against_reference(res, w, prompt)
+    c = eng.prefetch_engine.counts
+    assert c["prefixes"] > 0 and c["started"] == 0       # prefixes only, no whole copies
+    assert c["prefixes_used"] > 0
+    assert c["prefixes_used"] + c["prefixes_dropped"] <= c["prefixes"]
+    assert eng.transfer_scheduler.copies["prefix"] == c["prefixes"]
 
 
 def test_engine_full_mixtral_layer_matches_reference(cuda_device):

@@ -113,3 +113,38 @@ def test_request_and_result_types():
                         stage_timings={"prefill": 1.0})
     assert res.token_ids == [1, 2]
     assert [p.value for p in PrefetchPolicy] == ["none", "next_layer", "lookahead", "next_router"]
+
+
+class PrefixScheduler(FakeScheduler):
+    """Scheduler double for bounded prefixes: refuses expert 7, and a prefix counts as
+    consumed once `consume` names it (the expert's transfer completed it)."""
+
+    def __init__(self):
+        super().__init__()
+        self.prefixes = {}
+
+    def start_prefix(self, layer_id, expert_id, nbytes):
+        if expert_id == 7 or (layer_id, expert_id) in self.prefixes:
+            return False
+        self.prefixes[(layer_id, expert_id)] = nbytes
+        return True
+
+    def consume(self, layer_id, expert_id):
+        self.prefixes.pop((layer_id, expert_id))
+
+    def drop_prefix(self, layer_id, expert_id):
+        return self.prefixes.pop((layer_id, expert_id), None) is not None
+
+
+def test_prefix_prefetch_bookkeeping():
+    eng, sch, _ = _engine(PrefetchPolicy.NEXT_ROUTER, scheduler=PrefixScheduler())
+    assert eng.prefetch_prefix(3, [5, 1, 5, 7], 1 << 20) == [1, 5]   # ascending, once, 7 refused
+    assert sch.prefixes == {(3, 1): 1 << 20, (3, 5): 1 << 20} and sch.submitted == []
+    assert eng.prefetch_prefix(3, [1], 1 << 20) == []                # already started
+    sch.consume(3, 5)                                                 # layer 3 routed to 5
+    eng.cancel_stale(current_layer=3)                                 # layer 3 not passed yet
+    assert eng.counts["prefixes_used"] == 0 and (3, 1) in sch.prefixes
+    eng.cancel_stale(current_layer=4)
+    assert eng.counts == {"started": 0, "refused": 0, "cancelled": 0, "prefixes": 2,
+                          "prefixes_used": 1, "prefixes_dropped": 1}
+    assert sch.prefixes == {}                                         # the unused slot is back
