@@ -244,8 +244,8 @@ gemv_kernel(const uint16_t *__restrict__ W, const uint16_t *__restrict__ x, int 
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const int cc = c + u < nchunk ? c + u : nchunk - 1;
-        wv[0][u] = *reinterpret_cast<const uint4 *>(w0 + cc * 512);
-        wv[1][u] = *reinterpret_cast<const uint4 *>(w1 + cc * 512);
+        wv[0][u] = ld_stream16(w0 + cc * 512);
+        wv[1][u] = ld_stream16(w1 + cc * 512);
       }
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
@@ -299,7 +299,7 @@ __device__ __forceinline__ void gemv1_load8(uint4 (&a)[kGemv1Chunks], const uint
 #pragma unroll
   for (int u = 0; u < kGemv1Chunks; ++u) {
     const int cc = c + u < nchunk ? c + u : nchunk - 1;
-    a[u] = *reinterpret_cast<const uint4 *>(w + cc * 512);
+    a[u] = ld_stream16(w + cc * 512);
   }
 }
 

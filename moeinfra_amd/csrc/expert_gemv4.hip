@@ -76,7 +76,7 @@ __device__ __forceinline__ void stream_tiles(const moe_nf4_expert_t &ex, const u
   auto load = [&](Stage4<NP, BC> &st, int t, int sg) {
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
-      st.q[p] = *reinterpret_cast<const uint4 *>(wq[p] + t * tile_bytes + sg * 256);
+      st.q[p] = ld_stream16(wq[p] + t * tile_bytes + sg * 256);
       st.s[p] = wa[p][t * tile_blocks + sg * 8];
     }
     const uint4 *px = reinterpret_cast<const uint4 *>(ap + sg * kStageVals);
