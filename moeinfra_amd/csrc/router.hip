@@ -1,14 +1,19 @@
-// K2: gate linear + fp32 softmax + top-k + renormalise, one workgroup per token.
+// K2: gate linear + fp32 softmax + top-k + renormalise, one wavefront per token.
 //
 // Follows ExpertRouter.route_with_logits (engine/router.py:50-94):
 //   logits = bf16(x . gate^T)          F.linear in the activation dtype  (:66-69)
 //   p      = softmax(float(logits))    fp32                               (:81-84)
 //   w, idx = topk(p, k)                descending                         (:86-90)
 //   w     /= w.sum(-1)                                                    (:92)
-// The dot products accumulate in fp32 (each thread a strided slice of H, then a
-// butterfly reduction per wave and a fixed-order sum over the waves).  An optional fp32
-// per-expert bias is added to float(logits) before the softmax (skewed-routing
-// workloads).  Ties in p keep the lower index.
+// A workgroup holds eight tokens, one per wavefront.  The gate goes through LDS: whole when
+// its E x H values fit 64 KB (the Mixtral router: 8 x 4096), staged with every load in
+// flight at once, else in double-buffered 8 KB chunks; each workgroup reads it once for its
+// eight tokens.  A wave's gate products run on the 4x4x4 MFMA (16 K slices and four experts
+// per instruction, fp32 accumulation), a DPP/shuffle butterfly completes each expert's sum,
+// and the E logits land in lanes 0..E-1.  Softmax and top-k run across those lanes with
+// shuffle reductions and ballots.  An optional fp32 per-expert bias is added to
+// float(logits) before the softmax (skewed-routing workloads).  Ties in p keep the lower
+// index.
 #include "common.h"
 
 namespace moe {
@@ -38,109 +43,222 @@ __device__ __forceinline__ void gate_step(const uint16_t *__restrict__ gate, int
   }
 }
 
-constexpr int kRouterThreads = 256;
-constexpr int kRouterWaves = kRouterThreads / kWave;
+constexpr int kRtWaves = 8;  // tokens per workgroup, one wavefront each
+constexpr int kRtThreads = kRtWaves * kWave;
+constexpr int kRtChunkBytes = 8192;  // gate bytes per LDS chunk (all expert rows)
+// WHOLE: the E x H gate fits kRtWholeBytes of LDS and is staged at once (every load in
+// flight together: one memory round trip before the products); otherwise it streams in
+// double-buffered 8 KB chunks.
+constexpr int kRtWholeBytes = 65536;
+constexpr int kRtPad = 8;  // values of padding per LDS gate row (rows 16 bytes apart in banks)
 
-// One workgroup per token: the 256 threads split H (8 values per thread per step, 16-byte
-// loads of x and of every gate row), reduce within each wave and then across the four
-// waves in a fixed order; wave 0 finishes the softmax and top-k.
-template <int EMAX>
-__global__ void __launch_bounds__(kRouterThreads)
+// Over lanes 0..N-1 (N = 16: DPP within the row; N = 32, 64: then shuffles): every lane
+// of those rows gets the result, the same bits in all of them (each step combines two
+// partials that the partner combines in the other order).
+template <int N>
+__device__ __forceinline__ float rt_max(float v) {
+  v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xf, 0xf, false)));
+  v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xf, 0xf, false)));
+  v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x124, 0xf, 0xf, false)));
+  v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x128, 0xf, 0xf, false)));
+#pragma unroll
+  for (int o = 16; o < N; o <<= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+template <int N>
+__device__ __forceinline__ float rt_sum(float v) {
+#pragma unroll
+  for (int o = 1; o < N; o <<= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+typedef __attribute__((__vector_size__(4 * sizeof(short)))) short rt_s16x4;
+__device__ __forceinline__ rt_s16x4 rt_pair(uint32_t lo, uint32_t hi) {
+  return __builtin_bit_cast(rt_s16x4, make_uint2(lo, hi));
+}
+// Sum over the 16 lanes that share lane % 4 (DPP rotations within rows, then across rows).
+__device__ __forceinline__ float rt_sum16(float v) {
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x124, 0xf, 0xf, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x128, 0xf, 0xf, false));
+  v += __shfl_xor(v, 16, kWave);
+  v += __shfl_xor(v, 32, kWave);
+  return v;
+}
+
+// Gate products of one token per wavefront on v_mfma_f32_4x4x4_16b_bf16: per 128-value
+// step of H, lane (b = lane / 4, j = lane % 4) holds values 8b .. 8b+7 of the token (A
+// rows, the same token in all four) and of gate row 4g + j (B columns) for each group g of
+// four experts; the 16 MFMA blocks are 16 K slices, summed by a butterfly at the end.
+template <int EMAX, bool WHOLE>
+__global__ void __launch_bounds__(kRtThreads)
 router_topk_kernel(const uint16_t *__restrict__ x, const uint16_t *__restrict__ gate,
                    const float *__restrict__ bias, int64_t T, int H, int E, int k,
                    uint16_t *__restrict__ logits_out, float *__restrict__ w_out,
-                   int64_t *__restrict__ idx_out, int32_t *__restrict__ idx32_out) {
-  __shared__ float s_part[kRouterWaves][EMAX];
+                   int64_t *__restrict__ idx_out, int32_t *__restrict__ idx32_out, int tpw) {
+  static_assert(EMAX == 8 || EMAX == 16 || EMAX == 32, "EMAX must be 8, 16 or 32");
+  constexpr int G = EMAX / 4;
+  constexpr int CH = kRtChunkBytes / 2 / EMAX;  // streamed: values per LDS chunk (512, 256, 128)
+  constexpr int SUB = CH / 128;                 // 128-value MFMA steps per streamed chunk
+  constexpr int PPR = CH / 8;                   // 16-byte pieces per row and chunk
+  static_assert(EMAX * PPR == kRtThreads, "one 16-byte gate piece per thread and chunk");
+  constexpr int CROW = CH + kRtPad;             // streamed LDS row stride (values)
+  __shared__ __attribute__((aligned(16))) uint16_t s_g[WHOLE ? 1 : 2][WHOLE ? 8 : EMAX * CROW];
+  extern __shared__ __attribute__((aligned(16))) uint16_t s_whole[];  // WHOLE: [E][H + pad]
+
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = tid >> 6;
-  const int64_t t = blockIdx.x;
+  const int lj = lane & 3, lb = lane >> 2;
+  // Waves 0..tpw-1 hold tokens; every wave stages the gate (and, streamed, passes every
+  // chunk's barrier).
+  const int64_t t = (int64_t)blockIdx.x * tpw + wave;
+  const bool live = wave < tpw && t < T;
+  const uint16_t *xr = x + (live ? t : T - 1) * (int64_t)H;
+  const int n_steps = (H + 127) / 128;
+  // The lane's 8 values of 128-value step st (zeros past H, from a clamped in-bounds load).
+  auto load_x16 = [&](int st) -> uint4 {
+    const int v = st * 128 + 8 * lb;
+    const uint4 q = *reinterpret_cast<const uint4 *>(xr + (v < H ? v : H - 8));
+    const bool in = v < H;
+    return make_uint4(in ? q.x : 0u, in ? q.y : 0u, in ? q.z : 0u, in ? q.w : 0u);
+  };
 
-  float acc[EMAX];
+  f32x4 gacc[G];
 #pragma unroll
-  for (int e = 0; e < EMAX; ++e) acc[e] = 0.0f;
+  for (int g = 0; g < G; ++g) gacc[g] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  if constexpr (WHOLE) {
+    // Rows e < E of the gate in LDS, each padded with zeros to a multiple of 128 values
+    // (+ kRtPad), so every step reads inside its row; every thread's pieces in flight at
+    // once, with the token's first eight slices.
+    const int hp = n_steps * 128;
+    const int stride = hp + kRtPad;
+    constexpr int XB = 8;
+    uint4 xq[XB];
+#pragma unroll
+    for (int u = 0; u < XB; ++u) xq[u] = load_x16(u);
+    const int ppr = hp / 8;
+#pragma unroll 8
+    for (int p = tid; p < E * ppr; p += kRtThreads) {
+      const int e = p / ppr, o = (p - e * ppr) * 8;
+      *reinterpret_cast<uint4 *>(s_whole + e * stride + o) =
+          o < H ? *reinterpret_cast<const uint4 *>(gate + (int64_t)e * H + o)
+                : make_uint4(0u, 0u, 0u, 0u);
+    }
+    __syncthreads();
+    if (wave >= tpw) return;  // wave-uniform; no barrier follows
+    // Groups' lanes past E read row E - 1 (their sums are discarded).
+    const uint16_t *grow[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+      grow[g] = s_whole + (4 * g + lj < E ? 4 * g + lj : E - 1) * stride + 8 * lb;
+    for (int s0 = 0; s0 < n_steps; s0 += XB) {
+      if (s0 > 0) {
+#pragma unroll
+        for (int u = 0; u < XB; ++u) xq[u] = load_x16(s0 + u);
+      }
+      // Steps past the last re-read the last one with a zero token slice (load_x16).
+      uint4 gq[XB][G];
+#pragma unroll
+      for (int u = 0; u < XB; ++u) {
+        const int st = s0 + u < n_steps ? s0 + u : n_steps - 1;
+#pragma unroll
+        for (int g = 0; g < G; ++g) gq[u][g] = *reinterpret_cast<const uint4 *>(grow[g] + st * 128);
+      }
+#pragma unroll
+      for (int u = 0; u < XB; ++u)
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          gacc[g] = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(rt_pair(xq[u].x, xq[u].y),
+                                                          rt_pair(gq[u][g].x, gq[u][g].y), gacc[g], 0, 0, 0);
+          gacc[g] = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(rt_pair(xq[u].z, xq[u].w),
+                                                          rt_pair(gq[u][g].z, gq[u][g].w), gacc[g], 0, 0, 0);
+        }
+    }
+  } else {
+    // This thread's gate piece of a chunk: row ge (clamped to E - 1), values go .. go + 7.
+    const int ge = tid / PPR, go = (tid % PPR) * 8;
+    const uint16_t *grow = gate + (int64_t)(ge < E ? ge : E - 1) * H;
+    const int n_chunks = (H + CH - 1) / CH;
+    auto load_piece = [&](int c) -> uint4 {
+      const int v = c * CH + go;
+      return v < H ? *reinterpret_cast<const uint4 *>(grow + v) : make_uint4(0u, 0u, 0u, 0u);
+    };
+    uint4 piece = load_piece(0);
+    uint4 xq[SUB], xn[SUB];
+#pragma unroll
+    for (int u = 0; u < SUB; ++u) xq[u] = load_x16(u);
+    for (int c = 0; c < n_chunks; ++c) {
+      uint16_t *buf = s_g[c & 1];
+      *reinterpret_cast<uint4 *>(buf + ge * CROW + go) = piece;
+      __syncthreads();  // chunk c visible; the other buffer is free (its readers passed here)
+      if (c + 1 < n_chunks) {
+        piece = load_piece(c + 1);
+#pragma unroll
+        for (int u = 0; u < SUB; ++u) xn[u] = load_x16((c + 1) * SUB + u);
+      }
+      uint4 gq[SUB][G];
+#pragma unroll
+      for (int u = 0; u < SUB; ++u)
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+          gq[u][g] = *reinterpret_cast<const uint4 *>(buf + (4 * g + lj) * CROW + u * 128 + 8 * lb);
+#pragma unroll
+      for (int u = 0; u < SUB; ++u)
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          gacc[g] = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(rt_pair(xq[u].x, xq[u].y),
+                                                          rt_pair(gq[u][g].x, gq[u][g].y), gacc[g], 0, 0, 0);
+          gacc[g] = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(rt_pair(xq[u].z, xq[u].w),
+                                                          rt_pair(gq[u][g].z, gq[u][g].w), gacc[g], 0, 0, 0);
+        }
+#pragma unroll
+      for (int u = 0; u < SUB; ++u) xq[u] = xn[u];
+    }
+  }
 
-  const uint16_t *xr = x + t * (int64_t)H;
-  for (int c = tid * 8; c < H; c += kRouterThreads * 8) {
-    const uint4 xv = *reinterpret_cast<const uint4 *>(xr + c);
-    const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
-    float xf[8];
+  // Expert 4g + j's total: the butterfly over the 16 blocks leaves it in every lane with
+  // lane % 4 == j; lane e (< E) takes expert e from lane e % 4.
+  float sum = 0.0f;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      xf[2 * j] = bf16lo_to_f32(xw[j]);
-      xf[2 * j + 1] = bf16hi_to_f32(xw[j]);
-    }
-    gate_step<EMAX>(gate, H, E, c, xf, acc);
+  for (int g = 0; g < G; ++g) {
+    const float v = __shfl(rt_sum16(gacc[g][0]), lane & 3, kWave);
+    if ((lane >> 2) == g) sum = v;
   }
-#pragma unroll
-  for (int e = 0; e < EMAX; ++e) {
-    if (e < E) {
-      const float v = wave_sum(acc[e]);
-      if (lane == 0) s_part[wave][e] = v;
-    }
-  }
-  __syncthreads();
-  if (wave != 0) return;
 
-  float p[EMAX];
-  float m = -INFINITY;
-#pragma unroll
-  for (int e = 0; e < EMAX; ++e) {
-    if (e < E) {
-      float v = s_part[0][e];
-#pragma unroll
-      for (int w = 1; w < kRouterWaves; ++w) v += s_part[w][e];
-      const uint16_t lb = f32_to_bf16(v);
-      if (logits_out != nullptr && lane == e) logits_out[t * E + e] = lb;
-      float l = bf16_to_f32(lb);
-      if (bias != nullptr) l = l + bias[e];
-      p[e] = l;
-      m = fmaxf(m, l);
-    }
+  // ---- softmax and top-k across lanes 0..E-1 (lane e = expert e)
+  const bool valid = lane < E;
+  float l = -INFINITY;
+  if (valid) {
+    const uint16_t lb = f32_to_bf16(sum);
+    if (live && logits_out != nullptr) logits_out[t * E + lane] = lb;
+    l = bf16_to_f32(lb);
+    if (bias != nullptr) l = l + bias[lane];
   }
-  float s = 0.0f;
-#pragma unroll
-  for (int e = 0; e < EMAX; ++e) {
-    if (e < E) {
-      p[e] = expf(p[e] - m);
-      s += p[e];
-    }
-  }
-#pragma unroll
-  for (int e = 0; e < EMAX; ++e)
-    if (e < E) p[e] = p[e] / s;
-
-  // Top-k by repeated arg-max (strict '>' keeps the lowest index among equals).
-  float topw[MOE_MAX_TOPK];
-  int topi[MOE_MAX_TOPK];
-  uint64_t taken = 0;
-  float wsum = 0.0f;
+  constexpr int NR = EMAX <= 16 ? 16 : 32;  // lanes holding experts
+  const float mx = rt_max<NR>(l);
+  const float pe = valid ? expf(l - mx) : 0.0f;
+  const float p = pe / rt_sum<NR>(pe);
+  bool taken = false;
+  float wsum = 0.0f, my_w = 0.0f;
+  int my_i = 0;
   for (int j = 0; j < k; ++j) {
-    float best = -INFINITY;
-    int bi = -1;
-#pragma unroll
-    for (int e = 0; e < EMAX; ++e) {
-      if (e < E && !((taken >> e) & 1ull) && (bi < 0 || p[e] > best)) {
-        best = p[e];
-        bi = e;
-      }
-    }
-    taken |= 1ull << bi;
-    topw[j] = best;
-    topi[j] = bi;
+    const bool cand = valid && !taken;
+    const float best = rt_max<NR>(cand ? p : -1.0f);
+    const uint64_t hit = __ballot(cand && p == best);
+    // No candidate equal to the maximum (NaN probabilities): the lowest untaken expert.
+    const uint64_t any = __ballot(cand);
+    const int win = hit != 0 ? (int)__builtin_ctzll(hit) : (int)__builtin_ctzll(any);
+    taken |= lane == win;
     wsum += best;
+    if (lane == j) {
+      my_i = win;
+      my_w = best;
+    }
   }
-  if (lane < k) {
-    float wv = 0.0f;
-    int iv = 0;
-    for (int j = 0; j < k; ++j)
-      if (j == lane) {
-        wv = topw[j];
-        iv = topi[j];
-      }
-    w_out[t * k + lane] = wv / wsum;
-    idx_out[t * k + lane] = iv;
-    if (idx32_out != nullptr) idx32_out[t * k + lane] = iv;
+  if (live && lane < k) {
+    w_out[t * k + lane] = my_w / wsum;
+    idx_out[t * k + lane] = my_i;
+    if (idx32_out != nullptr) idx32_out[t * k + lane] = my_i;
   }
 }
 
@@ -161,19 +279,28 @@ extern "C" int moe_router_topk(const void *x_bf16, const void *gate_bf16, const 
   MOE_REQUIRE(((uintptr_t)x_bf16 % 16) == 0 && ((uintptr_t)gate_bf16 % 16) == 0,
               "x and gate must be 16-byte aligned");
   MOE_REQUIRE(T <= 0x7fffffff, "too many tokens");
-  const dim3 g((unsigned)T), b(moe::kRouterThreads);
+  // Tokens per workgroup: eight once that still gives every CU a workgroup, fewer (down to
+  // one wavefront with a token, the other seven only staging the gate) for smaller batches,
+  // so that they spread over the CUs.
+  const int64_t cus = moe::device_cu_count();
+  int tpw = moe::kRtWaves;
+  while (tpw > 1 && (T + tpw - 1) / tpw < cus) tpw >>= 1;
+  const dim3 g((unsigned)((T + tpw - 1) / tpw)), b(moe::kRtThreads);
   hipStream_t s = (hipStream_t)stream;
+  const int64_t gate_bytes = (int64_t)E * ((H + 127) / 128 * 128 + moe::kRtPad) * 2;
+  const bool whole = gate_bytes <= moe::kRtWholeBytes + 16 * 32;
   auto args = [&](auto kern) {
-    hipLaunchKernelGGL(kern, g, b, 0, s, (const uint16_t *)x_bf16, (const uint16_t *)gate_bf16,
-                       (const float *)bias_f32, T, H, E, k, (uint16_t *)logits_bf16,
-                       (float *)weights_f32, (int64_t *)idx_i64, (int32_t *)idx_i32);
+    hipLaunchKernelGGL(kern, g, b, whole ? (size_t)gate_bytes : 0, s, (const uint16_t *)x_bf16,
+                       (const uint16_t *)gate_bf16, (const float *)bias_f32, T, H, E, k,
+                       (uint16_t *)logits_bf16, (float *)weights_f32, (int64_t *)idx_i64,
+                       (int32_t *)idx_i32, tpw);
   };
   if (E <= 8)
-    args(moe::router_topk_kernel<8>);
+    whole ? args(moe::router_topk_kernel<8, true>) : args(moe::router_topk_kernel<8, false>);
   else if (E <= 16)
-    args(moe::router_topk_kernel<16>);
+    whole ? args(moe::router_topk_kernel<16, true>) : args(moe::router_topk_kernel<16, false>);
   else
-    args(moe::router_topk_kernel<32>);
+    whole ? args(moe::router_topk_kernel<32, true>) : args(moe::router_topk_kernel<32, false>);
   MOE_LAUNCH_CHECK();
   return MOE_STATUS_OK;
 }

@@ -68,27 +68,47 @@ def test_quantize_bitexact(cuda_device, shape):
 
 
 # ------------------------------------------------------------------------------ K2
-@pytest.mark.parametrize("T,H,E,skew", [(1, 4096, 8, False), (16, 1024, 8, False),
-                                        (40, 4096, 8, True), (513, 4096, 8, False),
-                                        (7, 256, 16, False)])
-def test_router_matches_oracle(cuda_device, T, H, E, skew):
+@pytest.mark.parametrize("T,H,E,skew,k", [(1, 4096, 8, False, 2), (16, 1024, 8, False, 2),
+                                          (40, 4096, 8, True, 2), (513, 4096, 8, False, 2),
+                                          (7, 256, 16, False, 2), (4096, 4096, 8, False, 2),
+                                          (4096, 4096, 8, True, 2), (9, 1000, 32, True, 4),
+                                          (33, 4104, 16, False, 8), (3, 8, 8, False, 1)])
+def test_router_matches_oracle(cuda_device, T, H, E, skew, k):
+    """One wavefront per token: T not a multiple of the eight tokens of a workgroup, H not
+    a multiple of the gate chunk (512 / 256 / 128 values for E <= 8 / 16 / 32), E = 32."""
     from moeinfra_amd import ops, synth
 
     gen = synth.make_generator(T * 31 + H)
     gate = synth._normal((E, H), gen, "cpu", 0.02)
     x = synth.make_activations(T, H, gen)
     bias = synth.zipf_bias(E, seed=T) if skew else None
-    lg_want, w_want, i_want = orc.router(bits(x), bits(gate), k=2,
+    lg_want, w_want, i_want = orc.router(bits(x), bits(gate), k=k,
                                          bias=None if bias is None else bias.numpy())
-    lg, w, idx = ops.router_topk(x.to(cuda_device), gate.to(cuda_device), 2,
+    lg, w, idx = ops.router_topk(x.to(cuda_device), gate.to(cuda_device), k,
                                  bias=None if bias is None else bias.to(cuda_device))
-    lg_b = bits(lg).astype(np.int32)
-    # fp32 accumulation order differs from the oracle's; bf16 logits agree within 1 ulp.
-    assert np.abs(lg_b - lg_want.astype(np.int32)).max() <= 1
-    keep = ~near_tie_rows(lg_want, None if bias is None else bias.numpy())
+    # fp32 accumulation order differs from the oracle's: the bf16 logits agree within one
+    # bf16 ulp plus the reordering error of an fp32 dot product, bounded by
+    # 2^-18 * sum_i |x_i g_ei| (H <= 8192 terms); for logits far from zero that is 1 ulp.
+    lf_g = orc.bf16_to_f32(bits(lg)).astype(np.float64)
+    lf_w = orc.bf16_to_f32(lg_want).astype(np.float64)
+    mag = np.abs(orc.bf16_to_f32(bits(x)).astype(np.float64)) @ \
+        np.abs(orc.bf16_to_f32(bits(gate)).astype(np.float64)).T
+    ulp = np.maximum(np.abs(lf_w), 1e-30) * 2.0 ** -7
+    assert (np.abs(lf_g - lf_w) <= ulp + 2.0 ** -18 * mag).all()
+    # Rows where any two of the k + 1 largest logits are within 1 bf16 ulp may order (or
+    # choose) differently.
+    tie = np.zeros(T, dtype=bool)
+    for kk in range(1, min(k, E - 1) + 1):
+        tie |= near_tie_rows(lg_want, None if bias is None else bias.numpy(), k=kk)
+    keep = ~tie
     assert keep.sum() >= max(1, T // 2)
     np.testing.assert_array_equal(idx.cpu().numpy()[keep], i_want[keep])
-    np.testing.assert_allclose(w.cpu().numpy()[keep], w_want[keep], rtol=2e-5, atol=1e-6)
+    # Weights: fp32 softmax rounding where a row's logits equal the oracle's; elsewhere the
+    # logit difference propagates (the renormalised softmax moves by at most half of it).
+    dl = np.abs(lf_g - lf_w).max(axis=-1, keepdims=True)
+    wg, ww = w.cpu().numpy()[keep], w_want[keep]
+    assert (np.abs(wg - ww) <= 2e-5 * np.abs(ww) + 1e-6 + 0.5 * dl[keep]).all()
+    assert (dl == 0).mean() > 0.9
     np.testing.assert_allclose(w.sum(-1).cpu().numpy(), 1.0, atol=1e-5)
 
 
