@@ -82,8 +82,10 @@ def oracle_layer(gate: torch.Tensor, experts, x: torch.Tensor, k: int = 2, bias=
     return orc.moe_layer(bits(x), bits(gate), expert_fn, k=k, bias=b)
 
 
-def near_tie_rows(logits_bits: np.ndarray, bias=None, k: int = 2) -> np.ndarray:
-    """Rows whose k-th and (k+1)-th largest fp32 logits are within 1 bf16 ulp."""
+def near_tie_rows(logits_bits: np.ndarray, bias=None, k: int = 2, slack=None) -> np.ndarray:
+    """Rows whose k-th and (k+1)-th largest fp32 logits are within 1 bf16 ulp, plus
+    ``slack`` (scalar or per row: the reordering error of the fp32 dot products behind the
+    logits, which two implementations may sum in different orders)."""
     lf = orc.bf16_to_f32(logits_bits).astype(np.float64)
     if bias is not None:
         lf = lf + np.asarray(bias, dtype=np.float64)[None, :]
@@ -92,4 +94,24 @@ def near_tie_rows(logits_bits: np.ndarray, bias=None, k: int = 2) -> np.ndarray:
         return np.zeros(s.shape[0], dtype=bool)
     gap = s[:, k - 1] - s[:, k]
     ulp = np.maximum(np.abs(s[:, k - 1]), 1e-30) * 2.0 ** -7
+    if slack is not None:
+        ulp = ulp + 2.0 * np.asarray(slack, dtype=np.float64)
     return gap <= ulp
+
+
+def logit_slack(x_bits: np.ndarray, gate_bits: np.ndarray) -> np.ndarray:
+    """Per token: 2^-18 * max_e sum_h |x_h g_eh|, a bound on how far two fp32 summation
+    orders of the router's dot products (H <= 8192 terms) can land apart."""
+    xa = np.abs(orc.bf16_to_f32(x_bits).astype(np.float64))
+    ga = np.abs(orc.bf16_to_f32(gate_bits).astype(np.float64))
+    return 2.0 ** -18 * (xa @ ga.T).max(axis=-1)
+
+
+def assert_weights_close(w_got, w_want, lg_got_bits, lg_want_bits, rtol=1e-5, atol=1e-6):
+    """Routing weights: fp32 softmax rounding where a row's bf16 logits equal the oracle's;
+    elsewhere the logit difference propagates (a renormalised softmax moves by at most
+    half of it)."""
+    dl = np.abs(orc.bf16_to_f32(lg_got_bits).astype(np.float64) -
+                orc.bf16_to_f32(lg_want_bits).astype(np.float64)).max(axis=-1, keepdims=True)
+    w_got, w_want = np.asarray(w_got, np.float64), np.asarray(w_want, np.float64)
+    assert (np.abs(w_got - w_want) <= rtol * np.abs(w_want) + atol + 0.5 * dl).all()

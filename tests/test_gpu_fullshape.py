@@ -23,7 +23,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import bits, near_tie_rows
+from helpers import assert_weights_close, bits, logit_slack, near_tie_rows
 from oracle import moe_oracle as orc
 
 pytestmark = pytest.mark.gpu
@@ -146,18 +146,19 @@ def test_moe_layer_full_shape(cuda_device, T, routing):
     x = torch.randn((T, H), generator=gen, device=cuda_device).to(torch.bfloat16)
     bias = synth.zipf_bias(E, 50 + T) if routing == "zipf" else None
     print(f"layer T={T} routing={routing}", flush=True)
-    out, _, w, idx = ops.layer_forward(table, E, gate, x, K, F,
-                                       bias=None if bias is None else bias.to(cuda_device))
+    out, lg, w, idx = ops.layer_forward(table, E, gate, x, K, F,
+                                        bias=None if bias is None else bias.to(cuda_device),
+                                        want_logits=True)
     torch.cuda.synchronize()
     assert bool(torch.isfinite(out.float()).all())
     xb, gb = bits(x), bits(gate)
     b = None if bias is None else bias.numpy()
     lg_o, w_o, idx_o = orc.router(xb, gb, k=K, bias=b)
-    ok = ~near_tie_rows(lg_o, bias=b)
+    ok = ~near_tie_rows(lg_o, bias=b, slack=logit_slack(xb, gb))
     assert ok.mean() > 0.9
     idx_g, w_g = idx.cpu().numpy(), w.cpu().numpy()
     np.testing.assert_array_equal(idx_g[ok], idx_o[ok])
-    np.testing.assert_allclose(w_g[ok], w_o[ok], rtol=1e-5, atol=1e-6)
+    assert_weights_close(w_g[ok], w_o[ok], bits(lg)[ok], lg_o[ok])
     rows = _sample_rows(idx_o, T, seed=T)
     want, _ = orc.moe_layer(xb[rows], gb, _expert_fn(keep, wide), k=K, bias=b)
     got = bits(out)[rows]
