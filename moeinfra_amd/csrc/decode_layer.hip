@@ -142,7 +142,8 @@ template <int NP, int D, bool SLOW, bool BC, typename ItemFn, typename FinishFn,
           typename SlowFn>
 __device__ __forceinline__ void stream_items(int n_items, int nsq, ItemFn &&next_item,
                                              FinishFn &&finish, Hook &&hook, SlowFn &&slow_code,
-                                             const uint32_t *tbl, const uint32_t (&lane_const)[NP]) {
+                                             const uint32_t *tbl, const uint32_t (&lane_const)[NP],
+                                             gq_t dummy) {
   const int total = n_items * nsq;
   if (total <= 0) {
     hook();
@@ -151,11 +152,13 @@ __device__ __forceinline__ void stream_items(int n_items, int nsq, ItemFn &&next
   ItemPtr<NP> P;
   next_item(P);
   int lt = 0, ls = 0;  // next stage to load (item, stage)
+  bool past = false;   // past the last stage: the (unused) loads read `dummy`, an L2-resident
+                       // buffer, so that re-reads of streamed lines do not go back to HBM
   auto load = [&](Stage4<NP, BC> &st) {
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
-      st.q[p] = ld_u4_nt(P.wq[p] + ls * 256);
-      st.s[p] = P.wa[p][ls * 8];
+      st.q[p] = ld_u4_nt(past ? dummy + ls * 256 : P.wq[p] + ls * 256);
+      st.s[p] = *(past ? (ga_t)(dummy + ls * 256) : P.wa[p] + ls * 8);
     }
     const gx_t px = P.ap + ls * kStageVals;
 #pragma unroll
@@ -171,6 +174,7 @@ __device__ __forceinline__ void stream_items(int n_items, int nsq, ItemFn &&next
         next_item(P);
       } else {
         ls = nsq - 1;
+        past = true;
       }
     }
   };
@@ -290,7 +294,7 @@ __device__ __forceinline__ void stream_aligned(GrabFn &&grab, PtrFn &&set_ptrs,
                                                FinishFn &&finish, Hook &&hook,
                                                const uint32_t *tbl,
                                                const uint32_t (&lane_const)[NP], size_t arow,
-                                               float *aslot, XPtr xbase) {
+                                               float *aslot, XPtr xbase, gq_t dummy) {
   static_assert(NSQ >= 2 && NSQ <= 8, "an item's absmax block must fit one load per lane");
   static_assert(DEPTH >= 2 && DEPTH <= NSQ && NSQ % DEPTH == 0, "depth must divide NSQ");
   static_assert(!LA || DEPTH >= 3, "lookahead needs depth >= 3");
@@ -369,9 +373,17 @@ __device__ __forceinline__ void stream_aligned(GrabFn &&grab, PtrFn &&set_ptrs,
   for (;;) {
 #pragma unroll
     for (int d = 0; d < NSQ; ++d) {
-      if (d == kNext && nxt >= 0) {
-        P = Pn;
-        load_abs();
+      if (d == kNext) {
+        if (nxt >= 0) {
+          P = Pn;
+          load_abs();
+        } else {
+          // Past the last item the loads re-read stages already streamed (unused): point
+          // them at `dummy`, an L2-resident buffer, instead of lines that the non-temporal
+          // loads have let go.
+#pragma unroll
+          for (int p = 0; p < NP; ++p) P.wq[p] = dummy + (lane >> 2) * 16;
+        }
       }
       const int g = d + DEPTH - 1;  // stage sequence index of this step's load
       load(st[g % DEPTH], g < NSQ ? g : g - NSQ);
@@ -911,10 +923,10 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
       auto finish1 = [&](f32x4 (&ac)[2], int i) { finish_item(ac, i, 1); };
       if (NORM)
         stream_aligned<2, 8, kGateUpDepth, true, true, kLookahead>(
-            grab, set_ptrs, finish1, hook, s_tbl, lane_const, row_blocks, s_aslot[wave], xl);
+            grab, set_ptrs, finish1, hook, s_tbl, lane_const, row_blocks, s_aslot[wave], xl, (gq_t)gate);
       else
         stream_aligned<2, 8, kGateUpDepth, true, true, kLookahead>(
-            grab, set_ptrs, finish1, hook, s_tbl, lane_const, row_blocks, s_aslot[wave], xb);
+            grab, set_ptrs, finish1, hook, s_tbl, lane_const, row_blocks, s_aslot[wave], xb, (gq_t)gate);
       return;
     }
     auto finish_raw = [&](f32x4 (&ac)[2], int i) {
@@ -923,10 +935,10 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
     };
     if (NORM)
       stream_aligned<2, 8, kGateUpDepth, true, true, kLookahead>(
-          grab, set_ptrs, finish_raw, hook, s_tbl, lane_const, row_blocks, s_aslot[wave], xl);
+          grab, set_ptrs, finish_raw, hook, s_tbl, lane_const, row_blocks, s_aslot[wave], xl, (gq_t)gate);
     else
       stream_aligned<2, 8, kGateUpDepth, true, true, kLookahead>(
-          grab, set_ptrs, finish_raw, hook, s_tbl, lane_const, row_blocks, s_aslot[wave], xb);
+          grab, set_ptrs, finish_raw, hook, s_tbl, lane_const, row_blocks, s_aslot[wave], xb, (gq_t)gate);
     __syncthreads();
     if (tid < 4 * nit) {
       const int slot = tid >> 2;
@@ -962,13 +974,13 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
     return s_code[s_rt.active[item_expert(ci, tile)]];
   };
   if (!slow && bc)
-    stream_items<2, 6, false, true>(n_items, nsq, next_item, finish, hook, slow_code, s_tbl, lane_const);
+    stream_items<2, 6, false, true>(n_items, nsq, next_item, finish, hook, slow_code, s_tbl, lane_const, (gq_t)gate);
   else if (!slow)
-    stream_items<2, 4, false, false>(n_items, nsq, next_item, finish, hook, slow_code, s_tbl, lane_const);
+    stream_items<2, 4, false, false>(n_items, nsq, next_item, finish, hook, slow_code, s_tbl, lane_const, (gq_t)gate);
   else if (bc)
-    stream_items<2, 6, true, true>(n_items, nsq, next_item, finish, hook, slow_code, s_tbl, lane_const);
+    stream_items<2, 6, true, true>(n_items, nsq, next_item, finish, hook, slow_code, s_tbl, lane_const, (gq_t)gate);
   else
-    stream_items<2, 4, true, false>(n_items, nsq, next_item, finish, hook, slow_code, s_tbl, lane_const);
+    stream_items<2, 4, true, false>(n_items, nsq, next_item, finish, hook, slow_code, s_tbl, lane_const, (gq_t)gate);
 }
 
 __global__ void __launch_bounds__(kDecThreads, 1)
@@ -1112,7 +1124,8 @@ decode_down_kernel(const ExpertTable tab, const DecodeRoute *__restrict__ route,
     };
     const uint32_t lane_const2[2] = {(uint32_t)lane << 2, (uint32_t)lane << 2};
     stream_aligned<2, 4, 4, true, false, kLookahead>(grab, set_ptrs2, finish2, hook, s_tbl,
-                                                     lane_const2, row_blocks, s_aslot[wave], (gx_t)nullptr);
+                                                     lane_const2, row_blocks, s_aslot[wave], (gx_t)nullptr,
+                                                     (gq_t)h);
   } else {
     // Each wave takes a contiguous part of the units.
     const int i0 = wave * n_units / kDecWaves;
@@ -1126,13 +1139,13 @@ decode_down_kernel(const ExpertTable tab, const DecodeRoute *__restrict__ route,
       return s_rt.code2[unit_fields(ci, tl, kp)];
     };
     if (!slow && bc)
-      stream_items<1, 8, false, true>(n_items, nsq, next_item, finish, hook, slow_code, s_tbl, lane_const);
+      stream_items<1, 8, false, true>(n_items, nsq, next_item, finish, hook, slow_code, s_tbl, lane_const, (gq_t)h);
     else if (!slow)
-      stream_items<1, 8, false, false>(n_items, nsq, next_item, finish, hook, slow_code, s_tbl, lane_const);
+      stream_items<1, 8, false, false>(n_items, nsq, next_item, finish, hook, slow_code, s_tbl, lane_const, (gq_t)h);
     else if (bc)
-      stream_items<1, 8, true, true>(n_items, nsq, next_item, finish, hook, slow_code, s_tbl, lane_const);
+      stream_items<1, 8, true, true>(n_items, nsq, next_item, finish, hook, slow_code, s_tbl, lane_const, (gq_t)h);
     else
-      stream_items<1, 8, true, false>(n_items, nsq, next_item, finish, hook, slow_code, s_tbl, lane_const);
+      stream_items<1, 8, true, false>(n_items, nsq, next_item, finish, hook, slow_code, s_tbl, lane_const, (gq_t)h);
   }
   __syncthreads();
 

@@ -73,11 +73,15 @@ __device__ __forceinline__ void stream_tiles(const moe_nf4_expert_t &ex, const u
   const size_t tile_bytes = 4 * row_bytes;
   const size_t tile_blocks = 4 * row_blocks;
 
+  // Past the last stage the (unused) prefetches read the lane's activations, which stay in
+  // L2, instead of weight lines that the non-temporal loads have let go.
+  bool past = false;
   auto load = [&](Stage4<NP, BC> &st, int t, int sg) {
+    const uint8_t *dummy = reinterpret_cast<const uint8_t *>(ap + sg * kStageVals);
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
-      st.q[p] = ld_stream16(wq[p] + t * tile_bytes + sg * 256);
-      st.s[p] = wa[p][t * tile_blocks + sg * 8];
+      st.q[p] = ld_stream16(past ? dummy : wq[p] + t * tile_bytes + sg * 256);
+      st.s[p] = past ? *reinterpret_cast<const float *>(dummy) : wa[p][t * tile_blocks + sg * 8];
     }
     const uint4 *px = reinterpret_cast<const uint4 *>(ap + sg * kStageVals);
 #pragma unroll
@@ -140,6 +144,7 @@ __device__ __forceinline__ void stream_tiles(const moe_nf4_expert_t &ex, const u
     if (lt == ntiles) {
       lt = ntiles - 1;
       ls = NS - 1;
+      past = true;
     }
   };
   // The scheduling barriers keep the prologue's loads in stage order.  Left free, the
