@@ -197,10 +197,12 @@ int moe_layer_forward_nf4_profiled(const moe_nf4_expert_t *experts, int32_t E,
  * serving loops, harnesses that forbid hipMalloc).  Same kernels and results as
  * moe_layer_forward_nf4; the workspace is the library's static per-device scratch of
  * MOE_NOALLOC_SCRATCH_BYTES (each device holds it until the process ends), and the call
- * allocates nothing.  Layers whose workspace (moe_layer_workspace_bytes) exceeds the
- * scratch are refused with MOE_STATUS_INVALID_ARGUMENT (Mixtral-8x7B shape: T <= 744 at
- * k = 2).  Every call on a device shares that device's scratch: calls that overlap on one
- * device (two streams, two threads) race. */
+ * allocates nothing.  A layer whose workspace (moe_layer_workspace_bytes) exceeds the
+ * scratch runs with one down-projection ypart plane instead of K splits when that fits
+ * (same routing; outputs within fp32 summation order); larger layers are refused with
+ * MOE_STATUS_INVALID_ARGUMENT (Mixtral-8x7B shape: T <= 744 at k = 2).  Every call on a
+ * device shares that device's scratch: calls that overlap on one device (two streams, two
+ * threads) race. */
 #define MOE_NOALLOC_SCRATCH_BYTES (64ll << 20)
 int moe_layer_forward_nf4_noalloc(const moe_nf4_expert_t *experts, int32_t E,
                                   const void *gate_bf16, const void *bias_f32,

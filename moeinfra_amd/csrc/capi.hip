@@ -61,10 +61,11 @@ struct LayerWs {
   int nsplit;
 };
 
-LayerWs layer_ws(int64_t T, int32_t k, int32_t E, int32_t H, int32_t F) {
+// nsplit_override > 0 replaces the default number of down-projection ypart planes.
+LayerWs layer_ws(int64_t T, int32_t k, int32_t E, int32_t H, int32_t F, int nsplit_override = 0) {
   LayerWs w{};
   const int64_t rows = T * k;
-  w.nsplit = choose_nsplit(T, k, E, H, F);
+  w.nsplit = nsplit_override > 0 ? nsplit_override : choose_nsplit(T, k, E, H, F);
   int64_t o = 0;
   w.idx32 = o;    o = align_up(o + rows * 4);
   w.counts = o;   o = align_up(o + (int64_t)E * 4);
@@ -150,11 +151,12 @@ namespace {
 int layer_forward(const moe_nf4_expert_t *experts, int32_t E, const void *gate_bf16,
                   const void *bias_f32, const void *x_bf16, int64_t T, int32_t H, int32_t F,
                   int32_t k, void *out_bf16, void *logits_bf16, void *weights_f32, void *idx_i64,
-                  void *workspace, int64_t workspace_bytes, hipStream_t s, hipEvent_t *ev) {
+                  void *workspace, int64_t workspace_bytes, hipStream_t s, hipEvent_t *ev,
+                  int nsplit_override = 0) {
   MOE_REQUIRE(T >= 0 && k >= 1 && E >= 1 && H >= 1 && F >= 1, "bad sizes");
   if (T == 0) return MOE_STATUS_OK;
   MOE_REQUIRE(out_bf16 && weights_f32 && idx_i64, "null output pointer");
-  const LayerWs w = layer_ws(T, k, E, H, F);
+  const LayerWs w = layer_ws(T, k, E, H, F, nsplit_override);
   MOE_REQUIRE(workspace != nullptr && workspace_bytes >= w.total,
               "workspace too small: need %lld bytes, got %lld", (long long)w.total,
               (long long)workspace_bytes);
@@ -367,7 +369,14 @@ extern "C" int moe_layer_forward_nf4_noalloc(const moe_nf4_expert_t *experts, in
                                              void *idx_i64, void *stream) {
   MOE_REQUIRE(T >= 0 && k >= 1 && E >= 1 && H >= 1 && F >= 1, "bad sizes");
   if (T == 0) return MOE_STATUS_OK;
-  const int64_t need = moe::layer_ws(T, k, E, H, F).total;
+  // When the default layout (down-projection K splits over several ypart planes) does not
+  // fit the scratch, one plane: the same results, fewer workgroups on the down projection.
+  int nsplit = 0;
+  int64_t need = moe::layer_ws(T, k, E, H, F).total;
+  if (need > MOE_NOALLOC_SCRATCH_BYTES) {
+    nsplit = 1;
+    need = moe::layer_ws(T, k, E, H, F, 1).total;
+  }
   MOE_REQUIRE(need <= MOE_NOALLOC_SCRATCH_BYTES,
               "layer needs %lld bytes of workspace, above the %lld-byte static scratch; call "
               "moe_layer_forward_nf4 with a workspace",
@@ -377,5 +386,5 @@ extern "C" int moe_layer_forward_nf4_noalloc(const moe_nf4_expert_t *experts, in
   if (rc != MOE_STATUS_OK) return rc;
   return moe::layer_forward(experts, E, gate_bf16, bias_f32, x_bf16, T, H, F, k, out_bf16,
                             logits_bf16, weights_f32, idx_i64, ws, MOE_NOALLOC_SCRATCH_BYTES,
-                            (hipStream_t)stream, nullptr);
+                            (hipStream_t)stream, nullptr, nsplit);
 }

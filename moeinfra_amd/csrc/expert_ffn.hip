@@ -431,8 +431,12 @@ int token_tiles_for(int64_t max_tokens_per_expert) { return max_tokens_per_exper
 
 bool gemv4_supported(int64_t max_tokens_per_expert, int32_t H, int32_t F);
 bool expert_gemm_supported(int32_t H, int32_t F);
-int launch_expert_gemm(const void *tab, const void *x, int32_t H, int32_t F, const void *route,
-                       void *h_ws, void *ypart, int phases, hipStream_t stream);
+bool expert_gemm_splits_ok(int32_t F, int32_t nsplit);
+bool expert_gemm_rows_ok(int64_t T, int64_t rows_total, int32_t H, int32_t F);
+int expert_gemm_splits(int64_t rows, int64_t active, int32_t H, int32_t F);
+int launch_expert_gemm(const void *tab, const void *x, int64_t T, int64_t rows_total,
+                       int64_t active_max, int32_t H, int32_t F, const void *route, void *h_ws,
+                       void *ypart, int32_t nsplit, int phases, hipStream_t stream);
 // Average routed rows per expert from which a layer uses the batched GEMM.
 constexpr int64_t kGemmMinRowsPerExpert = 32;
 
@@ -458,7 +462,9 @@ int choose_nsplit(int64_t T, int32_t k, int32_t E, int32_t H, int32_t F) {
   const int64_t rows = T * k;
   const int64_t active_max = rows < E ? rows : E;
   if (T <= 0 || gemv4_supported(T, H, F)) return 1;
-  if (rows >= kGemmMinRowsPerExpert * active_max && expert_gemm_supported(H, F)) return 1;
+  if (rows >= kGemmMinRowsPerExpert * active_max && expert_gemm_supported(H, F) &&
+      expert_gemm_rows_ok(T, rows, H, F))
+    return expert_gemm_splits(rows, active_max, H, F);
   if (!midbatch_supported(H, F, 1) || !midbatch_rows_ok(T, rows, H, F)) return 1;
   return midbatch_splits(active_max, H, F);
 }
@@ -504,9 +510,11 @@ int launch_expert_ffn(const moe_nf4_expert_t *experts, int32_t E, const void *x,
                         stream);
   // Many tokens per expert on average: the LDS-staged GEMM streams each weight tile once per
   // 128 tokens (the per-tile kernels below re-stream it every 16 or 32 tokens).
-  if (nsplit == 1 && fused == nullptr && rows_total >= kGemmMinRowsPerExpert * active_max &&
-      expert_gemm_supported(H, F))
-    return launch_expert_gemm(&tab, x, H, F, &rt, h_ws, ypart, phases, stream);
+  if (fused == nullptr && rows_total >= kGemmMinRowsPerExpert * active_max &&
+      expert_gemm_supported(H, F) && expert_gemm_splits_ok(F, nsplit) &&
+      expert_gemm_rows_ok(T, rows_total, H, F))
+    return launch_expert_gemm(&tab, x, T, rows_total, active_max, H, F, &rt, h_ws, ypart, nsplit,
+                              phases, stream);
   // Fewer: the mid-batch kernels stream each weight tile once per 32 tokens of its expert
   // (32x32x16 MFMA, 16-byte weight loads): the streamed form (whole-K waves, activations
   // through LDS, `nsplit` K splits of the down projection) where the shape allows, else the

@@ -1,98 +1,188 @@
-// K4 for batches: grouped NF4 GEMM on the 16x16x32 bf16 MFMA with the activations staged
+// K4 for batches: grouped NF4 GEMM on the 32x32x16 bf16 MFMA with the activations staged
 // in LDS, for many tokens per expert (prefill).
 //
 //   gate/up:  h[off_e + r][f] = bf16(bf16(silu(bf16(w1_e x_t))) * bf16(w3_e x_t))[f]
-//   down:     ypart[off_e + r][c] = sum_f w2_e[c][f] * h[off_e + r][f]        (fp32)
+//   down:     ypart[s][off_e + r][c] = sum_{f in K split s} w2_e[c][f] * h[off_e + r][f]   (fp32)
 // for the rows r of every active expert e (token t = perm_tok[off_e + r]), the semantics of
 // ReconstructedNF4Expert.forward (transfer/nf4_reconstruct.py:152-155) applied to the rows
 // model/moe_layer.py:174-186 gathers.
 //
-// Tiling.  A workgroup item is (active expert, 128-row token tile, weight tile): 8 waves,
-// each owning 16 weight rows of NP = 2 B streams (gate/up: w1 and w3 rows; down: two
-// 16-row tiles of w2, 128 rows apart), for all 128 tokens of the tile (eight 16-token
-// MFMA tiles).  The K loop runs over 64-value NF4 blocks:
-//  * the token tile's 128 x 64 activations are loaded cooperatively (one 16-byte load per
-//    thread and half block), two blocks ahead, and staged in LDS (double buffer, 128-byte
-//    rows whose 16-byte chunks are XOR-swizzled by the row, see a_swizzle);
-//  * each lane's 8 packed bytes per stream and block come from a register ring 8 blocks
-//    deep (the HBM latency), and are turned into bf16 operands by the 64 KB LDS table;
-//  * per 16-token tile and stream, two MFMAs (K = 32 each) produce the block's partial
-//    product, scaled by the row's absmax into the fp32 accumulator.
-// The K order inside a block is the one of the per-expert kernels (expert_ffn.hip): lane
-// (n, g) holds values 16g..16g+7 for the first MFMA and 16g+8..16g+15 for the second, for
-// the weights (B, column n) and the activations (A, row n) alike.
+// Work.  An item is (active expert, weight tile, K split, token tile), the token tile
+// fastest: the items that share a weight tile are consecutive, and the persistent
+// workgroups take them XCD by XCD (workgroup b runs on XCD b % 8, so b is renumbered to keep
+// consecutive items on one XCD and its L2).  An item is 16 MFMAs per K step over all its
+// waves' weight fragments (32 weight rows each) and token tiles (32 tokens each):
+//  * large batches (>= 512 routed rows per expert): 256 tokens x 8 fragments, four waves
+//    (one per SIMD) of 2 fragments x 8 token tiles;
+//  * otherwise: 128 tokens x 16 fragments, eight waves (two per SIMD) of 2 fragments x 4
+//    token tiles.
+// Gate/up fragments pair w1 and w3 rows; down fragments are w2 row tiles.  Every lane holds
+// 16 fp32 sums per (fragment, token tile).
+//
+// Weights. The B operand of the MFMA is the weight exactly as the reference materializes it
+// before its matmul, bf16(code[nibble] * absmax) with an fp32 product (bitsandbytes'
+// dequantize_4bit inside the Linear4bit built at transfer/nf4_reconstruct.py:57-114, which
+// dequantizes the whole weight for more than one token): a 64 KB LDS table maps a packed byte
+// to its two fp32 code values (ds_read_b64), the lane multiplies them by its row's block
+// absmax and rounds to bf16. Lane l = 32 kg + i of fragment f holds row i of the fragment; per
+// NF4 block it loads the 16 packed bytes 16 kg .. 16 kg + 15 of its row (values 32 kg .. 32 kg
+// + 31), four 8-value K slices, one per MFMA step q.
+//
+// Activations.  The item's tokens x 64 bf16 tile of each block goes through LDS (128-byte
+// rows, 16-byte pieces XOR-swizzled by the row); the A operand of step q for token row m is
+// piece 4 kg + q of the row, the K slice the weight lanes hold.  The tiles arrive by LDS DMA
+// (buffer loads into LDS: rows past the expert's count read zeros), two blocks ahead into
+// three planes or, for 256-token tiles, one block ahead into two; the workgroup meets at one
+// LDS-only barrier per block, which leaves the weight loads in flight.
 #include "nf4_tile.h"
 
 namespace moe {
 namespace {
 
-constexpr int kGemmWaves = 8;
-constexpr int kGemmThreads = kGemmWaves * kWave;
-constexpr int kGemmM = 128;             // tokens per item
-constexpr int kGemmMT = kGemmM / 16;    // 16-token MFMA tiles per item
-constexpr int kARowHalves = 64;         // LDS row stride of the activation tile, in bf16
-constexpr int kGemmBDepth = 8;          // weight blocks in flight per wave
-constexpr int kGemmADepth = 4;          // activation blocks in flight per thread
-// The block loop is unrolled by kGemmBDepth from block 0, so b % kGemmADepth and b % 2 are
-// those of the unrolled index: the activation registers and LDS buffers are then indexed
-// statically (a dynamic index would make the compiler move the register array to LDS).
-// Loads complete in issue order (vmcnt), so the wait for the activations of block b + 1
-// also waits for every weight load issued before them: kGemmADepth - 1 blocks is the
-// latency the loads of both operands get.
-static_assert(kGemmBDepth % kGemmADepth == 0 && kGemmADepth % 2 == 0,
-              "buffer indices must follow the unrolled index");
+constexpr int kGmBDepth = 4;                 // NF4 blocks in flight per wave (= loop unroll)
+constexpr int kPairWords = 256 * 32 * 2;     // code-pair table: 256 bytes x 32 replicas x 8 B
+constexpr uint32_t kGmOob = 0x80000000u;     // buffer offset past any accepted activation tensor
+// The block loop is unrolled by kGmBDepth from block 0 (K splits hold a multiple of 4
+// blocks), so ring slot b % kGmBDepth is static; the activation plane is a runtime LDS
+// offset.
+static_assert(kGmBDepth == 4, "ring slot and unroll");
 
-// Position of 16-byte chunk c (of 8) of activation-tile row r: c ^ a_swizzle(r & 15).
-// gfx950 serves a 64-lane ds_read_b128 16 lanes per cycle, in the lane groups
-// {0-3, 12-15, 20-27} and {4-11, 16-19, 28-31} (and the same + 32), over 64 four-byte
-// banks.  The MFMA operand read has lane (n, g) fetch chunk 2g (then 2g + 1) of row n; with
-// this swizzle the 16 lanes of every group cover 16 distinct (row parity, position) pairs,
-// i.e. all 64 banks once.  The cooperative stores (8 lanes per cycle, one row) stay
-// conflict-free for any swizzle.
-__device__ __forceinline__ int a_swizzle(int r) { return ((r >> 1) & 3) | (((r + 4) >> 1) & 4); }
+#define GM_GLOBAL __attribute__((address_space(1)))
+#define GM_LDS __attribute__((address_space(3)))
+typedef const GM_GLOBAL uint8_t *gm_gq_t;
+typedef const GM_GLOBAL float *gm_ga_t;
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
+typedef __attribute__((__vector_size__(2 * sizeof(float)))) float f32x2;
 
-template <bool GATEUP>
-__global__ void __launch_bounds__(kGemmThreads, 1)
-expert_gemm_kernel(const ExpertTable tab, const uint16_t *__restrict__ act, int H, int F,
-                   Route rt, uint16_t *__restrict__ h_out, float *__restrict__ y_out) {
-  __shared__ __attribute__((aligned(16))) uint32_t s_tbl[kTableWords];
-  __shared__ __attribute__((aligned(16))) uint16_t s_a[2][kGemmM * kARowHalves];
-  __shared__ uint32_t s_raw[32];
-  __shared__ float s_code[32];
-  __shared__ int s_ex[MOE_MAX_EXPERTS][4];  // per active expert: id, rows, row offset, first item
+// s_waitcnt immediate that waits until at most n (< 64) vector memory loads are outstanding
+// (gfx9 encoding: vmcnt[3:0] in bits 3:0, vmcnt[5:4] in bits 15:14; expcnt and lgkmcnt at
+// their maxima, i.e. not waited for).
+constexpr int gm_vmcnt(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+// LDS-only barrier: orders the workgroup's LDS accesses without waiting for the waves'
+// outstanding global loads (__syncthreads would wait for the whole weight ring).
+__device__ __forceinline__ void gm_lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Position of 16-byte piece p in activation row r.  gfx950 serves a 64-lane ds_read_b128 16
+// lanes per cycle, in the lane groups {0-3, 12-15, 20-27} and {4-11, 16-19, 28-31} (and the
+// same + 32); the lanes of one group read one piece index of 16 rows whose (r & 1,
+// (r >> 1) & 7) are distinct, so the swizzled positions cover all 64 banks once.
+__device__ __forceinline__ int gm_pos(int r, int p) { return p ^ ((r >> 1) & 7); }
+
+// Instruction order of one MFMA step of a wave with MT token tiles and NF fragments: 16
+// MFMAs of the previous step; NF x 4 v_perm and LDS table reads and MT A-operand reads of
+// this step; 12 NF VALU turning the table entries into bf16 weights.  The LDS reads go out
+// between the first MFMAs, and the conversions, which wait for them, run under the remaining
+// MFMAs instead of stalling in a row.
+template <int MT, int NF>
+__device__ __forceinline__ void gm_step_schedule() {
+  constexpr int kMfma = 0x008, kValu = 0x002, kDsRead = 0x100;
+  constexpr int kRest = MT * NF - 2 - NF - MT / 4;  // MFMAs under the conversions
+  static_assert(MT * NF == 16 && MT % 4 == 0 && kRest > 0, "step shape");
+  __builtin_amdgcn_sched_group_barrier(kMfma, 2, 0);
+#pragma unroll
+  for (int i = 0; i < NF; ++i) {
+    __builtin_amdgcn_sched_group_barrier(kValu, 4, 0);
+    __builtin_amdgcn_sched_group_barrier(kDsRead, 4, 0);
+    __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
+  }
+#pragma unroll
+  for (int i = 0; i < MT / 4; ++i) {
+    __builtin_amdgcn_sched_group_barrier(kDsRead, 4, 0);
+    __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
+  }
+#pragma unroll
+  for (int i = 0; i < kRest; ++i) {
+    __builtin_amdgcn_sched_group_barrier(kValu, (12 * NF + kRest - 1) / kRest, 0);
+    __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// Four packed bytes (values 2j, 2j+1 per byte) -> eight bf16 weights bf16(code * s).  The
+// table entry of byte v for replica rep sits at byte (v << 8) | (rep << 3): {code[v >> 4],
+// code[v & 15]}; `lc` is the lane's rep << 3.
+__device__ __forceinline__ bf16x8 gm_dequant(const uint32_t *tbl, uint32_t w, uint32_t lc, float s) {
+  uint32_t o[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t addr = __builtin_amdgcn_perm(w, lc, 0x0c0c0400u + (j << 8));
+    const f32x2 c = *reinterpret_cast<const f32x2 *>(reinterpret_cast<const char *>(tbl) + addr);
+    o[j] = pack_bf16x2(c[0] * s, c[1] * s);
+  }
+  return as_bf16x8(o[0], o[1], o[2], o[3]);
+}
+
+// The DMA's inline asm names M0, a register the compiler reserves and sets before each of
+// its own uses (this kernel has none besides the asm).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+// W waves per workgroup (one workgroup per CU) and MT 32-token tiles per item: W = 4,
+// MT = 4 (one wave per SIMD, 4 fragments each), W = 4, MT = 8 (one wave per SIMD, 2
+// fragments against 8 token tiles: half the dequantization and weight loads per MFMA), both
+// with the steps software-pipelined within the wave; or W = 8, MT = 4 (two waves per SIMD, 2
+// fragments each, the other wave covering a wave's stalls).
+template <bool GATEUP, int W, int MT>
+__global__ void __launch_bounds__(W * 64, 1)
+expert_gemm_kernel(const ExpertTable tab, const uint16_t *__restrict__ act, uint32_t act_bytes,
+                   int K, int NROWS, Route rt, int rows_total, int nsplit,
+                   uint16_t *__restrict__ h_out, float *__restrict__ y_out) {
+  constexpr int kGmThreads = W * kWave;
+  constexpr int kGmMT = MT;                            // 32-token MFMA tiles per item
+  constexpr int kGmM = 32 * MT;                        // tokens per item
+  constexpr int kGmPlane = kGmM * 128;                 // bytes of one block's activation tile
+  constexpr int kGmNF = 64 / MT / W;                   // fragments per wave (16 MFMAs a step)
+  // Activation planes: three (the DMA runs two blocks ahead) when they fit beside the 64 KB
+  // table, else two (one block ahead).
+  constexpr int kPlanes = MT == 8 ? 2 : 3;
+  constexpr int kLA = kPlanes - 1;
+  constexpr int kRT = GATEUP ? kGmNF / 2 : kGmNF;      // 32-row tiles per wave
+  constexpr int kRowsWave = 32 * kRT;                  // weight rows per wave
+  constexpr int kRowsItem = W * kRowsWave;             // weight rows per item
+  constexpr int kGmFill = kGmPlane / 16 / kGmThreads;  // 16-byte pieces per thread and block
+  constexpr bool kPipe = W == 4;
+  static_assert(((W == 4 && (MT == 4 || MT == 8)) || (W == 8 && MT == 4)) &&
+                    kGmFill * kGmThreads * 16 == kGmPlane,
+                "supported shapes");
+  // The activation planes at LDS offset 0 (the DMA's M0 base stays small), then the table.
+  __shared__ __attribute__((aligned(16))) uint8_t s_lds[kPlanes * kGmPlane + kPairWords * 4];
+  uint32_t *const s_pair = reinterpret_cast<uint32_t *>(s_lds + kPlanes * kGmPlane);
+  // Codebooks of every active expert: [0,16) w1 (down: w2), [16,32) w3 (down: w2).
+  __shared__ float s_codes[MOE_MAX_EXPERTS][32];
+  // Per active expert: id, rows, row offset, first item, token tiles.
+  __shared__ int s_ex[MOE_MAX_EXPERTS][5];
+  // Stream pointers of every active expert: gate/up w1, w3 packed, w1, w3 absmax; down w2
+  // packed, w2 absmax.
+  __shared__ const void *s_ptr[MOE_MAX_EXPERTS][4];
   __shared__ int s_nitems;
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
-  const int wave = tid >> 6;
-  const int n = lane & 15;
-  const int g = lane >> 4;
-  const int K = GATEUP ? H : F;                  // reduction length
-  const int NROWS = GATEUP ? F : H;              // weight rows (output columns)
-  const int NB = K >> 6;                         // NF4 blocks per weight row
-  const int WROWS = GATEUP ? 128 : 256;          // weight rows per item
-  const int n_tiles = NROWS / WROWS;
-  const uint32_t lc = (uint32_t)(lane & 31) << 2;
-  // gate/up: replicas 0-31 hold w1's codebook, 32-63 w3's; down: both w2's.
-  const uint32_t lane_const[2] = {lc, lc | 128u};
-  bool built = false;
-
-  // Items: for each active expert (ascending), its token tiles x weight tiles, the token
-  // tile fastest so that concurrent items share weight tiles in L2.  Wave 0 stages the
-  // active experts' ids, row counts, row offsets and first item indices in LDS once, so
-  // that decoding an item is one LDS read and a ballot instead of a chain of global loads.
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int li = lane & 31;
+  const int kg = lane >> 5;
+  const int NB = K >> 6;
+  const int NBp = NB / nsplit;            // blocks of one K split (a multiple of 4)
+  const int wtiles = NROWS / kRowsItem;
+  const uint32_t row_bytes = (uint32_t)(K >> 1);
   static_assert(MOE_MAX_EXPERTS <= kWave, "one lane per active expert");
+
   const int n_active = rt.active[0];
   if (n_active == 0) return;  // uniform over the grid, before any barrier
   if (wave == 0) {
-    int e = 0, cnt = 0, items = 0;
+    int e = 0, cnt = 0, items = 0, mtiles = 0;
     if (lane < n_active) {
       e = rt.active[1 + lane];
-      // An absent expert (all-null table entry) has no items.
+      // An absent expert (null pointers) gets no items; the caller routes no token to it.
       cnt = (GATEUP ? tab.e[e].w1_packed : tab.e[e].w2_packed) != nullptr ? rt.counts[e] : 0;
-      items = ((cnt + kGemmM - 1) / kGemmM) * n_tiles;
+      mtiles = (cnt + kGmM - 1) / kGmM;
+      items = mtiles * nsplit * wtiles;
     }
-    int incl = items;  // inclusive prefix sum over the lanes
+    int incl = items;
 #pragma unroll
     for (int o = 1; o < kWave; o <<= 1) {
       const int v = __shfl_up(incl, o);
@@ -103,217 +193,404 @@ expert_gemm_kernel(const ExpertTable tab, const uint16_t *__restrict__ act, int 
       s_ex[lane][1] = cnt;
       s_ex[lane][2] = rt.offsets[e];
       s_ex[lane][3] = incl - items;
+      s_ex[lane][4] = mtiles;
+      const moe_nf4_expert_t &ex = tab.e[e];
+      if constexpr (GATEUP) {
+        s_ptr[lane][0] = ex.w1_packed;
+        s_ptr[lane][1] = ex.w3_packed;
+        s_ptr[lane][2] = ex.w1_absmax;
+        s_ptr[lane][3] = ex.w3_absmax;
+      } else {
+        s_ptr[lane][0] = ex.w2_packed;
+        s_ptr[lane][1] = ex.w2_packed;
+        s_ptr[lane][2] = ex.w2_absmax;
+        s_ptr[lane][3] = ex.w2_absmax;
+      }
     }
     if (lane == kWave - 1) s_nitems = incl;
   }
-  // Codebooks: when every active expert holds the codebooks of the first one (the usual
-  // case: one NF4 codebook for all tensors), the table is built once for the launch;
-  // otherwise it is checked per item.
-  // The first present active expert supplies the reference codebooks; with none present
-  // there is no item (uniform over the grid, before any barrier).
-  int e0 = -1;
-  for (int a = 0; a < n_active && e0 < 0; ++a) {
-    const int e = rt.active[1 + a];
-    if ((GATEUP ? tab.e[e].w1_packed : tab.e[e].w2_packed) != nullptr) e0 = e;
+  for (int i = tid; i < n_active * 32; i += kGmThreads) {
+    const moe_nf4_expert_t &ex = tab.e[rt.active[1 + (i >> 5)]];
+    const int j = i & 15;
+    float c = 0.0f;
+    if ((GATEUP ? ex.w1_packed : ex.w2_packed) != nullptr) {
+      if (GATEUP)
+        c = ((const float *)((i & 16) ? ex.w3_code : ex.w1_code))[j];
+      else
+        c = ((const float *)ex.w2_code)[j];
+    }
+    s_codes[i >> 5][i & 31] = c;
   }
-  if (e0 < 0) return;
+  __syncthreads();
+  // One table for the launch when every present active expert holds the same codebooks
+  // (the usual case); otherwise the table is rebuilt where an item's expert changes.
   int cb_diff = 0;
   {
-    const float *lo0 = (const float *)(GATEUP ? tab.e[e0].w1_code : tab.e[e0].w2_code);
-    const float *hi0 = (const float *)(GATEUP ? tab.e[e0].w3_code : tab.e[e0].w2_code);
-    for (int i = tid; i < n_active * 32; i += kGemmThreads) {
-      const int e = rt.active[1 + (i >> 5)], j = i & 15;
-      if ((GATEUP ? tab.e[e].w1_packed : tab.e[e].w2_packed) == nullptr) continue;
-      const float *lo = (const float *)(GATEUP ? tab.e[e].w1_code : tab.e[e].w2_code);
-      const float *hi = (const float *)(GATEUP ? tab.e[e].w3_code : tab.e[e].w2_code);
-      const float *x = (i & 16) ? hi : lo;
-      const float *x0 = (i & 16) ? hi0 : lo0;
-      cb_diff |= __builtin_bit_cast(uint32_t, x[j]) != __builtin_bit_cast(uint32_t, x0[j]);
-    }
+    int a0 = 0;
+    while (a0 + 1 < n_active && s_ex[a0][1] == 0) ++a0;
+    for (int i = tid; i < n_active * 32; i += kGmThreads)
+      if (s_ex[i >> 5][1] > 0)
+        cb_diff |= __builtin_bit_cast(uint32_t, s_codes[i >> 5][i & 31]) !=
+                   __builtin_bit_cast(uint32_t, s_codes[a0][i & 31]);
   }
-  const bool per_item_table = __syncthreads_or(cb_diff) != 0;  // also publishes s_ex
-  if (!per_item_table) {
-    const moe_nf4_expert_t &ex0 = tab.e[e0];
-    if (GATEUP)
-      ensure_table<kGemmThreads>(s_tbl, s_raw, s_code, (const float *)ex0.w1_code, (const float *)ex0.w3_code, built);
-    else
-      ensure_table<kGemmThreads>(s_tbl, s_raw, s_code, (const float *)ex0.w2_code, (const float *)ex0.w2_code, built);
-  }
+  const bool per_item_table = __syncthreads_or(cb_diff) != 0;
   const int n_items = s_nitems;
+  const int G = (int)gridDim.x;
+  // Workgroups are dispatched to the 8 XCDs round-robin: renumber so that XCD x takes the
+  // consecutive items [x G/8, (x + 1) G/8) of every round.
+  const int vb = (G & 7) == 0 ? (int)(blockIdx.x & 7) * (G >> 3) + (int)(blockIdx.x >> 3)
+                              : (int)blockIdx.x;
+  if (vb >= n_items) return;  // uniform over the workgroup
 
-  for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
-    // The item's expert: the last active expert whose first item is <= item.
-    const int a = __popcll(__ballot(lane < n_active && s_ex[lane < n_active ? lane : 0][3] <= item)) - 1;
-    const int e = s_ex[a][0], cnt = s_ex[a][1], off = s_ex[a][2];
-    const int rem = item - s_ex[a][3];
-    const int mtiles = (cnt + kGemmM - 1) / kGemmM;
-    const int nt = rem / mtiles;
-    const int mt_i = rem - nt * mtiles;
-    const int m_base = mt_i * kGemmM;
-    const moe_nf4_expert_t &ex = tab.e[e];
-    if (per_item_table) {
-      if (GATEUP)
-        ensure_table<kGemmThreads>(s_tbl, s_raw, s_code, (const float *)ex.w1_code, (const float *)ex.w3_code, built);
-      else
-        ensure_table<kGemmThreads>(s_tbl, s_raw, s_code, (const float *)ex.w2_code, (const float *)ex.w2_code, built);
-    }
+  auto ex_field = [&](int a, int f) { return __builtin_amdgcn_readfirstlane(s_ex[a][f]); };
+  // Item -> (active index, weight tile, split, token tile); wave-uniform.
+  auto decode = [&](int item, int &a, int &wt, int &sp, int &mt) {
+    const int sel = lane < n_active ? lane : 0;
+    a = __popcll(__ballot(lane < n_active && s_ex[sel][3] <= item)) - 1;
+    int rem = item - ex_field(a, 3);
+    const int mtiles = ex_field(a, 4);
+    const int q = rem / mtiles;
+    mt = rem - q * mtiles;
+    wt = q / nsplit;
+    sp = q - wt * nsplit;
+  };
 
-    // Weight streams of this lane: row (row0 + n) of each stream.
-    const int row0 = nt * WROWS + 16 * wave;
-    const uint8_t *wq[2];
-    const float *wa[2];
-    if (GATEUP) {
-      const size_t r = (size_t)(row0 + n);
-      wq[0] = (const uint8_t *)ex.w1_packed + r * (K >> 1) + 8 * g;
-      wq[1] = (const uint8_t *)ex.w3_packed + r * (K >> 1) + 8 * g;
-      wa[0] = (const float *)ex.w1_absmax + r * NB;
-      wa[1] = (const float *)ex.w3_absmax + r * NB;
-    } else {
-      const size_t r0 = (size_t)(row0 + n), r1 = r0 + 128;
-      wq[0] = (const uint8_t *)ex.w2_packed + r0 * (K >> 1) + 8 * g;
-      wq[1] = (const uint8_t *)ex.w2_packed + r1 * (K >> 1) + 8 * g;
-      wa[0] = (const float *)ex.w2_absmax + r0 * NB;
-      wa[1] = (const float *)ex.w2_absmax + r1 * NB;
+  // Replica of the lane's table lookups per fragment: with one codebook in the table, lanes
+  // l and l + 32 take different replicas (every half-wave covers all 32); with two
+  // (gate/up, w1's differing from w3's), replicas 0-15 hold w1's and 16-31 w3's.
+  constexpr int kStreams = GATEUP ? 2 : 1;
+  uint32_t lc[kStreams];
+  int tbl_a = -1;
+  auto build_table = [&](int a) {
+    gm_lds_barrier();  // every wave is done with the previous table
+    for (int i = tid; i < 256 * 32; i += kGmThreads) {
+      const int v = i >> 5;
+      const float *c = s_codes[a] + ((i & 16) ? 16 : 0);
+      *reinterpret_cast<f32x2 *>(&s_pair[2 * i]) = f32x2{c[v >> 4], c[v & 15]};
     }
-    // Activation loads of this thread: token-tile rows ar0 and ar0 + 64, 16 bytes at
-    // half-block byte offset 16 * ac (one load per row and block).
-    const int ac = tid & 7;
-    const int ar0 = tid >> 3;  // 0..63
-    const uint16_t *asrc[2];
+    int two = 0;
+    if (GATEUP && lane < 16)
+      two = __builtin_bit_cast(uint32_t, s_codes[a][lane]) != __builtin_bit_cast(uint32_t, s_codes[a][16 + lane]);
+    two = __ballot(two) != 0;
 #pragma unroll
-    for (int h2 = 0; h2 < 2; ++h2) {
-      const int r = m_base + ar0 + 64 * h2;
-      const int rr = r < cnt ? r : cnt - 1;  // rows past the expert's last repeat it (unused)
-      const size_t src_row = GATEUP ? (size_t)rt.perm_tok[off + rr] : (size_t)(off + rr);
-      asrc[h2] = act + src_row * K + 8 * ac;
-    }
+    for (int p = 0; p < kStreams; ++p)
+      lc[p] = (two ? (uint32_t)((lane & 15) | (p << 4)) : (uint32_t)(li ^ (kg << 4))) << 3;
+    gm_lds_barrier();
+    tbl_a = a;
+  };
 
-    // Rows ar0 and ar0 + 64 share the swizzle (64 is a multiple of 16).
-    const int a_st = ar0 * kARowHalves + 8 * (ac ^ a_swizzle(ar0));
-    u32x4 abuf[kGemmADepth][2];
-    auto load_a = [&](u32x4 (&dst)[2], int b) {
-      const int bb = b < NB ? b : NB - 1;  // past the end: the last block again (unused)
+  const __amdgpu_buffer_rsrc_t rsrc =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(act), (short)0, (int)act_bytes, 0x00020000);
+
+  // Activation fill by LDS DMA: for piece set j, wave w writes rows 8 W j + 8 w .. + 7 of a
+  // plane with one 16-byte-per-lane buffer load; lane L lands at byte 16 L of the wave's
+  // 1 KB, i.e. row fr = 8 W j + 8 w + L / 8 at position L % 8, so it loads the piece that
+  // belongs there, gm_pos(fr, L % 8) (the swizzle is an involution; 8 W j leaves it alone).
+  const int fr = 8 * wave + (lane >> 3);
+  const uint32_t fsrc = 8u * (uint32_t)gm_pos(fr, lane & 7);
+  // Lane's A operand: token row li of each 32-token tile, piece 4 kg + q.
+  int a_lds[4];
 #pragma unroll
-      for (int h2 = 0; h2 < 2; ++h2)
-        dst[h2] = *reinterpret_cast<const u32x4 *>(asrc[h2] + (size_t)bb * 64);
+  for (int q = 0; q < 4; ++q) a_lds[q] = li * 128 + 16 * gm_pos(li, 4 * kg + q);
+  // Fragment f's rows: gate/up stream f & 1, rows 32 (f >> 1) + i of the wave's; down rows
+  // 32 f + i of the wave's.  Per block, 16 bytes at 32 b + 16 kg of the row; per group of 4
+  // blocks, the row's 4 absmax values (one 16-byte load: a 4-byte load per block would
+  // touch 32 rows' lines for 256 bytes).
+  const uint32_t w_lane = (uint32_t)li * row_bytes + 16u * kg;
+  const uint32_t s_lane = (uint32_t)li * (uint32_t)NB;
+  const GM_LDS uint8_t *const s_a0 = (const GM_LDS uint8_t *)s_lds;
+  const uint32_t s_a0_off = (uint32_t)(uintptr_t)s_a0;
+  const GM_LDS char *const tbl = (const GM_LDS char *)s_pair;
+
+  f32x16 acc[kGmMT][kGmNF];
+  u32x4 ring[kGmBDepth][kGmNF];
+  f32x4 absc[kGmNF], absn[kGmNF];  // absmax of the current and the next group of 4 blocks
+
+  for (int item = vb; item < n_items; item += G) {
+    int a, wt, sp, mt;
+    decode(item, a, wt, sp, mt);
+    if (tbl_a < 0 || (per_item_table && a != tbl_a)) build_table(a);
+    const int cnt = ex_field(a, 1), off = ex_field(a, 2);
+    const uint32_t row0 = (uint32_t)(wt * kRowsItem + wave * kRowsWave);
+    const uint32_t kb0 = (uint32_t)(sp * NBp);
+    auto uptr = [&](int f) {
+      const uint64_t v = (uint64_t)(uintptr_t)s_ptr[a][f];
+      const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+      const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32));
+      return (uint64_t)lo | ((uint64_t)hi << 32);
     };
-    auto store_a = [&](const u32x4 (&src)[2], int buf) {
+    gm_gq_t wb[kGmNF];
+    gm_ga_t ab[kGmNF];
 #pragma unroll
-      for (int h2 = 0; h2 < 2; ++h2)
-        *reinterpret_cast<u32x4 *>(&s_a[buf][a_st + 64 * h2 * kARowHalves]) = src[h2];
-    };
-    // Operand reads of lane (n, g): chunks 2g and 2g + 1 of row n (+ 16 m).
-    const int a_rd0 = n * kARowHalves + 8 * ((2 * g) ^ a_swizzle(n));
-    const int a_rd1 = n * kARowHalves + 8 * ((2 * g + 1) ^ a_swizzle(n));
-    uint2 bq[kGemmBDepth][2];
+    for (int f = 0; f < kGmNF; ++f) {
+      const int s = GATEUP ? (f & 1) : 0;
+      const uint32_t fr0 = row0 + 32u * (uint32_t)(GATEUP ? (f >> 1) : f);
+      wb[f] = (gm_gq_t)(uintptr_t)uptr(s) + (fr0 * row_bytes + kb0 * 32u);
+      ab[f] = (gm_ga_t)(uintptr_t)uptr(2 + s) + (fr0 * (uint32_t)NB + kb0);
+    }
+    uint32_t fo[kGmFill];
+#pragma unroll
+    for (int j = 0; j < kGmFill; ++j) {
+      const int r = mt * kGmM + fr + 8 * W * j;
+      uint32_t o = kGmOob;
+      if (r < cnt) {
+        const uint32_t arow = GATEUP ? (uint32_t)rt.perm_tok[off + r] : (uint32_t)(off + r);
+        o = (arow * (uint32_t)K + kb0 * 64u + fsrc) * 2u;
+      }
+      fo[j] = o;
+    }
+
+    // Weights of block b and absmax of blocks b4..b4+3 (past the split's end: its last
+    // block / group again, unused).
     auto load_b = [&](int slot, int b) {
-      const int bb = b < NB ? b : NB - 1;
+      const uint32_t bo = w_lane + (uint32_t)(b < NBp ? b : NBp - 1) * 32u;
 #pragma unroll
-      for (int p = 0; p < 2; ++p) bq[slot][p] = *reinterpret_cast<const uint2 *>(wq[p] + (size_t)bb * 32);
+      for (int f = 0; f < kGmNF; ++f) ring[slot][f] = *reinterpret_cast<const GM_GLOBAL u32x4 *>(wb[f] + bo);
     };
-    // Absmax of blocks 4j..4j+3 as one 16-byte load per stream (rows hold NB % 4 == 0
-    // values), two groups of four in registers: group j lives in slot j % 2.
-    f32x4 bs4[2][2];
-    auto load_s = [&](int slot, int b4) {
-      const int bb = b4 < NB ? b4 : NB - 4;
+    auto load_s = [&](f32x4 (&dst)[kGmNF], int b4) {
+      const uint32_t so = s_lane + (uint32_t)(b4 < NBp ? b4 : NBp - 4);
 #pragma unroll
-      for (int p = 0; p < 2; ++p) bs4[slot][p] = *reinterpret_cast<const f32x4 *>(wa[p] + bb);
+      for (int f = 0; f < kGmNF; ++f) dst[f] = *reinterpret_cast<const GM_GLOBAL f32x4 *>(ab[f] + so);
+    };
+    // Activations of block b into the plane at LDS byte `plane`: kGmFill VMEM instructions
+    // per thread.  Written as inline asm so that the compiler neither counts them nor makes
+    // LDS reads wait for them (it cannot tell the planes apart); the explicit vmcnt waits
+    // before the barriers count them.  M0 holds the wave's 1 KB destination.
+    auto dma = [&](uint32_t plane, int b) {
+      const uint32_t adv = (uint32_t)(b < NBp ? b : NBp - 1) * 128u;
+#pragma unroll
+      for (int j = 0; j < kGmFill; ++j) {
+        const uint32_t dst = plane + (uint32_t)(8 * W * j + 8 * wave) * 128u;
+        asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                     :
+                     : "s"(dst), "v"(fo[j] + adv), "s"(rsrc)
+                     : "m0");
+      }
+    };
+    // One MFMA step: the A operands of the four token tiles and the table entries of the
+    // four fragments' K slices (LDS), then the bf16 weights, then 16 MFMAs.
+    struct Pre {
+      u32x4 a[kGmMT];
+      f32x2 c[kGmNF][4];
+    };
+    auto issue = [&](Pre &P, const GM_LDS uint8_t *plane, const GM_LDS char *tb, int slot, int q) {
+#pragma unroll
+      for (int t = 0; t < kGmMT; ++t) P.a[t] = *reinterpret_cast<const GM_LDS u32x4 *>(plane + a_lds[q] + t * 32 * 128);
+#pragma unroll
+      for (int f = 0; f < kGmNF; ++f)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t addr = __builtin_amdgcn_perm(ring[slot][f][q], lc[GATEUP ? (f & 1) : 0], 0x0c0c0400u + (j << 8));
+          P.c[f][j] = *reinterpret_cast<const GM_LDS f32x2 *>(tb + addr);
+        }
+    };
+    auto convert = [&](const Pre &P, int slot, bf16x8 (&bv)[kGmNF]) {
+#pragma unroll
+      for (int f = 0; f < kGmNF; ++f) {
+        const float sc = absc[f][slot];
+        uint32_t o[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] = pack_bf16x2(P.c[f][j][0] * sc, P.c[f][j][1] * sc);
+        bv[f] = as_bf16x8(o[0], o[1], o[2], o[3]);
+      }
+    };
+    auto mfmas = [&](const Pre &P, const bf16x8 (&bv)[kGmNF]) {
+#pragma unroll
+      for (int t = 0; t < kGmMT; ++t)
+#pragma unroll
+        for (int f = 0; f < kGmNF; ++f)
+          acc[t][f] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(P.a[t]), bv[f], acc[t][f], 0, 0, 0);
     };
 
-    f32x4 acc[2][kGemmMT];
 #pragma unroll
-    for (int p = 0; p < 2; ++p)
+    for (int t = 0; t < kGmMT; ++t)
 #pragma unroll
-      for (int m = 0; m < kGemmMT; ++m) acc[p][m] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      for (int f = 0; f < kGmNF; ++f)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[t][f][v] = 0.0f;
+    // The step in flight: its operands, consumed one step later (zeros before block 0).
+    Pre pc;
+    bf16x8 bc[kGmNF];
+#pragma unroll
+    for (int t = 0; t < kGmMT; ++t) pc.a[t] = u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int f = 0; f < kGmNF; ++f) bc[f] = as_bf16x8(0u, 0u, 0u, 0u);
 
-    // Prologue: activation block 0 to LDS, blocks 1..DA-1 in registers, weight blocks
-    // 0..DB-2.
+    // Prologue: activations of blocks 0..kLA-1, weights of blocks 0..BDepth-2.  The previous
+    // item's reads of every plane ended before its last barrier.
 #pragma unroll
-    for (int d = 0; d < kGemmADepth; ++d) load_a(abuf[d], d);
+    for (int d = 0; d < kLA; ++d) dma(s_a0_off + d * kGmPlane, d);
 #pragma unroll
-    for (int d = 0; d < kGemmBDepth - 1; ++d) load_b(d, d);
-    load_s(0, 0);
-    load_s(1, 4);
-    store_a(abuf[0], 0);
-    __syncthreads();
+    for (int d = 0; d < kGmBDepth - 1; ++d) load_b(d, d);
+    load_s(absc, 0);
+    load_s(absn, 4);
+    // The prologue's activations landed (the weight loads issued after them may not).
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(gm_vmcnt(kGmNF * (kGmBDepth - 1)));
+    gm_lds_barrier();
 
-    for (int b0 = 0; b0 < NB; b0 += kGemmBDepth) {
+    // One block: the DMA of block b + kLA's activations into plane `dst`, block b + 3's
+    // weights, and block b's four MFMA steps from plane `src` and the table.
+    auto block = [&](uint32_t dst, const GM_LDS uint8_t *src, int d, int b) {
+      dma(dst, b + kLA);
+      load_b((d + kGmBDepth - 1) % kGmBDepth, b + kGmBDepth - 1);
+      if (d == 0 && b > 0) {  // group b / 4 starts: its absmax is the one loaded 4 blocks ago
 #pragma unroll
-      for (int d = 0; d < kGemmBDepth; ++d) {
-        const int b = b0 + d;
-        if (b < NB) {
-          load_b((d + kGemmBDepth - 1) % kGemmBDepth, b + kGemmBDepth - 1);
-          // Once the blocks of a group are done (block b = 4j + 4 starts), group j + 2
-          // replaces it: four blocks ahead of its first use.
-          if (d % 4 == 0 && b >= 4) load_s((d / 4 + 1) % 2, b + 4);
-          load_a(abuf[d % kGemmADepth], b + kGemmADepth);  // block b's were stored at b-1
-          const uint16_t *sa = s_a[d & 1];
-          bf16x8 w0[2], w1[2];
+        for (int f = 0; f < kGmNF; ++f) absc[f] = absn[f];
+        load_s(absn, b + 4);
+      }
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-          for (int p = 0; p < 2; ++p) {
-            uint32_t l[8];
-            lookup8(s_tbl, bq[d][p], lane_const[p], l);
-            w0[p] = as_bf16x8(l[0], l[1], l[2], l[3]);
-            w1[p] = as_bf16x8(l[4], l[5], l[6], l[7]);
-          }
+      for (int q = 0; q < 4; ++q) {
+        if constexpr (kPipe) {
+          Pre pn;
+          bf16x8 bn[kGmNF];
+          issue(pn, src, tbl, d, q);
+          mfmas(pc, bc);  // the previous step (for q = 0 the previous block's last)
+          convert(pn, d, bn);
+          pc = pn;
 #pragma unroll
-          for (int m = 0; m < kGemmMT; ++m) {
-            const bf16x8 a0 = as_bf16x8(*reinterpret_cast<const u32x4 *>(sa + m * 16 * kARowHalves + a_rd0));
-            const bf16x8 a1 = as_bf16x8(*reinterpret_cast<const u32x4 *>(sa + m * 16 * kARowHalves + a_rd1));
-#pragma unroll
-            for (int p = 0; p < 2; ++p) scale_acc(acc[p][m], mfma_block(a0, w0[p], a1, w1[p]), bs4[(d / 4) % 2][p][d % 4]);
-          }
-          // Block b+1's activations (loaded at block b+1-DA) to the other buffer.
-          store_a(abuf[(d + 1) % kGemmADepth], (d + 1) & 1);
-          __syncthreads();
+          for (int f = 0; f < kGmNF; ++f) bc[f] = bn[f];
+          gm_step_schedule<MT, kGmNF>();
+        } else {
+          Pre p;
+          bf16x8 bv[kGmNF];
+          issue(p, src, tbl, d, q);
+          convert(p, d, bv);
+          mfmas(p, bv);
         }
       }
+      // Block b + 1's activations (issued kLA - 1 blocks earlier) must have landed for every
+      // wave before the barrier.  Issued after them: with kLA = 2 every load of block b (block
+      // b + 2's activations, kGmFill; block b + 3's weights, kGmNF; at a group start kGmNF
+      // absmax loads); with kLA = 1 block b's weight and absmax loads (the DMA comes first,
+      // an asm statement the loads do not move across).  Waiting down to those counts covers
+      // any order the compiler gave the loads of a block.
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_waitcnt(gm_vmcnt((kLA - 1) * kGmFill + kGmNF));
+      gm_lds_barrier();
+    };
+    int pb = 0;  // plane of block b: b % kPlanes
+    for (int b0 = 0; b0 < NBp; b0 += kGmBDepth) {
+#pragma unroll
+      for (int d = 0; d < kGmBDepth; ++d) {
+        // Plane (b + kLA) % kPlanes = (b - 1) % kPlanes was last read in block b - 1, before
+        // the barrier.
+        const int pd = pb == 0 ? kPlanes - 1 : pb - 1;
+        block(s_a0_off + pd * kGmPlane, s_a0 + pb * kGmPlane, d, b0 + d);
+        pb = pb == kPlanes - 1 ? 0 : pb + 1;
+      }
     }
+    if constexpr (kPipe) mfmas(pc, bc);
 
-    // Epilogue: lane (n, g) holds rows 4g+i of each 16-token tile, column n of its streams.
+    // Lane l = 32 kg + i holds column i of each fragment for token rows
+    // 32 t + 8 (v >> 2) + 4 kg + (v & 3) of the item's tile.
 #pragma unroll
-    for (int m = 0; m < kGemmMT; ++m) {
+    for (int t = 0; t < kGmMT; ++t) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = m_base + m * 16 + 4 * g + i;
-        if (r < cnt) {
-          if (GATEUP) {
-            h_out[(size_t)(off + r) * F + row0 + n] = swiglu_bf16(acc[0][m][i], acc[1][m][i]);
+      for (int v = 0; v < 16; ++v) {
+        const int m = mt * kGmM + 32 * t + 8 * (v >> 2) + 4 * kg + (v & 3);
+        if (m < cnt) {
+          const size_t orow = (size_t)(off + m);
+          if constexpr (GATEUP) {
+#pragma unroll
+            for (int r2 = 0; r2 < kRT; ++r2)
+              h_out[orow * NROWS + row0 + 32 * r2 + li] = swiglu_bf16(acc[t][2 * r2][v], acc[t][2 * r2 + 1][v]);
           } else {
-            float *yrow = y_out + (size_t)(off + r) * H;
-            yrow[row0 + n] = acc[0][m][i];
-            yrow[row0 + 128 + n] = acc[1][m][i];
+            float *yrow = y_out + ((size_t)sp * rows_total + orow) * NROWS + row0 + li;
+#pragma unroll
+            for (int f = 0; f < kGmNF; ++f) yrow[32 * f] = acc[t][f][v];
           }
         }
       }
     }
   }
+  // The last item's DMAs past its end are still writing LDS: they must land before the
+  // workgroup's LDS is released.
+  __builtin_amdgcn_s_waitcnt(gm_vmcnt(0));
 }
+#pragma clang diagnostic pop
 
 }  // namespace
 
-// The batched form of K4: gate/up (phases bit 0) and/or down (bit 1) with the LDS-staged
-// GEMM.  Needs H % 256 == 0 (down tiles of 256 rows) and F % 256 == 0 (gate/up tiles of 128
-// rows; absmax rows of a multiple of 4 blocks); writes ypart as one split.
-bool expert_gemm_supported(int32_t H, int32_t F) { return H % 256 == 0 && F % 256 == 0; }
+// Kernel shape of a launch: 256-token items (W = 4, MT = 8) from 512 routed rows per active
+// expert on average, else 128-token items with two waves per SIMD (W = 8, MT = 4).
+struct GemmShape {
+  int waves, mt;
+};
+GemmShape gemm_shape(int64_t rows, int64_t active) {
+  return active > 0 && rows >= 512 * active ? GemmShape{4, 8} : GemmShape{8, 4};
+}
 
-int launch_expert_gemm(const void *tab_v, const void *x, int32_t H, int32_t F, const void *route_v,
-                       void *h_ws, void *ypart, int phases, hipStream_t stream) {
-  MOE_REQUIRE(expert_gemm_supported(H, F), "shape not supported by the batched expert GEMM");
-  const ExpertTable &tab = *static_cast<const ExpertTable *>(tab_v);
-  const Route &rt = *static_cast<const Route *>(route_v);
-  const dim3 grid((unsigned)device_cu_count()), blk(kGemmThreads);
+// The batched form of K4: gate/up (phases bit 0) and/or down (bit 1).  Gate/up items cover
+// 1024 / MT rows of F, down items 2048 / MT rows of H (at most 512); the down projection
+// splits K over `nsplit` ypart planes, each a whole number of 4-block absmax groups.
+bool expert_gemm_supported(int32_t H, int32_t F) { return H % 512 == 0 && F % 256 == 0; }
+
+bool expert_gemm_splits_ok(int32_t F, int32_t nsplit) {
+  const int nb = F / 64;
+  return nsplit >= 1 && nb % nsplit == 0 && (nb / nsplit) % 4 == 0;
+}
+
+// Activation tensors are addressed with 32-bit buffer offsets below kGmOob.
+bool expert_gemm_rows_ok(int64_t T, int64_t rows_total, int32_t H, int32_t F) {
+  return T * (int64_t)H * 2 < (int64_t)kGmOob && rows_total * (int64_t)F * 2 < (int64_t)kGmOob;
+}
+
+// Down-projection splits for a layer of `rows` routed rows over `active` experts: the
+// smallest power of two (up to kGmMaxSplits) that gives every CU kGmItemsPerCu items, when
+// the shape allows it.  Routed counts vary around the average, so an expert's last token
+// tile is often nearly empty but costs a whole item: several items per CU keep that from
+// setting the launch's length.
+#ifndef GM_ITEMS_PER_CU
+#define GM_ITEMS_PER_CU 4
+#endif
+#ifndef GM_MAX_SPLITS
+#define GM_MAX_SPLITS 8
+#endif
+int expert_gemm_splits(int64_t rows, int64_t active, int32_t H, int32_t F) {
+  const GemmShape g = gemm_shape(rows, active);
+  const int64_t per = active > 0 ? (rows + active - 1) / active : 0;
+  const int64_t m = 32 * g.mt, rows_item = 2048 / g.mt;
+  const int64_t items = active * ((per + m - 1) / m) * (H / rows_item);
+  const int64_t want = GM_ITEMS_PER_CU * (int64_t)device_cu_count();
+  int s = 1;
+  while (s < GM_MAX_SPLITS && items * s < want && expert_gemm_splits_ok(F, 2 * s)) s *= 2;
+  return s;
+}
+
+template <int W, int MT>
+static int launch_gemm_shape(const ExpertTable &tab, const void *x, int64_t T, int64_t rows_total,
+                             int32_t H, int32_t F, const Route &rt, void *h_ws, void *ypart,
+                             int32_t nsplit, int phases, hipStream_t stream) {
+  const dim3 grid((unsigned)device_cu_count()), blk(W * kWave);
   if (phases & 1) {
-    hipLaunchKernelGGL(expert_gemm_kernel<true>, grid, blk, 0, stream, tab, (const uint16_t *)x, H,
-                       F, rt, (uint16_t *)h_ws, (float *)nullptr);
+    hipLaunchKernelGGL((expert_gemm_kernel<true, W, MT>), grid, blk, 0, stream, tab,
+                       (const uint16_t *)x, (uint32_t)(T * H * 2), H, F, rt, (int)rows_total, 1,
+                       (uint16_t *)h_ws, (float *)nullptr);
     MOE_LAUNCH_CHECK();
   }
   if (phases & 2) {
-    hipLaunchKernelGGL(expert_gemm_kernel<false>, grid, blk, 0, stream, tab, (const uint16_t *)h_ws,
-                       H, F, rt, (uint16_t *)nullptr, (float *)ypart);
+    hipLaunchKernelGGL((expert_gemm_kernel<false, W, MT>), grid, blk, 0, stream, tab,
+                       (const uint16_t *)h_ws, (uint32_t)(rows_total * F * 2), F, H, rt,
+                       (int)rows_total, nsplit, (uint16_t *)nullptr, (float *)ypart);
     MOE_LAUNCH_CHECK();
   }
   return MOE_STATUS_OK;
+}
+
+int launch_expert_gemm(const void *tab_v, const void *x, int64_t T, int64_t rows_total,
+                       int64_t active_max, int32_t H, int32_t F, const void *route_v, void *h_ws,
+                       void *ypart, int32_t nsplit, int phases, hipStream_t stream) {
+  MOE_REQUIRE(expert_gemm_supported(H, F), "shape not supported by the batched expert GEMM");
+  MOE_REQUIRE(expert_gemm_splits_ok(F, nsplit), "K split count not supported by the batched expert GEMM");
+  MOE_REQUIRE(expert_gemm_rows_ok(T, rows_total, H, F), "activations too large for the batched expert GEMM");
+  const ExpertTable &tab = *static_cast<const ExpertTable *>(tab_v);
+  const Route &rt = *static_cast<const Route *>(route_v);
+  const GemmShape g = gemm_shape(rows_total, active_max);
+  if (g.mt == 8)
+    return launch_gemm_shape<4, 8>(tab, x, T, rows_total, H, F, rt, h_ws, ypart, nsplit, phases, stream);
+  return launch_gemm_shape<8, 4>(tab, x, T, rows_total, H, F, rt, h_ws, ypart, nsplit, phases, stream);
 }
 
 }  // namespace moe

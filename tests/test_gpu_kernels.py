@@ -265,7 +265,10 @@ def test_decode_single_token_long_ffn(cuda_device):
 # per expert.
 @pytest.mark.parametrize("H,F,E,T,seed,skew", [
     (512, 1024, 8, 160, 31, False),
-    (256, 512, 8, 300, 32, True),
+    (256, 512, 8, 300, 32, True),     # H % 512 != 0: the per-tile kernels
+    (512, 768, 8, 300, 35, True),
+    (512, 1024, 4, 1100, 36, False),  # >= 512 rows per expert: 256-token items, K splits
+    (512, 768, 8, 2500, 37, True),    # skewed: 128- and 256-token tiles, partial tiles
     (1024, 3584, 8, 512, 33, False),
     (1024, 3584, 8, 700, 34, True),
 ])
@@ -281,7 +284,8 @@ def test_layer_batched_gemm(cuda_device, H, F, E, T, seed, skew):
 # Batched layers whose experts do not share one codebook: the GEMM rebuilds its lookup
 # table per work item.  Expert 0 keeps the NF4 codebook, so the first active expert's
 # table is not the one of every item.
-@pytest.mark.parametrize("H,F,T", [(512, 1024, 300), (256, 512, 160)])
+@pytest.mark.parametrize("H,F,T", [(512, 1024, 300), (256, 512, 160), (512, 768, 160),
+                                   (512, 768, 2100)])  # >= 512 rows per expert: 256-token items
 def test_layer_batched_gemm_mixed_codebooks(cuda_device, H, F, T):
     codes = {e: (orc.NF4_CODE * np.float32(0.75 + 0.05 * e)).astype(np.float32)
              for e in (1, 4, 6)}

@@ -1,8 +1,10 @@
 """The allocation-free layer entry point (moe_layer_forward_nf4_noalloc), called through the
 C ABI, against moe_layer_forward_nf4 with a caller workspace: bit-identical outputs on
 consecutive calls that shrink (mid-batch T = 40, fused small-batch routing T = 16, decode
-form T = 3), so the static scratch's leftovers from a larger call change nothing; layers
-whose workspace exceeds the scratch are refused before any launch."""
+form T = 3), so the static scratch's leftovers from a larger call change nothing; a batched
+layer whose K-split workspace exceeds the scratch runs with one down-projection plane (same
+routing, outputs within fp32 summation order); layers that exceed it even so are refused
+before any launch."""
 from __future__ import annotations
 
 import numpy as np
@@ -75,14 +77,38 @@ def test_noalloc_layer_matches_workspace_layer(cuda_device):
             np.testing.assert_array_equal(a, b)
 
 
+def test_noalloc_batched_layer_falls_back_to_one_plane(cuda_device):
+    from moeinfra_amd import _lib
+
+    lib = _lib.lib()
+    H, F, E, k, T = 1024, 3584, 8, 2, 2200
+    # The default layout (down-projection K splits) does not fit the scratch here.
+    assert lib.moe_layer_workspace_bytes(T, k, E, H, F) > _lib.MOE_NOALLOC_SCRATCH_BYTES
+    _keep, table, gate = _experts(cuda_device, H, F, E, seed=920)
+    g = torch.Generator(device=cuda_device).manual_seed(921)
+    x = torch.randn((T, H), generator=g, device=cuda_device).to(torch.bfloat16)
+    print(f"noalloc batched layer T={T}", flush=True)
+    got = _run(lib, table, E, gate, None, x, F, k, noalloc=True)
+    want = _run(lib, table, E, gate, None, x, F, k, noalloc=False)
+    for a, b in zip(got[1:], want[1:]):  # logits, weights, ids: the same kernels
+        np.testing.assert_array_equal(a, b)
+    # The outputs add the down projection's K splits in another order (fp32): rel-L2 bound.
+    from oracle import moe_oracle as orc
+    assert orc.rel_l2(orc.bf16_to_f32(got[0]), orc.bf16_to_f32(want[0])) <= 1e-3
+
+
 def test_noalloc_refuses_a_layer_above_the_scratch():
     from moeinfra_amd import _lib
 
     lib = _lib.lib()
     H, F, E, k = 4096, 14336, 8, 2
-    assert lib.moe_layer_workspace_bytes(744, k, E, H, F) <= _lib.MOE_NOALLOC_SCRATCH_BYTES
-    assert lib.moe_layer_workspace_bytes(745, k, E, H, F) > _lib.MOE_NOALLOC_SCRATCH_BYTES
-    # Null outputs as well: a refusal happens before any launch either way.
+    # Mixtral shape: the layer fits up to T = 744 (one down-projection plane above T = 210).
+    # With null outputs, T = 744 passes the size check and stops at the pointer check, T = 745
+    # is refused for its size; both before any launch.
+    rc = lib.moe_layer_forward_nf4_noalloc(None, E, None, None, None, 744, H, F, k, None, None,
+                                           None, None, None)
+    assert rc == _lib.MOE_STATUS_INVALID_ARGUMENT
+    assert "static scratch" not in lib.moe_last_error().decode()
     rc = lib.moe_layer_forward_nf4_noalloc(None, E, None, None, None, 745, H, F, k, None, None,
                                            None, None, None)
     assert rc == _lib.MOE_STATUS_INVALID_ARGUMENT
