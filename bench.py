@@ -203,7 +203,7 @@ def _moe_pass(lib, layers, xs, bias, T, H, F, E, K, steps, warmup, events=True, 
 
     L = len(layers)
     dev = xs[0].device
-    nsplit = ops.choose_nsplit(T, K, E, H)
+    nsplit = ops.choose_nsplit(T, K, E, H, F)
     ws_bytes = lib.moe_layer_workspace_bytes(T, K, E, H, F)
     ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=dev)
     outs = [torch.empty((T, H), dtype=torch.bfloat16, device=dev) for _ in range(L)]

@@ -174,6 +174,11 @@ int moe_expert_swiglu_nf4(const moe_nf4_expert_t *expert, const void *x_bf16, in
  * receive the routing.  workspace >= moe_layer_workspace_bytes(T, k, E, H, F), 256-byte
  * aligned. */
 int64_t moe_layer_workspace_bytes(int64_t T, int32_t k, int32_t E, int32_t H, int32_t F);
+/* Number of fp32 ypart planes (K splits of the down projection) the layer and the expert
+ * FFN use by default for this shape: what moe_expert_ffn_nf4 / moe_expert_down_nf4 callers
+ * pass as nsplit to run the layer's kernels (sizing helper, like the workspace query; the
+ * reference has no K splits).  -1 for invalid sizes. */
+int32_t moe_layer_down_splits(int64_t T, int32_t k, int32_t E, int32_t H, int32_t F);
 int moe_layer_forward_nf4(const moe_nf4_expert_t *experts, int32_t E, const void *gate_bf16,
                           const void *bias_f32, const void *x_bf16, int64_t T, int32_t H,
                           int32_t F, int32_t k, void *out_bf16, void *logits_bf16,

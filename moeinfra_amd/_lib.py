@@ -56,6 +56,7 @@ SIGNATURES = {
     "moe_expert_swiglu_nf4": ([ctypes.POINTER(MoeNf4Expert), _vp, _i64, _i32, _i32, _vp, _vp,
                                _i64, _vp], ctypes.c_int),
     "moe_layer_workspace_bytes": ([_i64, _i32, _i32, _i32, _i32], ctypes.c_int64),
+    "moe_layer_down_splits": ([_i64, _i32, _i32, _i32, _i32], ctypes.c_int32),
     "moe_layer_forward_nf4": ([ctypes.POINTER(MoeNf4Expert), _i32, _vp, _vp, _vp, _i64, _i32,
                                _i32, _i32, _vp, _vp, _vp, _vp, _vp, _i64, _vp], ctypes.c_int),
     "moe_layer_forward_nf4_noalloc": ([ctypes.POINTER(MoeNf4Expert), _i32, _vp, _vp, _vp, _i64,

@@ -141,6 +141,11 @@ extern "C" int64_t moe_layer_workspace_bytes(int64_t T, int32_t k, int32_t E, in
   return moe::layer_ws(T, k, E, H, F).total;
 }
 
+extern "C" int32_t moe_layer_down_splits(int64_t T, int32_t k, int32_t E, int32_t H, int32_t F) {
+  if (T < 0 || k < 1 || E < 1 || H < 1 || F < 1) return -1;
+  return moe::choose_nsplit(T, k, E, H, F);
+}
+
 namespace moe {
 namespace {
 // Decode batches (T <= 4, T*k <= 8, E <= 16) run the two-launch decode layer (routing in

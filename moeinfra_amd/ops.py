@@ -186,9 +186,13 @@ def expert_table(experts: Sequence[Optional[MoeNf4Expert]]):
     return arr
 
 
-def choose_nsplit(T: int, k: int, E: int, H: int) -> int:
-    """Mirror of the library's default number of cross-workgroup K splits (one)."""
-    return 1
+def choose_nsplit(T: int, k: int, E: int, H: int, F: int) -> int:
+    """The library's default number of down-projection K splits (ypart planes) for a layer
+    of T tokens, top-k k, E experts and hidden/FFN sizes H/F."""
+    n = lib().moe_layer_down_splits(T, k, E, H, F)
+    if n < 1:
+        raise ValueError(f"invalid layer sizes T={T} k={k} E={E} H={H} F={F}")
+    return n
 
 
 def expert_ffn(table, num_experts: int, x: torch.Tensor, k: int, hidden: int, inter: int,
@@ -198,7 +202,7 @@ def expert_ffn(table, num_experts: int, x: torch.Tensor, k: int, hidden: int, in
     _require(x, "hidden_states", torch.bfloat16, dev)
     T = x.shape[0]
     if nsplit is None:
-        nsplit = choose_nsplit(T, k, num_experts, hidden)
+        nsplit = choose_nsplit(T, k, num_experts, hidden, inter)
     h = torch.empty((T * k, inter), dtype=torch.bfloat16, device=dev)
     ypart = torch.empty((nsplit, T * k, hidden), dtype=torch.float32, device=dev)
     check(lib().moe_expert_ffn_nf4(table, num_experts, x.data_ptr(), T, k, hidden, inter,
