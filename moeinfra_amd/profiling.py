@@ -1,0 +1,117 @@
+"""Kernel tables from a rocprofv3 kernel-trace database (the SQLite file that
+``rocprofv3 --kernel-trace -d DIR -o NAME -- python3 bench.py ...`` writes as
+``DIR/.../NAME_results.db``).
+
+``python -m moeinfra_amd.profiling steps DB [N]`` prints the per-step kernel table of the
+last N decode steps of an end-to-end run (a step ends with ``argmax_finish_kernel``, the
+last launch of the captured decode step): wall time from the step's first kernel start to
+its last kernel end, busy time (sum of kernel durations), and per kernel and grid the
+launches, average duration and share of the busy time.
+
+``python -m moeinfra_amd.profiling kernels DB [SUBSTR]`` prints count / average / median /
+min duration per kernel and grid over the whole trace (optionally only names containing
+SUBSTR).
+
+Only the ``kernels`` view of the database is read (columns name, grid_x, start, end in
+nanoseconds).
+"""
+from __future__ import annotations
+
+import sqlite3
+import statistics as st
+import sys
+from typing import Dict, List, Sequence, Tuple
+
+Launch = Tuple[str, int, int, int]  # (name, grid_x, start ns, end ns)
+
+STEP_END_KERNEL = "argmax_finish_kernel"
+
+
+def short_name(name: str) -> str:
+    """Kernel name without the namespace, `void ` and the argument list."""
+    return name.replace("moe::(anonymous namespace)::", "").replace("void ", "").split("(")[0]
+
+
+def read_launches(db_path: str) -> List[Launch]:
+    con = sqlite3.connect(db_path)
+    try:
+        rows = con.execute("select name, grid_x, start, end from kernels order by start").fetchall()
+    finally:
+        con.close()
+    return [(str(n), int(g), int(a), int(b)) for n, g, a, b in rows]
+
+
+def split_steps(launches: Sequence[Launch], last: int | None = None) -> List[List[Launch]]:
+    """Launches grouped into decode steps: each step runs from the launch after one
+    argmax_finish_kernel to the next one, inclusive; the last `last` steps."""
+    ends = [i for i, r in enumerate(launches) if STEP_END_KERNEL in r[0]]
+    steps = [list(launches[a + 1:b + 1]) for a, b in zip(ends[:-1], ends[1:])]
+    return steps[-last:] if last else steps
+
+
+def step_table(steps: Sequence[Sequence[Launch]]) -> Tuple[Dict[str, float], List[Tuple[str, int, float, float, float, float]]]:
+    """(summary, rows): summary has wall/busy/idle microseconds per step and launches per
+    step; rows are (kernel, grid, launches per step, avg us, us per step, % of busy),
+    the heaviest first."""
+    if not steps:
+        raise ValueError(f"no complete decode step (no two {STEP_END_KERNEL} launches) in the trace")
+    walls = [s[-1][3] - s[0][2] for s in steps]
+    busy = [sum(b - a for _, _, a, b in s) for s in steps]
+    summary = {
+        "steps": float(len(steps)),
+        "wall_us": st.mean(walls) / 1e3,
+        "busy_us": st.mean(busy) / 1e3,
+        "idle_us": (st.mean(walls) - st.mean(busy)) / 1e3,
+        "launches": st.mean(len(s) for s in steps),
+    }
+    agg: Dict[Tuple[str, int], List[float]] = {}
+    for s in steps:
+        for n, g, a, b in s:
+            agg.setdefault((short_name(n), g), []).append((b - a) / 1e3)
+    rows = []
+    for (n, g), v in agg.items():
+        per_step = sum(v) / len(steps)
+        rows.append((n, g, len(v) / len(steps), st.mean(v), per_step, 100.0 * per_step / summary["busy_us"]))
+    rows.sort(key=lambda r: -r[4])
+    return summary, rows
+
+
+def kernel_table(launches: Sequence[Launch], substr: str = "") -> List[Tuple[str, int, int, float, float, float]]:
+    """(kernel, grid, count, avg us, median us, min us) per kernel and grid, the largest
+    total first."""
+    by: Dict[Tuple[str, int], List[float]] = {}
+    for n, g, a, b in launches:
+        if substr and substr not in n:
+            continue
+        by.setdefault((short_name(n), g), []).append((b - a) / 1e3)
+    rows = [(n, g, len(v), st.mean(v), st.median(v), min(v)) for (n, g), v in by.items()]
+    rows.sort(key=lambda r: -r[2] * r[3])
+    return rows
+
+
+def _main(argv: Sequence[str]) -> int:
+    if len(argv) < 2 or argv[0] not in ("steps", "kernels"):
+        print(__doc__)
+        return 2
+    launches = read_launches(argv[1])
+    if argv[0] == "steps":
+        last = int(argv[2]) if len(argv) > 2 else None
+        summary, rows = step_table(split_steps(launches, last))
+        print(f"steps {summary['steps']:.0f}: wall/step {summary['wall_us']:.1f} us, busy/step "
+              f"{summary['busy_us']:.1f} us, idle/step {summary['idle_us']:.1f} us, launches/step "
+              f"{summary['launches']:.1f}")
+        print("| kernel | grid | launches/step | avg us | us/step | % of busy |")
+        print("|---|---|---:|---:|---:|---:|")
+        for n, g, per, avg, us, pct in rows:
+            print(f"| {n} | {g}x1 | {per:.0f} | {avg:.2f} | {us:.1f} | {pct:.1f} |")
+    else:
+        substr = argv[2] if len(argv) > 2 else ""
+        print("| kernel | grid | launches | avg us | median us | min us |")
+        print("|---|---|---:|---:|---:|---:|")
+        for n, g, cnt, avg, med, mn in kernel_table(launches, substr):
+            print(f"| {n} | {g}x1 | {cnt} | {avg:.2f} | {med:.2f} | {mn:.2f} |")
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(_main(sys.argv[1:]))
