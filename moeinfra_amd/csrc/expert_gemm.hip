@@ -39,13 +39,8 @@
 namespace moe {
 namespace {
 
-constexpr int kGmBDepth = 4;                 // NF4 blocks in flight per wave (= loop unroll)
 constexpr int kPairWords = 256 * 32 * 2;     // code-pair table: 256 bytes x 32 replicas x 8 B
 constexpr uint32_t kGmOob = 0x80000000u;     // buffer offset past any accepted activation tensor
-// The block loop is unrolled by kGmBDepth from block 0 (K splits hold a multiple of 4
-// blocks), so ring slot b % kGmBDepth is static; the activation plane is a runtime LDS
-// offset.
-static_assert(kGmBDepth == 4, "ring slot and unroll");
 
 #define GM_GLOBAL __attribute__((address_space(1)))
 #define GM_LDS __attribute__((address_space(3)))
@@ -126,7 +121,7 @@ __device__ __forceinline__ bf16x8 gm_dequant(const uint32_t *tbl, uint32_t w, ui
 // fragments against 8 token tiles: half the dequantization and weight loads per MFMA), both
 // with the steps software-pipelined within the wave; or W = 8, MT = 4 (two waves per SIMD, 2
 // fragments each, the other wave covering a wave's stalls).
-template <bool GATEUP, int W, int MT>
+template <bool GATEUP, int W, int MT, int NF, int BD>
 __global__ void __launch_bounds__(W * 64, 1)
 expert_gemm_kernel(const ExpertTable tab, const uint16_t *__restrict__ act, uint32_t act_bytes,
                    int K, int NROWS, Route rt, int rows_total, int nsplit,
@@ -135,7 +130,12 @@ expert_gemm_kernel(const ExpertTable tab, const uint16_t *__restrict__ act, uint
   constexpr int kGmMT = MT;                            // 32-token MFMA tiles per item
   constexpr int kGmM = 32 * MT;                        // tokens per item
   constexpr int kGmPlane = kGmM * 128;                 // bytes of one block's activation tile
-  constexpr int kGmNF = 64 / MT / W;                   // fragments per wave (16 MFMAs a step)
+  constexpr int kGmNF = NF;                            // 32-row weight fragments per wave
+  // NF4 blocks in flight per wave: the weight ring.  The block loop is unrolled by BD from
+  // block 0, so ring slot b % BD is static; absmax comes per group of 4 blocks (K splits
+  // hold whole groups); the activation plane is a runtime LDS offset.
+  constexpr int kGmBDepth = BD;
+  static_assert(BD % 4 == 0, "ring depth: whole absmax groups");
   // Activation planes: three (the DMA runs two blocks ahead) when they fit beside the 64 KB
   // table, else two (one block ahead).
   constexpr int kPlanes = MT == 8 ? 2 : 3;
@@ -144,8 +144,9 @@ expert_gemm_kernel(const ExpertTable tab, const uint16_t *__restrict__ act, uint
   constexpr int kRowsWave = 32 * kRT;                  // weight rows per wave
   constexpr int kRowsItem = W * kRowsWave;             // weight rows per item
   constexpr int kGmFill = kGmPlane / 16 / kGmThreads;  // 16-byte pieces per thread and block
-  constexpr bool kPipe = W == 4;
-  static_assert(((W == 4 && (MT == 4 || MT == 8)) || (W == 8 && MT == 4)) &&
+  constexpr bool kPipe = W == 4 && MT * NF == 16;
+  static_assert(((W == 4 && MT == 8 && NF == 2) || (W == 8 && MT == 4 && NF == 2) ||
+                 (W == 4 && MT == 4 && NF == 4)) &&
                     kGmFill * kGmThreads * 16 == kGmPlane,
                 "supported shapes");
   // The activation planes at LDS offset 0 (the DMA's M0 base stays small), then the table.
@@ -387,7 +388,7 @@ expert_gemm_kernel(const ExpertTable tab, const uint16_t *__restrict__ act, uint
     auto convert = [&](const Pre &P, int slot, bf16x8 (&bv)[kGmNF]) {
 #pragma unroll
       for (int f = 0; f < kGmNF; ++f) {
-        const float sc = absc[f][slot];
+        const float sc = absc[f][slot & 3];  // block slot % 4 of its absmax group
         uint32_t o[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) o[j] = pack_bf16x2(P.c[f][j][0] * sc, P.c[f][j][1] * sc);
@@ -434,7 +435,7 @@ expert_gemm_kernel(const ExpertTable tab, const uint16_t *__restrict__ act, uint
     auto block = [&](uint32_t dst, const GM_LDS uint8_t *src, int d, int b) {
       dma(dst, b + kLA);
       load_b((d + kGmBDepth - 1) % kGmBDepth, b + kGmBDepth - 1);
-      if (d == 0 && b > 0) {  // group b / 4 starts: its absmax is the one loaded 4 blocks ago
+      if (d % 4 == 0 && b > 0) {  // group b / 4 starts: its absmax was loaded 4 blocks ago
 #pragma unroll
         for (int f = 0; f < kGmNF; ++f) absc[f] = absn[f];
         load_s(absn, b + 4);
@@ -474,11 +475,13 @@ expert_gemm_kernel(const ExpertTable tab, const uint16_t *__restrict__ act, uint
     for (int b0 = 0; b0 < NBp; b0 += kGmBDepth) {
 #pragma unroll
       for (int d = 0; d < kGmBDepth; ++d) {
-        // Plane (b + kLA) % kPlanes = (b - 1) % kPlanes was last read in block b - 1, before
-        // the barrier.
-        const int pd = pb == 0 ? kPlanes - 1 : pb - 1;
-        block(s_a0_off + pd * kGmPlane, s_a0 + pb * kGmPlane, d, b0 + d);
-        pb = pb == kPlanes - 1 ? 0 : pb + 1;
+        if (BD == 4 || b0 + d < NBp) {  // a split (4 k blocks) may end inside a BD-block step
+          // Plane (b + kLA) % kPlanes = (b - 1) % kPlanes was last read in block b - 1,
+          // before the barrier.
+          const int pd = pb == 0 ? kPlanes - 1 : pb - 1;
+          block(s_a0_off + pd * kGmPlane, s_a0 + pb * kGmPlane, d, b0 + d);
+          pb = pb == kPlanes - 1 ? 0 : pb + 1;
+        }
       }
     }
     if constexpr (kPipe) mfmas(pc, bc);
@@ -513,18 +516,21 @@ expert_gemm_kernel(const ExpertTable tab, const uint16_t *__restrict__ act, uint
 
 }  // namespace
 
-// Kernel shape of a launch: 256-token items (W = 4, MT = 8) from 512 routed rows per active
-// expert on average, else 128-token items with two waves per SIMD (W = 8, MT = 4).
+// Kernel shape of a launch (waves, token tiles per item, fragments per wave, ring depth):
+// 256-token items (W = 4, MT = 8) from 512 routed rows per active expert on average, else
+// 128-token items with two waves per SIMD (W = 8, MT = 4).
 struct GemmShape {
-  int waves, mt;
+  int waves, mt, nf, bd;
+  int64_t tokens() const { return 32 * mt; }
+  int64_t down_rows() const { return 32LL * waves * nf; }
 };
 GemmShape gemm_shape(int64_t rows, int64_t active) {
-  return active > 0 && rows >= 512 * active ? GemmShape{4, 8} : GemmShape{8, 4};
+  return active > 0 && rows >= 512 * active ? GemmShape{4, 8, 2, 4} : GemmShape{8, 4, 2, 4};
 }
 
 // The batched form of K4: gate/up (phases bit 0) and/or down (bit 1).  Gate/up items cover
-// 1024 / MT rows of F, down items 2048 / MT rows of H (at most 512); the down projection
-// splits K over `nsplit` ypart planes, each a whole number of 4-block absmax groups.
+// 16 W NF rows of F, down items 32 W NF rows of H (at most 512); the down projection splits
+// K over `nsplit` ypart planes, each a whole number of 4-block absmax groups.
 bool expert_gemm_supported(int32_t H, int32_t F) { return H % 512 == 0 && F % 256 == 0; }
 
 bool expert_gemm_splits_ok(int32_t F, int32_t nsplit) {
@@ -537,41 +543,43 @@ bool expert_gemm_rows_ok(int64_t T, int64_t rows_total, int32_t H, int32_t F) {
   return T * (int64_t)H * 2 < (int64_t)kGmOob && rows_total * (int64_t)F * 2 < (int64_t)kGmOob;
 }
 
-// Down-projection splits for a layer of `rows` routed rows over `active` experts: the
-// smallest power of two (up to kGmMaxSplits) that gives every CU kGmItemsPerCu items, when
-// the shape allows it.  Routed counts vary around the average, so an expert's last token
-// tile is often nearly empty but costs a whole item: several items per CU keep that from
-// setting the launch's length.
+// Down-projection splits for a layer of `rows` routed rows over `active` experts and a
+// launch shape: the smallest power of two (up to kGmMaxSplits) that gives every CU
+// kGmItemsPerCu items, when the shape allows it.  Routed counts vary around the average, so
+// an expert's last token tile is often nearly empty but costs a whole item: several items
+// per CU keep that from setting the launch's length.
 #ifndef GM_ITEMS_PER_CU
 #define GM_ITEMS_PER_CU 4
 #endif
 #ifndef GM_MAX_SPLITS
 #define GM_MAX_SPLITS 8
 #endif
-int expert_gemm_splits(int64_t rows, int64_t active, int32_t H, int32_t F) {
-  const GemmShape g = gemm_shape(rows, active);
+static int gemm_splits_for(const GemmShape &g, int64_t rows, int64_t active, int32_t H, int32_t F) {
   const int64_t per = active > 0 ? (rows + active - 1) / active : 0;
-  const int64_t m = 32 * g.mt, rows_item = 2048 / g.mt;
-  const int64_t items = active * ((per + m - 1) / m) * (H / rows_item);
+  const int64_t m = g.tokens();
+  const int64_t items = active * ((per + m - 1) / m) * (H / g.down_rows());
   const int64_t want = GM_ITEMS_PER_CU * (int64_t)device_cu_count();
   int s = 1;
   while (s < GM_MAX_SPLITS && items * s < want && expert_gemm_splits_ok(F, 2 * s)) s *= 2;
   return s;
 }
+int expert_gemm_splits(int64_t rows, int64_t active, int32_t H, int32_t F) {
+  return gemm_splits_for(gemm_shape(rows, active), rows, active, H, F);
+}
 
-template <int W, int MT>
+template <int W, int MT, int NF, int BD>
 static int launch_gemm_shape(const ExpertTable &tab, const void *x, int64_t T, int64_t rows_total,
                              int32_t H, int32_t F, const Route &rt, void *h_ws, void *ypart,
                              int32_t nsplit, int phases, hipStream_t stream) {
   const dim3 grid((unsigned)device_cu_count()), blk(W * kWave);
   if (phases & 1) {
-    hipLaunchKernelGGL((expert_gemm_kernel<true, W, MT>), grid, blk, 0, stream, tab,
+    hipLaunchKernelGGL((expert_gemm_kernel<true, W, MT, NF, BD>), grid, blk, 0, stream, tab,
                        (const uint16_t *)x, (uint32_t)(T * H * 2), H, F, rt, (int)rows_total, 1,
                        (uint16_t *)h_ws, (float *)nullptr);
     MOE_LAUNCH_CHECK();
   }
   if (phases & 2) {
-    hipLaunchKernelGGL((expert_gemm_kernel<false, W, MT>), grid, blk, 0, stream, tab,
+    hipLaunchKernelGGL((expert_gemm_kernel<false, W, MT, NF, BD>), grid, blk, 0, stream, tab,
                        (const uint16_t *)h_ws, (uint32_t)(rows_total * F * 2), F, H, rt,
                        (int)rows_total, nsplit, (uint16_t *)nullptr, (float *)ypart);
     MOE_LAUNCH_CHECK();
@@ -579,18 +587,24 @@ static int launch_gemm_shape(const ExpertTable &tab, const void *x, int64_t T, i
   return MOE_STATUS_OK;
 }
 
-int launch_expert_gemm(const void *tab_v, const void *x, int64_t T, int64_t rows_total,
-                       int64_t active_max, int32_t H, int32_t F, const void *route_v, void *h_ws,
-                       void *ypart, int32_t nsplit, int phases, hipStream_t stream) {
+static int check_gemm_args(int64_t T, int64_t rows_total, int32_t H, int32_t F, int32_t nsplit) {
   MOE_REQUIRE(expert_gemm_supported(H, F), "shape not supported by the batched expert GEMM");
   MOE_REQUIRE(expert_gemm_splits_ok(F, nsplit), "K split count not supported by the batched expert GEMM");
   MOE_REQUIRE(expert_gemm_rows_ok(T, rows_total, H, F), "activations too large for the batched expert GEMM");
+  return MOE_STATUS_OK;
+}
+
+int launch_expert_gemm(const void *tab_v, const void *x, int64_t T, int64_t rows_total,
+                       int64_t active_max, int32_t H, int32_t F, const void *route_v, void *h_ws,
+                       void *ypart, int32_t nsplit, int phases, hipStream_t stream) {
+  const int rc = check_gemm_args(T, rows_total, H, F, nsplit);
+  if (rc != MOE_STATUS_OK) return rc;
   const ExpertTable &tab = *static_cast<const ExpertTable *>(tab_v);
   const Route &rt = *static_cast<const Route *>(route_v);
   const GemmShape g = gemm_shape(rows_total, active_max);
   if (g.mt == 8)
-    return launch_gemm_shape<4, 8>(tab, x, T, rows_total, H, F, rt, h_ws, ypart, nsplit, phases, stream);
-  return launch_gemm_shape<8, 4>(tab, x, T, rows_total, H, F, rt, h_ws, ypart, nsplit, phases, stream);
+    return launch_gemm_shape<4, 8, 2, 4>(tab, x, T, rows_total, H, F, rt, h_ws, ypart, nsplit, phases, stream);
+  return launch_gemm_shape<8, 4, 2, 4>(tab, x, T, rows_total, H, F, rt, h_ws, ypart, nsplit, phases, stream);
 }
 
 }  // namespace moe
