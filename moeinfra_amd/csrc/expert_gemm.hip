@@ -140,6 +140,11 @@ expert_gemm_kernel(const ExpertTable tab, const uint16_t *__restrict__ act, uint
   // table, else two (one block ahead).
   constexpr int kPlanes = MT == 8 ? 2 : 3;
   constexpr int kLA = kPlanes - 1;
+  constexpr uint32_t kTblHi = (uint32_t)(kPlanes * kGmPlane) >> 16;  // table offset / 64 KB
+  static_assert(kPlanes * kGmPlane < 65536 || (kPlanes * kGmPlane) % 65536 == 0, "table offset");
+  // v_perm selector of a table address: byte 0 = lc's byte 0 (replica), byte 1 = the packed
+  // byte (added per lookup), byte 2 = lc's byte 2 (table offset / 64 KB) or zero, byte 3 zero.
+  constexpr uint32_t kTblSel = kTblHi ? 0x0c020400u : 0x0c0c0400u;
   constexpr int kRT = GATEUP ? kGmNF / 2 : kGmNF;      // 32-row tiles per wave
   constexpr int kRowsWave = 32 * kRT;                  // weight rows per wave
   constexpr int kRowsItem = W * kRowsWave;             // weight rows per item
@@ -275,7 +280,8 @@ expert_gemm_kernel(const ExpertTable tab, const uint16_t *__restrict__ act, uint
     two = __ballot(two) != 0;
 #pragma unroll
     for (int p = 0; p < kStreams; ++p)
-      lc[p] = (two ? (uint32_t)((lane & 15) | (p << 4)) : (uint32_t)(li ^ (kg << 4))) << 3;
+      lc[p] = ((two ? (uint32_t)((lane & 15) | (p << 4)) : (uint32_t)(li ^ (kg << 4))) << 3) |
+              (kTblHi << 16);
     gm_lds_barrier();
     tbl_a = a;
   };
@@ -301,7 +307,10 @@ expert_gemm_kernel(const ExpertTable tab, const uint16_t *__restrict__ act, uint
   const uint32_t s_lane = (uint32_t)li * (uint32_t)NB;
   const GM_LDS uint8_t *const s_a0 = (const GM_LDS uint8_t *)s_lds;
   const uint32_t s_a0_off = (uint32_t)(uintptr_t)s_a0;
-  const GM_LDS char *const tbl = (const GM_LDS char *)s_pair;
+  // Table reads address byte (v << 8) | (rep << 3) of the table.  Past 64 KB (two 32 KB
+  // planes in front) the table's offset does not fit a ds_read's 16-bit immediate; the
+  // v_perm that builds the address then inserts its high byte (from lc) instead.
+  const GM_LDS char *const tbl = (const GM_LDS char *)s_lds + (kTblHi ? 0 : kPlanes * kGmPlane);
 
   f32x16 acc[kGmMT][kGmNF];
   u32x4 ring[kGmBDepth][kGmNF];
@@ -329,16 +338,20 @@ expert_gemm_kernel(const ExpertTable tab, const uint16_t *__restrict__ act, uint
       wb[f] = (gm_gq_t)(uintptr_t)uptr(s) + (fr0 * row_bytes + kb0 * 32u);
       ab[f] = (gm_ga_t)(uintptr_t)uptr(2 + s) + (fr0 * (uint32_t)NB + kb0);
     }
+    // Rows past the expert's count read past the tensor (zeros).  The token ids of all rows
+    // are loaded together (clamped to the last row, then masked): one round trip, where a
+    // load behind a branch per row would wait for each in turn.
     uint32_t fo[kGmFill];
 #pragma unroll
     for (int j = 0; j < kGmFill; ++j) {
       const int r = mt * kGmM + fr + 8 * W * j;
-      uint32_t o = kGmOob;
-      if (r < cnt) {
-        const uint32_t arow = GATEUP ? (uint32_t)rt.perm_tok[off + r] : (uint32_t)(off + r);
-        o = (arow * (uint32_t)K + kb0 * 64u + fsrc) * 2u;
-      }
-      fo[j] = o;
+      const int rc = r < cnt ? r : cnt - 1;
+      fo[j] = GATEUP ? (uint32_t)rt.perm_tok[off + rc] : (uint32_t)(off + rc);
+    }
+#pragma unroll
+    for (int j = 0; j < kGmFill; ++j) {
+      const int r = mt * kGmM + fr + 8 * W * j;
+      fo[j] = r < cnt ? (fo[j] * (uint32_t)K + kb0 * 64u + fsrc) * 2u : kGmOob;
     }
 
     // Weights of block b and absmax of blocks b4..b4+3 (past the split's end: its last
@@ -381,7 +394,7 @@ expert_gemm_kernel(const ExpertTable tab, const uint16_t *__restrict__ act, uint
       for (int f = 0; f < kGmNF; ++f)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const uint32_t addr = __builtin_amdgcn_perm(ring[slot][f][q], lc[GATEUP ? (f & 1) : 0], 0x0c0c0400u + (j << 8));
+          const uint32_t addr = __builtin_amdgcn_perm(ring[slot][f][q], lc[GATEUP ? (f & 1) : 0], kTblSel + (j << 8));
           P.c[f][j] = *reinterpret_cast<const GM_LDS f32x2 *>(tb + addr);
         }
     };
@@ -423,8 +436,7 @@ expert_gemm_kernel(const ExpertTable tab, const uint16_t *__restrict__ act, uint
     for (int d = 0; d < kLA; ++d) dma(s_a0_off + d * kGmPlane, d);
 #pragma unroll
     for (int d = 0; d < kGmBDepth - 1; ++d) load_b(d, d);
-    load_s(absc, 0);
-    load_s(absn, 4);
+    load_s(absn, 0);  // moved to absc as block 0 starts
     // The prologue's activations landed (the weight loads issued after them may not).
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(gm_vmcnt(kGmNF * (kGmBDepth - 1)));
@@ -433,13 +445,24 @@ expert_gemm_kernel(const ExpertTable tab, const uint16_t *__restrict__ act, uint
     // One block: the DMA of block b + kLA's activations into plane `dst`, block b + 3's
     // weights, and block b's four MFMA steps from plane `src` and the table.
     auto block = [&](uint32_t dst, const GM_LDS uint8_t *src, int d, int b) {
-      dma(dst, b + kLA);
-      load_b((d + kGmBDepth - 1) % kGmBDepth, b + kGmBDepth - 1);
-      if (d % 4 == 0 && b > 0) {  // group b / 4 starts: its absmax was loaded 4 blocks ago
+      // Issue order: absmax (at a group start), activations, weights.  The wait before the
+      // barrier counts the loads issued after the activations it needs, so the absmax loads
+      // go first: issued last, that count would also have to cover them.
+      if (d % 4 == 0) {  // static: group b / 4 starts; its absmax was loaded 4 blocks ago
+        // The loads that filled absn were issued before a block's activation DMA, whose
+        // wait completed them.  Reading absn here, before this block's DMA is issued, puts
+        // the compiler's own wait for them (it cannot count the DMA) where the hardware has
+        // only the previous block's weight loads outstanding: a no-op, where further on it
+        // would also wait for the DMA just issued.
+#pragma unroll
+        for (int f = 0; f < kGmNF; ++f) asm volatile("" ::"v"(absn[f]));
 #pragma unroll
         for (int f = 0; f < kGmNF; ++f) absc[f] = absn[f];
         load_s(absn, b + 4);
       }
+      __builtin_amdgcn_sched_barrier(0);
+      dma(dst, b + kLA);
+      load_b((d + kGmBDepth - 1) % kGmBDepth, b + kGmBDepth - 1);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
@@ -462,13 +485,14 @@ expert_gemm_kernel(const ExpertTable tab, const uint16_t *__restrict__ act, uint
         }
       }
       // Block b + 1's activations (issued kLA - 1 blocks earlier) must have landed for every
-      // wave before the barrier.  Issued after them: with kLA = 2 every load of block b (block
-      // b + 2's activations, kGmFill; block b + 3's weights, kGmNF; at a group start kGmNF
-      // absmax loads); with kLA = 1 block b's weight and absmax loads (the DMA comes first,
-      // an asm statement the loads do not move across).  Waiting down to those counts covers
-      // any order the compiler gave the loads of a block.
+      // wave before the barrier.  Issued after them (sched_barriers keep the three groups in
+      // order; the DMA is an asm statement no load moves across): with kLA = 1 block b's
+      // weight loads (kGmNF); with kLA = 2 block b - 1's weight loads, then block b's absmax
+      // loads if any, activations (kGmFill) and weights (kGmNF).  Waiting down to kGmNF,
+      // resp. kGmFill + 2 kGmNF, completes exactly the loads up to those activations (with
+      // block b's absmax loads present, block b - 1's weights too).
       __builtin_amdgcn_sched_barrier(0);
-      __builtin_amdgcn_s_waitcnt(gm_vmcnt((kLA - 1) * kGmFill + kGmNF));
+      __builtin_amdgcn_s_waitcnt(gm_vmcnt(kLA == 1 ? kGmNF : kGmFill + 2 * kGmNF));
       gm_lds_barrier();
     };
     int pb = 0;  // plane of block b: b % kPlanes
