@@ -511,22 +511,36 @@ expert_gemm_kernel(const ExpertTable tab, const uint16_t *__restrict__ act, uint
     if constexpr (kPipe) mfmas(pc, bc);
 
     // Lane l = 32 kg + i holds column i of each fragment for token rows
-    // 32 t + 8 (v >> 2) + 4 kg + (v & 3) of the item's tile.
+    // 32 t + 8 (v >> 2) + 4 kg + (v & 3) of the item's tile.  The stores go through a buffer
+    // descriptor that spans the expert's cnt rows: a row past the expert's last is dropped by
+    // the range check (which covers the per-lane offset, so the row goes there), instead of a
+    // branch and 64-bit address arithmetic per value.
+    {
+      constexpr uint32_t kEs = GATEUP ? 2u : 4u;  // bytes per output value
+      char *obase = GATEUP ? (char *)(h_out + (size_t)off * NROWS)
+                           : (char *)(y_out + ((size_t)sp * rows_total + off) * NROWS);
+      const __amdgpu_buffer_rsrc_t orsrc = __builtin_amdgcn_make_buffer_rsrc(
+          obase, (short)0, (int)((uint32_t)cnt * (uint32_t)NROWS * kEs), 0x00020000);
+      const uint32_t lane_off = ((uint32_t)(mt * kGmM + 4 * kg) * (uint32_t)NROWS + row0 + (uint32_t)li) * kEs;
+      const uint32_t row_step = (uint32_t)NROWS * kEs;
 #pragma unroll
-    for (int t = 0; t < kGmMT; ++t) {
+      for (int t = 0; t < kGmMT; ++t) {
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int m = mt * kGmM + 32 * t + 8 * (v >> 2) + 4 * kg + (v & 3);
-        if (m < cnt) {
-          const size_t orow = (size_t)(off + m);
+        for (int v = 0; v < 16; ++v) {
+          const uint32_t o = lane_off + (uint32_t)(32 * t + 8 * (v >> 2) + (v & 3)) * row_step;
           if constexpr (GATEUP) {
 #pragma unroll
             for (int r2 = 0; r2 < kRT; ++r2)
-              h_out[orow * NROWS + row0 + 32 * r2 + li] = swiglu_bf16(acc[t][2 * r2][v], acc[t][2 * r2 + 1][v]);
+              __builtin_amdgcn_raw_buffer_store_b16(swiglu_bf16(acc[t][2 * r2][v], acc[t][2 * r2 + 1][v]),
+                                                    orsrc, (int)(o + 64u * r2), 0, 0);
           } else {
-            float *yrow = y_out + ((size_t)sp * rows_total + orow) * NROWS + row0 + li;
 #pragma unroll
-            for (int f = 0; f < kGmNF; ++f) yrow[32 * f] = acc[t][f][v];
+            for (int f = 0; f < kGmNF; ++f) {
+              // Element by value: a bit cast of the vector element itself reads element 0.
+              const float val = acc[t][f][v];
+              __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, val), orsrc,
+                                                    (int)(o + 128u * f), 0, 0);
+            }
           }
         }
       }
