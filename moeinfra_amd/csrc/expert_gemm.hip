@@ -112,6 +112,22 @@ __device__ __forceinline__ bf16x8 gm_dequant(const uint32_t *tbl, uint32_t w, ui
   return as_bf16x8(o[0], o[1], o[2], o[3]);
 }
 
+// bf16(bf16(silu(bf16(g))) * bf16(u)), the op order of F.silu(gate) * up on bf16 tensors,
+// with silu(x) = x / (1 + e^-x) from the hardware's 2^x and reciprocal (about 1 ulp each in
+// fp32, a few ulp for |x| in the tens) instead of an exactly rounded exp and division: the
+// bf16 rounding of silu can then differ from the correctly rounded one by one bf16 ulp, for
+// the values whose fp32 silu lies within a few fp32 ulp of a bf16 rounding boundary.  The
+// batched products' fp32 sums already differ from a sequential sum by more than that.  Large
+// negative x: 2^x overflows to inf, the reciprocal to 0, silu to -0, as the exact form.
+__device__ __forceinline__ uint16_t gm_swiglu_bf16(float g, float u) {
+  const uint32_t gu = pack_bf16x2(g, u);  // both rounded to bf16 in one conversion
+  const float gb = __builtin_bit_cast(float, gu << 16);
+  const float ub = __builtin_bit_cast(float, gu & 0xffff0000u);
+  const float e = __builtin_amdgcn_exp2f(gb * -1.44269504088896341f);
+  const float sb = bf16_to_f32(f32_to_bf16(gb * __builtin_amdgcn_rcpf(1.0f + e)));
+  return f32_to_bf16(sb * ub);
+}
+
 // The DMA's inline asm names M0, a register the compiler reserves and sets before each of
 // its own uses (this kernel has none besides the asm).
 #pragma clang diagnostic push
@@ -531,7 +547,7 @@ expert_gemm_kernel(const ExpertTable tab, const uint16_t *__restrict__ act, uint
           if constexpr (GATEUP) {
 #pragma unroll
             for (int r2 = 0; r2 < kRT; ++r2)
-              __builtin_amdgcn_raw_buffer_store_b16(swiglu_bf16(acc[t][2 * r2][v], acc[t][2 * r2 + 1][v]),
+              __builtin_amdgcn_raw_buffer_store_b16(gm_swiglu_bf16(acc[t][2 * r2][v], acc[t][2 * r2 + 1][v]),
                                                     orsrc, (int)(o + 64u * r2), 0, 0);
           } else {
 #pragma unroll
