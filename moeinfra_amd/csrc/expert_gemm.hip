@@ -592,9 +592,11 @@ bool expert_gemm_splits_ok(int32_t F, int32_t nsplit) {
   return nsplit >= 1 && nb % nsplit == 0 && (nb / nsplit) % 4 == 0;
 }
 
-// Activation tensors are addressed with 32-bit buffer offsets below kGmOob.
+// Activation tensors (x, h) and an expert's outputs (its h rows, its fp32 ypart rows of one
+// split) are addressed with 32-bit buffer offsets below kGmOob.
 bool expert_gemm_rows_ok(int64_t T, int64_t rows_total, int32_t H, int32_t F) {
-  return T * (int64_t)H * 2 < (int64_t)kGmOob && rows_total * (int64_t)F * 2 < (int64_t)kGmOob;
+  return T * (int64_t)H * 2 < (int64_t)kGmOob && rows_total * (int64_t)F * 2 < (int64_t)kGmOob &&
+         rows_total * (int64_t)H * 4 < (int64_t)kGmOob;
 }
 
 // Down-projection splits for a layer of `rows` routed rows over `active` experts and a
