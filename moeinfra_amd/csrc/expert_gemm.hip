@@ -32,8 +32,10 @@
 // rows, 16-byte pieces XOR-swizzled by the row); the A operand of step q for token row m is
 // piece 4 kg + q of the row, the K slice the weight lanes hold.  The tiles arrive by LDS DMA
 // (buffer loads into LDS: rows past the expert's count read zeros), two blocks ahead into
-// three planes or, for 256-token tiles, one block ahead into two; the workgroup meets at one
-// LDS-only barrier per block, which leaves the weight loads in flight.
+// three planes or, for 256-token tiles, one block ahead into two.  With two planes the
+// workgroup meets at one LDS-only barrier per block, which leaves the weight loads in
+// flight; with three, each wave waits only until every wave has issued its reads of the
+// previous block (an LDS counter), so waves can drift up to a block apart.
 #include "nf4_tile.h"
 
 namespace moe {
@@ -60,6 +62,16 @@ __device__ __forceinline__ void gm_lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Waits until the workgroup counter *c reaches `target`.  The wait is bounded (~1 ms, far
+// beyond a block's few microseconds): a counting error then gives wrong results instead of
+// a wave that never ends.
+__device__ __forceinline__ void gm_wait_ge(int *c, int target) {
+  for (int i = 0; i < (1 << 14); ++i) {
+    if (__hip_atomic_load(c, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) return;
+    __builtin_amdgcn_s_sleep(1);
+  }
 }
 
 // Position of 16-byte piece p in activation row r.  gfx950 serves a 64-lane ds_read_b128 16
@@ -166,6 +178,17 @@ expert_gemm_kernel(const ExpertTable tab, const uint16_t *__restrict__ act, uint
   constexpr int kRowsItem = W * kRowsWave;             // weight rows per item
   constexpr int kGmFill = kGmPlane / 16 / kGmThreads;  // 16-byte pieces per thread and block
   constexpr bool kPipe = W == 4 && MT * NF == 16;
+  // With the DMA two blocks ahead (three planes) the waves meet through one LDS counter
+  // instead of a barrier per block.  At block b's start a wave waits for its own share of
+  // block b + 1's activations (issued a block earlier), then until every wave has issued
+  // its reads of block b - 1 (a wave's count per block after its last step's reads):
+  // those waves have passed block b - 1's start, so every share of block b's plane has
+  // landed, and plane (b + 2) % 3 = (b - 1) % 3 is free for the DMA.  The first wave to pass
+  // block b's start finds exactly b counts from each wave, so no wave gets more than a block
+  // ahead and an early wave's counts never stand in for a late wave's.  Two planes (DMA one
+  // block ahead) keep the barrier: a wave's share of the next plane lands only at its
+  // block's end.
+  constexpr bool kOneSided = kLA == 2;
   static_assert(((W == 4 && MT == 8 && NF == 2) || (W == 8 && MT == 4 && NF == 2) ||
                  (W == 4 && MT == 4 && NF == 4)) &&
                     kGmFill * kGmThreads * 16 == kGmPlane,
@@ -181,6 +204,9 @@ expert_gemm_kernel(const ExpertTable tab, const uint16_t *__restrict__ act, uint
   // packed, w2 absmax.
   __shared__ const void *s_ptr[MOE_MAX_EXPERTS][4];
   __shared__ int s_nitems;
+  // Three-plane shape: threads whose wave has issued the reads of its current block's plane
+  // (counted over the item), in place of a barrier per block.
+  __shared__ int s_rdone;
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
@@ -456,11 +482,20 @@ expert_gemm_kernel(const ExpertTable tab, const uint16_t *__restrict__ act, uint
     // The prologue's activations landed (the weight loads issued after them may not).
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(gm_vmcnt(kGmNF * (kGmBDepth - 1)));
+    if (kOneSided && threadIdx.x == 0) s_rdone = 0;
     gm_lds_barrier();
 
     // One block: the DMA of block b + kLA's activations into plane `dst`, block b + 3's
     // weights, and block b's four MFMA steps from plane `src` and the table.
     auto block = [&](uint32_t dst, const GM_LDS uint8_t *src, int d, int b) {
+      if constexpr (kOneSided) {
+        // Own share of block b + 1's activations: only block b - 1's weight loads were
+        // issued after it.
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(gm_vmcnt(kGmNF));
+        if (b > 0) gm_wait_ge(&s_rdone, kGmThreads * b);
+        __builtin_amdgcn_sched_barrier(0);
+      }
       // Issue order: absmax (at a group start), activations, weights.  The wait before the
       // barrier counts the loads issued after the activations it needs, so the absmax loads
       // go first: issued last, that count would also have to cover them.
@@ -496,6 +531,14 @@ expert_gemm_kernel(const ExpertTable tab, const uint16_t *__restrict__ act, uint
           Pre p;
           bf16x8 bv[kGmNF];
           issue(p, src, tbl, d, q);
+          if (kOneSided && q == 3) {
+            // After the block's last reads of its plane (release: they complete first).  Every
+            // lane adds 1 (the compiler folds the wave's adds into one ds_add of 64), so the
+            // counts are threads: kGmThreads per block.
+            __builtin_amdgcn_sched_barrier(0);
+            __hip_atomic_fetch_add(&s_rdone, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+            __builtin_amdgcn_sched_barrier(0);
+          }
           convert(p, d, bv);
           mfmas(p, bv);
         }
@@ -507,9 +550,11 @@ expert_gemm_kernel(const ExpertTable tab, const uint16_t *__restrict__ act, uint
       // loads if any, activations (kGmFill) and weights (kGmNF).  Waiting down to kGmNF,
       // resp. kGmFill + 2 kGmNF, completes exactly the loads up to those activations (with
       // block b's absmax loads present, block b - 1's weights too).
-      __builtin_amdgcn_sched_barrier(0);
-      __builtin_amdgcn_s_waitcnt(gm_vmcnt(kLA == 1 ? kGmNF : kGmFill + 2 * kGmNF));
-      gm_lds_barrier();
+      if constexpr (!kOneSided) {
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(gm_vmcnt(kLA == 1 ? kGmNF : kGmFill + 2 * kGmNF));
+        gm_lds_barrier();
+      }
     };
     int pb = 0;  // plane of block b: b % kPlanes
     for (int b0 = 0; b0 < NBp; b0 += kGmBDepth) {
@@ -525,6 +570,9 @@ expert_gemm_kernel(const ExpertTable tab, const uint16_t *__restrict__ act, uint
       }
     }
     if constexpr (kPipe) mfmas(pc, bc);
+    // Every wave's reads of the item's planes have ended before the next item's table,
+    // counter reset and prologue DMA.
+    if constexpr (kOneSided) gm_lds_barrier();
 
     // Lane l = 32 kg + i holds column i of each fragment for token rows
     // 32 t + 8 (v >> 2) + 4 kg + (v & 3) of the item's tile.  The stores go through a buffer
