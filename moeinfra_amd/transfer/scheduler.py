@@ -1,6 +1,6 @@
 """Expert-residency transfer scheduler: the TransferScheduler API of the reference's
 transfer/scheduler.py:35-628 (submit / execute_next / drain / cancel / pending_count /
-submit_async / poll_async), built for this package's offload path.
+submit_async / poll_async / bandwidth_monitor), built for this package's offload path.
 
 Bringing expert (layer, expert) onto the GPU:
 
@@ -41,6 +41,7 @@ from typing import Optional
 
 import torch
 
+from .bandwidth import BandwidthMonitor
 from .device_slots import DeviceExpertSlots
 from .expert_image import ImageLayout
 from .nf4_reconstruct import ReconstructedNF4Expert
@@ -70,6 +71,7 @@ class TransferScheduler:
         self.bandwidth_gbps = bandwidth_gbps
         self.max_concurrent = max_concurrent
         self._logger = logger or logging.getLogger(__name__)
+        self._bw_monitor = BandwidthMonitor(window_s=5.0)
         self._staging_pool = staging_pool
         self._transfer_stream = transfer_stream
         self._device_slots = device_slots
@@ -139,6 +141,10 @@ class TransferScheduler:
                     self._cache_manager.demote_to_cpu(*key)
                 return True
         return False
+
+    @property
+    def bandwidth_monitor(self) -> BandwidthMonitor:
+        return self._bw_monitor
 
     # ------------------------------------------------------------------ copies
     def _slots_for(self, nbytes: int) -> DeviceExpertSlots:
@@ -304,6 +310,8 @@ class TransferScheduler:
         profile.update(total_execute_next_ms=elapsed_ms, success=success,
                        bytes_transferred=nbytes if success else 0)
         EXECUTE_NEXT_PROFILE.append(profile)
+        if success:
+            self._bw_monitor.record(nbytes)
         return TransferResult(request_id=request.request_id, success=success,
                               elapsed_ms=elapsed_ms, bytes_transferred=nbytes if success else 0,
                               error=error)
@@ -350,6 +358,7 @@ class TransferScheduler:
         for key, h in list(self._async.items()):
             if h.status == TransferStatus.IN_FLIGHT and h.event.query():
                 h.status = TransferStatus.READY
+                self._bw_monitor.record(h.nbytes)
             if h.status == TransferStatus.CANCELLED and h.event.query():
                 del self._async[key]
             elif h.status == TransferStatus.READY and \
@@ -387,6 +396,7 @@ class TransferScheduler:
             return handle(TransferStatus.REJECTED)
         h = handle(TransferStatus.IN_FLIGHT, done)
         h.gpu_state, h.cpu_expert = expert, cpu_expert
+        h.nbytes = self._cache_manager.get_size_bytes(*key)   # the expert is in the GPU tier now
         self._async[key] = h
         return h
 
@@ -405,6 +415,8 @@ class TransferScheduler:
             return TransferStatus.CANCELLED
         if not done:
             return TransferStatus.IN_FLIGHT
+        if h.status == TransferStatus.IN_FLIGHT:
+            self._bw_monitor.record(h.nbytes)
         h.status = TransferStatus.READY
         del self._async[key]
         return TransferStatus.READY

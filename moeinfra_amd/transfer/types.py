@@ -60,3 +60,6 @@ class TransferHandle:
     status: TransferStatus = TransferStatus.IN_FLIGHT
     gpu_state: object = None
     cpu_expert: object = None
+    #: Bytes the transfer moves host -> device (recorded by the bandwidth monitor when the
+    #: copy is seen complete).
+    nbytes: int = 0

@@ -188,6 +188,11 @@ def test_async_transfers_publish_at_once_and_order_the_compute(cuda_device):
     assert sch.poll_async(1, 0) == TransferStatus.CANCELLED
     assert sch.poll_async(0, 3) == TransferStatus.READY
     assert sch.poll_async(0, 3) == TransferStatus.REJECTED      # retired
+    # Once observed complete, every copy reached the bandwidth monitor once (the cancelled
+    # one did not).
+    for e in range(E):
+        sch.poll_async(0, e)
+    assert sch.bandwidth_monitor.bytes_in_window() == sum(h.nbytes for h in handles) > 0
 
 
 def test_device_slots_are_leased_to_live_experts(cuda_device):

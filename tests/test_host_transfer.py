@@ -1,7 +1,7 @@
 """Transfer path host logic (transfer/*.py of the reference) -- CPU only.
 
 PinnedMemoryBudget and the staging pool's slot accounting (tests/test_pinned_memory.py,
-tests/test_reusable_staging.py of the reference) and the
+tests/test_reusable_staging.py of the reference), BandwidthMonitor and the
 TransferScheduler queue (tests/test_transfer.py) with a fake cache manager.  Pinned
 buffers and H2D copies need a GPU and are covered by the GPU tests.
 """
@@ -15,6 +15,7 @@ import numpy as np
 import pytest
 import torch
 
+from moeinfra_amd.transfer.bandwidth import BandwidthMonitor
 from moeinfra_amd.transfer.pinned_memory import PinnedMemoryBudget
 from moeinfra_amd.transfer.reusable_staging import ReusablePinnedStagingPool
 from moeinfra_amd.transfer.scheduler import EXECUTE_NEXT_PROFILE, TransferScheduler
@@ -155,6 +156,34 @@ def test_parse_blob_tolerates_garbage():
     assert parse_blob(torch.tensor(list(b"[1,2]"), dtype=torch.uint8)) == {}
 
 
+# --------------------------------------------------------------------------- bandwidth
+def test_bandwidth_monitor():
+    m = BandwidthMonitor(window_s=5.0)
+    assert m.current_gbps() == 0.0 and m.peak_gbps() == 0.0
+    m.record(1 << 30, now=100.0)
+    assert m.current_gbps(now=100.0) == 0.0                 # one sample: no rate yet
+    m.record(1 << 30, now=100.5)
+    assert m.current_gbps(now=101.0) == pytest.approx(2.0)  # 2 GiB over 1 s
+    assert m.peak_gbps() == pytest.approx(4.0)              # 2 GiB over 0.5 s at the record
+    assert m.current_gbps(now=200.0) == 0.0                 # both samples left the window
+    m.reset()
+    assert m.peak_gbps() == 0.0 and m.bytes_in_window() == 0
+    with pytest.raises(ValueError):
+        BandwidthMonitor(0)
+
+
+def test_bandwidth_monitor_wall_clock():
+    """The reference's own checks (tests/test_transfer.py:152-190): two samples a moment
+    apart give a positive rate, the peak stays at or above it, reset clears both."""
+    m = BandwidthMonitor(window_s=5.0)
+    m.record(1 << 30)
+    time.sleep(0.01)
+    m.record(1 << 30)
+    assert m.current_gbps() > 0.0 and m.peak_gbps() >= m.current_gbps()
+    m.reset()
+    assert m.current_gbps() == 0.0 and m.peak_gbps() == 0.0
+
+
 # --------------------------------------------------------------------------- scheduler
 def sched(cm=None, **kw):
     cm = cm or FakeCM()
@@ -198,6 +227,7 @@ def test_priority_then_fifo_order():
     assert cm.demoted == [(0, 2), (0, 1), (0, 3), (0, 0)]
     assert all(r.success and r.bytes_transferred == 10 and r.elapsed_ms > 0 for r in results)
     assert s.pending_count() == 0 and s.execute_next() is None and s.drain() == []
+    assert s.bandwidth_monitor.bytes_in_window() == 40
 
 
 def test_cancel_keeps_heap_order():
