@@ -67,6 +67,13 @@ const char *moe_last_error(void);
 /* Library version (major*10000 + minor*100 + patch). */
 int moe_version(void);
 
+/* Count of bounded in-kernel waits that gave up on the current device (lanes), for tests:
+ * the batched expert GEMM's waves meet through an LDS counter whose wait ends after ~1 ms
+ * whatever happens, so that every kernel exits; a non-zero count means a counting error
+ * (wrong results). reset != 0 clears it. Synchronous. No counterpart in the reference (its
+ * kernels are bitsandbytes' and torch's). */
+int moe_wait_timeouts(int64_t *count, int32_t reset);
+
 /* ---------------------------------------------------------------- K1: NF4 dequant
  * out_bf16[i] = bf16(code[q_i] * absmax[i / blocksize]) for i < numel.
  * Replaces the bitsandbytes dequantize_4bit that Linear4bit runs on the state built

@@ -40,6 +40,7 @@ class MoeNf4Expert(ctypes.Structure):
 SIGNATURES = {
     "moe_last_error": ([], ctypes.c_char_p),
     "moe_version": ([], ctypes.c_int),
+    "moe_wait_timeouts": ([ctypes.POINTER(_i64), _i32], ctypes.c_int),
     "moe_nf4_dequant_bf16": ([_vp, _vp, _vp, _vp, _i64, _i32, _vp], ctypes.c_int),
     "moe_nf4_quantize_bf16": ([_vp, _i64, _i32, _vp, _vp, _vp, _vp], ctypes.c_int),
     "moe_router_topk": ([_vp, _vp, _vp, _i64, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp],
@@ -119,3 +120,11 @@ def check(rc: int, what: str) -> None:
     if rc == MOE_STATUS_UNSUPPORTED:
         raise NotImplementedError(f"{what}: {msg}")
     raise MoeHipError(f"{what}: {msg} (status {rc})")
+
+
+def wait_timeouts(reset: bool = True) -> int:
+    """Bounded in-kernel waits that gave up on the current device since the last reset
+    (0 unless a kernel's wave counting went wrong).  Synchronous."""
+    n = _i64(0)
+    check(lib().moe_wait_timeouts(ctypes.byref(n), 1 if reset else 0), "moe_wait_timeouts")
+    return int(n.value)

@@ -64,14 +64,24 @@ __device__ __forceinline__ void gm_lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+}  // namespace
+
+// Bounded waits of this device that gave up (lanes), read and cleared by
+// moe_wait_timeouts(); zero unless a counting error or extreme wave drift occurred.
+__device__ unsigned int g_wait_timeouts;
+
+namespace {
+
 // Waits until the workgroup counter *c reaches `target`.  The wait is bounded (~1 ms, far
 // beyond a block's few microseconds): a counting error then gives wrong results instead of
-// a wave that never ends.
+// a wave that never ends, and the lanes that gave up are counted in g_wait_timeouts (a
+// vector-memory atomic), which the layer tests require to stay zero.
 __device__ __forceinline__ void gm_wait_ge(int *c, int target) {
   for (int i = 0; i < (1 << 14); ++i) {
     if (__hip_atomic_load(c, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) return;
     __builtin_amdgcn_s_sleep(1);
   }
+  __hip_atomic_fetch_add(&g_wait_timeouts, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Position of 16-byte piece p in activation row r.  gfx950 serves a 64-lane ds_read_b128 16
@@ -521,6 +531,12 @@ expert_gemm_kernel(const ExpertTable tab, const uint16_t *__restrict__ act, uint
           Pre pn;
           bf16x8 bn[kGmNF];
           issue(pn, src, tbl, d, q);
+          if (kOneSided && q == 3) {
+            // After the block's last reads of its plane, as in the unpipelined step below.
+            __builtin_amdgcn_sched_barrier(0);
+            __hip_atomic_fetch_add(&s_rdone, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+            __builtin_amdgcn_sched_barrier(0);
+          }
           mfmas(pc, bc);  // the previous step (for q = 0 the previous block's last)
           convert(pn, d, bn);
           pc = pn;
@@ -712,3 +728,19 @@ int launch_expert_gemm(const void *tab_v, const void *x, int64_t T, int64_t rows
 }
 
 }  // namespace moe
+
+// Reads (and with reset != 0 clears) the current device's count of bounded waits that gave
+// up.  Synchronous with respect to the device: a diagnostic for tests, not for hot loops.
+extern "C" int moe_wait_timeouts(int64_t *count, int32_t reset) {
+  MOE_REQUIRE(count != nullptr, "null count");
+  unsigned int v = 0;
+  MOE_HIP_CHECK(hipMemcpyFromSymbol(&v, HIP_SYMBOL(moe::g_wait_timeouts), sizeof(v), 0,
+                                    hipMemcpyDeviceToHost));
+  if (reset) {
+    const unsigned int zero = 0;
+    MOE_HIP_CHECK(hipMemcpyToSymbol(HIP_SYMBOL(moe::g_wait_timeouts), &zero, sizeof(zero), 0,
+                                    hipMemcpyHostToDevice));
+  }
+  *count = (int64_t)v;
+  return MOE_STATUS_OK;
+}

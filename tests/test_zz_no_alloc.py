@@ -113,3 +113,88 @@ def test_noalloc_refuses_a_layer_above_the_scratch():
                                            None, None, None)
     assert rc == _lib.MOE_STATUS_INVALID_ARGUMENT
     assert "static scratch" in lib.moe_last_error().decode()
+
+
+def _capture_and_compare(lib, table, E, gate, x, F, k, replays=3):
+    """Captures the allocation-free layer into a graph, replays it `replays` times with
+    eager work and host synchronisations between the replays, and checks every replay's
+    outputs bit for bit against an eager call with a caller workspace."""
+    from moeinfra_amd import _lib
+
+    dev = x.device
+    T, H = x.shape
+    out = torch.empty((T, H), dtype=torch.bfloat16, device=dev)
+    logits = torch.empty((T, E), dtype=torch.bfloat16, device=dev)
+    w = torch.empty((T, k), dtype=torch.float32, device=dev)
+    idx = torch.empty((T, k), dtype=torch.int64, device=dev)
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    rcs = []
+    with torch.cuda.stream(side), torch.cuda.graph(graph, stream=side):
+        rcs.append(lib.moe_layer_forward_nf4_noalloc(
+            table, E, gate.data_ptr(), None, x.data_ptr(), T, H, F, k, out.data_ptr(),
+            logits.data_ptr(), w.data_ptr(), idx.data_ptr(), side.cuda_stream))
+    _lib.check(rcs[0], "captured noalloc layer")
+    want = _run(lib, table, E, gate, None, x, F, k, noalloc=False)
+    for r in range(replays):
+        for t in (out, logits, w, idx):
+            t.fill_(-1)                      # eager work between the replays
+        torch.cuda.synchronize(dev)
+        graph.replay()
+        torch.cuda.synchronize(dev)
+        got = (bits(out), bits(logits), w.cpu().numpy(), idx.cpu().numpy())
+        for a, b in zip(got, want):
+            np.testing.assert_array_equal(a, b, err_msg=f"replay {r}, T={T}")
+
+
+def test_noalloc_layer_under_graph_capture(cuda_device):
+    """After eager calls (the scratch address is known), the allocation-free layer captured
+    into a HIP graph replays bit-identically to the workspace entry point: decode form
+    (T = 1), fused small-batch routing (T = 16) and the mid-batch path (T = 40)."""
+    from moeinfra_amd import _lib
+
+    lib = _lib.lib()
+    H, F, E, k = 1024, 3584, 8, 2
+    _keep, table, gate = _experts(cuda_device, H, F, E, seed=930)
+    g = torch.Generator(device=cuda_device).manual_seed(931)
+    for T in (1, 16, 40):
+        print(f"noalloc layer under graph capture T={T}", flush=True)
+        x = torch.randn((T, H), generator=g, device=cuda_device).to(torch.bfloat16)
+        _run(lib, table, E, gate, None, x, F, k, noalloc=True)   # warm-up call
+        _capture_and_compare(lib, table, E, gate, x, F, k)
+
+
+_FIRST_CALL_SCRIPT = r"""
+import sys
+sys.path[:0] = [{repo!r}, {tests!r}]
+import torch
+import test_zz_no_alloc as m
+from moeinfra_amd import _lib
+dev = torch.device("cuda:0")
+lib = _lib.lib()
+H, F, E, k, T = 1024, 3584, 8, 2, 16
+_keep, table, gate = m._experts(dev, H, F, E, seed=940)
+x = torch.randn((T, H), generator=torch.Generator(device=dev).manual_seed(941),
+                device=dev).to(torch.bfloat16)
+torch.cuda.synchronize()
+m._capture_and_compare(lib, table, E, gate, x, F, k)   # the process's first noalloc call
+print("first-call capture ok", flush=True)
+"""
+
+
+def test_noalloc_first_call_under_graph_capture(cuda_device):
+    """In a fresh process whose first allocation-free call is made under graph capture (the
+    scratch address is looked up inside the capture), the captured layer still replays
+    bit-identically to the workspace entry point."""
+    import os
+    import subprocess
+    import sys
+
+    here = os.path.dirname(os.path.abspath(__file__))
+    script = _FIRST_CALL_SCRIPT.format(repo=os.path.dirname(here), tests=here)
+    print("noalloc first call under graph capture (child process)", flush=True)
+    proc = subprocess.run([sys.executable, "-c", script], capture_output=True, text=True,
+                          timeout=300)
+    print(proc.stdout[-2000:], proc.stderr[-4000:], flush=True)
+    assert proc.returncode == 0 and "first-call capture ok" in proc.stdout
