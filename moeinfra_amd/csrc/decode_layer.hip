@@ -42,6 +42,9 @@ constexpr int kDecThreads = kDecWaves * kWave;
 constexpr int kDecMaxKParts = 8;
 // Items per workgroup whose sums the single-token gate/up path keeps in LDS until the end.
 constexpr int kRawSlots = 32;
+// Multi-token gate/up: the T tokens go to LDS once per workgroup when T * H fits this many
+// values (32 KB; the Mixtral step, T = 4 and H = 4096, does).
+constexpr int kXtMaxVals = kDecMaxTokens * 4096;
 
 
 // Routing of one decode step, written by workgroup 0 of the gate/up kernel and read by
@@ -129,7 +132,25 @@ struct ItemPtr {
   ga_t wa[NP];
   gx_t ap;
   ga_t ab[NP];  // absmax of the item's first tile row at its first stage (aligned stream)
+  // Activations staged in LDS (aligned stream, kXLds): the lane's 16-byte pieces of stage 0,
+  // in 16-byte units from the staging buffer's base (four pieces, one per token row of the
+  // lane, or one quarter with BC); stage s adds 64 s.
+  uint32_t xo[4];
 };
+
+// Where the aligned stream's activations come from.
+constexpr int kXGlobal = 0;  // global memory, loaded with the stage's weights
+constexpr int kXRegs = 1;    // registers, loaded once (one token for the whole stream)
+constexpr int kXLds = 2;     // the workgroup's LDS copy of the tokens, read a stage ahead
+
+// LDS copy of the T <= 4 tokens of a multi-token decode step: row t holds token t's H
+// values as 16-byte pieces; piece i (0..3) of each 64-byte chunk sits at position
+// i ^ (t & 3), so that the four lanes of a block, which read the same chunk of four
+// different tokens (or four quarters of one token), hit four different bank groups.
+typedef const __attribute__((address_space(3))) u32x4_t *lx_t;
+__device__ __forceinline__ uint32_t xlds_piece(int t, int H, int piece) {
+  return (uint32_t)(t * (H >> 3) + (piece & ~3) + ((piece & 3) ^ (t & 3)));
+}
 
 // Streams n_items items of nsq stages each (stage = 4 rows x 256 packed bytes per weight
 // stream) through a D-stage register pipeline.  next_item(P) is called once per item, in
@@ -281,6 +302,10 @@ struct StageQ {
   uint4 q[NP];
   uint4 xa[NX];
 };
+template <int NP>
+struct StageQ<NP, 0> {
+  uint4 q[NP];
+};
 
 // XREG activations from global memory or, for the fused-norm kernel, from LDS.
 __device__ __forceinline__ uint4 ld_x(gx_t p) { return ld_u4(p); }
@@ -288,7 +313,7 @@ __device__ __forceinline__ uint4 ld_x(const uint16_t *lds_p) {
   return *reinterpret_cast<const uint4 *>(lds_p);
 }
 
-template <int NP, int NSQ, int DEPTH, bool BC, bool XREG, bool LA, typename GrabFn,
+template <int NP, int NSQ, int DEPTH, bool BC, int XM, bool LA, typename GrabFn,
           typename PtrFn, typename FinishFn, typename Hook, typename XPtr>
 __device__ __forceinline__ void stream_aligned(GrabFn &&grab, PtrFn &&set_ptrs,
                                                FinishFn &&finish, Hook &&hook,
@@ -298,6 +323,9 @@ __device__ __forceinline__ void stream_aligned(GrabFn &&grab, PtrFn &&set_ptrs,
   static_assert(NSQ >= 2 && NSQ <= 8, "an item's absmax block must fit one load per lane");
   static_assert(DEPTH >= 2 && DEPTH <= NSQ && NSQ % DEPTH == 0, "depth must divide NSQ");
   static_assert(!LA || DEPTH >= 3, "lookahead needs depth >= 3");
+  static_assert(XM != kXLds || LA, "LDS activations are read in the lookahead slot");
+  constexpr bool XREG = XM == kXRegs;
+  constexpr bool XLDS = XM == kXLds;
   constexpr int NX = XREG ? 1 : (BC ? 1 : 4);
   // First step that loads a stage of the next item.
   constexpr int kNext = NSQ - DEPTH + 1;
@@ -335,16 +363,36 @@ __device__ __forceinline__ void stream_aligned(GrabFn &&grab, PtrFn &&set_ptrs,
     for (int sg = 0; sg < NSQ; ++sg) xr[sg] = ld_x(xbase + sg * kStageVals);
   }
   load_abs();
-  auto load = [&](StageQ<NP, NX> &st, int sg) {
+  auto load = [&](StageQ<NP, XM == kXGlobal ? NX : 0> &st, int sg) {
 #pragma unroll
     for (int p = 0; p < NP; ++p) st.q[p] = ld_u4_nt(P.wq[p] + sg * 256);
-    if (!XREG) {
+    if constexpr (XM == kXGlobal) {
       const gx_t px = P.ap + sg * kStageVals;
 #pragma unroll
       for (int i = 0; i < NX; ++i) st.xa[i] = ld_u4(px + 8 * i);
     }
   };
-  StageQ<NP, NX> st[DEPTH];
+  // kXLds: the current stage's activations (xc) and the next stage's (xn), read from LDS
+  // one step ahead; xoc holds the current item's piece offsets (P moves on to the next
+  // item at step kNext).
+  uint4 xc[XLDS ? NX : 1], xn[XLDS ? NX : 1];
+  uint32_t xoc[XLDS ? NX : 1];
+  auto lds_x = [&](uint4 (&dst)[XLDS ? NX : 1], const uint32_t (&xo)[XLDS ? NX : 1], int sg) {
+    if constexpr (XLDS) {
+      const lx_t xl = (lx_t)xbase;
+#pragma unroll
+      for (int i = 0; i < NX; ++i) {
+        const u32x4_t v = xl[xo[i] + 64 * sg];
+        dst[i] = make_uint4(v.x, v.y, v.z, v.w);
+      }
+    }
+  };
+  if constexpr (XLDS) {
+#pragma unroll
+    for (int i = 0; i < NX; ++i) xoc[i] = P.xo[i];
+    lds_x(xc, xoc, 0);
+  }
+  StageQ<NP, XM == kXGlobal ? NX : 0> st[DEPTH];
 #pragma unroll
   for (int d = 0; d < DEPTH - 1; ++d) {
     load(st[d], d);
@@ -388,8 +436,14 @@ __device__ __forceinline__ void stream_aligned(GrabFn &&grab, PtrFn &&set_ptrs,
       const int g = d + DEPTH - 1;  // stage sequence index of this step's load
       load(st[g % DEPTH], g < NSQ ? g : g - NSQ);
       __builtin_amdgcn_sched_barrier(0);  // this step's loads before its products
-      const StageQ<NP, NX> &cs = st[d % DEPTH];
-      const uint4 *xa = XREG ? &xr[d] : cs.xa;
+      const StageQ<NP, XM == kXGlobal ? NX : 0> &cs = st[d % DEPTH];
+      const uint4 *xa;
+      if constexpr (XM == kXGlobal)
+        xa = cs.xa;
+      else if constexpr (XREG)
+        xa = &xr[d];
+      else
+        xa = xc;
       float scl[NP];
 #pragma unroll
       for (int p = 0; p < NP; ++p) scl[p] = aslot[p * kASlotFloats + j * kASlotRow + 8 * d + (blk >> 1)];
@@ -399,7 +453,19 @@ __device__ __forceinline__ void stream_aligned(GrabFn &&grab, PtrFn &&set_ptrs,
       if (LA) {
         // Stage d+1 is in buffer (d+1) % DEPTH (for d = NSQ-1: the next item's stage 0, or
         // a re-read of this item's when it is the last one).
-        const StageQ<NP, NX> &ns = st[(d + 1) % DEPTH];
+        const StageQ<NP, XM == kXGlobal ? NX : 0> &ns = st[(d + 1) % DEPTH];
+        if constexpr (XLDS) {
+          // Stage d + 1 of this item, or (d = NSQ - 1) stage 0 of the next one, whose
+          // pointers P holds since step kNext (the current item's again after the last).
+          if (d + 1 < NSQ) {
+            lds_x(xn, xoc, d + 1);
+          } else {
+            uint32_t xo_n[NX];
+#pragma unroll
+            for (int i = 0; i < NX; ++i) xo_n[i] = P.xo[i];
+            lds_x(xn, xo_n, 0);
+          }
+        }
         s16x4 bn[LA ? NP : 1][8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
@@ -414,6 +480,10 @@ __device__ __forceinline__ void stream_aligned(GrabFn &&grab, PtrFn &&set_ptrs,
         for (int i = 0; i < 8; ++i)
 #pragma unroll
           for (int p = 0; p < NP; ++p) bq[p][i] = bn[p][i];
+        if constexpr (XLDS) {
+#pragma unroll
+          for (int i = 0; i < NX; ++i) xc[i] = xn[i];
+        }
       } else {
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
@@ -437,6 +507,10 @@ __device__ __forceinline__ void stream_aligned(GrabFn &&grab, PtrFn &&set_ptrs,
     for (int p = 0; p < NP; ++p) acc[p] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     if (nxt < 0) break;
     store_abs();
+    if constexpr (XLDS) {
+#pragma unroll
+      for (int i = 0; i < NX; ++i) xoc[i] = P.xo[i];
+    }
     cur = nxt;
     nxt = nxt2;
     if (nxt >= 0) set_ptrs(Pn, nxt);
@@ -657,6 +731,8 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
   // NORM: the normalised token (gate products read it here) and the norm's wave sums.
   __shared__ __attribute__((aligned(16))) uint16_t s_xn[NORM ? kDecNormMaxH : 8];
   __shared__ float s_npart[kDecWaves];
+  // Multi-token steps (no fused norm): the tokens, swizzled as xlds_piece describes.
+  __shared__ uint4 s_xt[NORM ? 1 : kXtMaxVals / 8];
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
@@ -709,6 +785,19 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
     }
   };
   load_round(0);
+  // Multi-token steps: this thread's pieces of the tokens for the LDS copy (stored before
+  // the routing barrier).  Only T > 1 loads them; on the single-token path the compiler's
+  // waits stay exact.
+  const bool xlds = !NORM && T > 1 && T * H <= kXtMaxVals;
+  constexpr int kXtPer = kXtMaxVals / 8 / kDecThreads;  // pieces per thread at most
+  uint4 xtv[kXtPer];
+  if (xlds) {
+#pragma unroll
+    for (int r = 0; r < kXtPer; ++r) {
+      const int q = tid + kDecThreads * r;
+      if (q < T * (H >> 3)) xtv[r] = ld_u4((gx_t)x + (size_t)q * 8);
+    }
+  }
   // Metadata of experts wave + 8q (wave-uniform, so the table entries are scalar loads):
   // lane l < 16 reads w1 code[l], 16..31 w3 code[l-16], 32..63 w2 code[l & 15]; lane f < 4
   // keeps stream pointer f (w1_packed, w1_absmax, w3_packed, w3_absmax).
@@ -804,8 +893,16 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
     const bool d2 = __ballot(lane >= 32 && lane < 48 && diff) != 0;
     if (lane == 0) s_slowbits[ee] = (uint8_t)((d1 ? 1 : 0) | (d2 ? 2 : 0));
   }
-  // Gate sums, codebooks, stream pointers, the lookup table and the work counter are
-  // visible to every wave after this barrier.
+  if (xlds) {
+#pragma unroll
+    for (int r = 0; r < kXtPer; ++r) {
+      const int q = tid + kDecThreads * r;
+      const int t = q / (H >> 3);
+      if (q < T * (H >> 3)) s_xt[xlds_piece(t, H, q - t * (H >> 3))] = xtv[r];
+    }
+  }
+  // Gate sums, codebooks, stream pointers, the lookup table, the work counter and the token
+  // copy are visible to every wave after this barrier.
   __syncthreads();
 
   // ---- routing and grouping by wave 0 (one wave, so that the SIMDs do not run the same
@@ -883,6 +980,10 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
     const int jj = (!bc && lanej < s_rt.counts[a]) ? lanej : 0;
     const int tok = s_rt.perm_tok[s_rt.offsets[a] + jj];
     P.ap = (gx_t)xt + (size_t)tok * H + blk * 32 + (bc ? lanej * 8 : 0);
+    // The LDS copy: with BC quarter lanej of the token's chunk blk, else the whole chunk
+    // of the lane's token row (the expert's first token again past its count).
+#pragma unroll
+    for (int i = 0; i < 4; ++i) P.xo[i] = xlds_piece(tok, H, 4 * blk + (bc ? lanej : i));
   };
   // nrows: MFMA result rows that hold tokens (1 on the single-token path, whose other rows
   // are never accumulated).
@@ -922,10 +1023,10 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
     if (nit > kRawSlots) {
       auto finish1 = [&](f32x4 (&ac)[2], int i) { finish_item(ac, i, 1); };
       if (NORM)
-        stream_aligned<2, 8, kGateUpDepth, true, true, kLookahead>(
+        stream_aligned<2, 8, kGateUpDepth, true, kXRegs, kLookahead>(
             grab, set_ptrs, finish1, hook, s_tbl, lane_const, row_blocks, s_aslot[wave], xl, (gq_t)gate);
       else
-        stream_aligned<2, 8, kGateUpDepth, true, true, kLookahead>(
+        stream_aligned<2, 8, kGateUpDepth, true, kXRegs, kLookahead>(
             grab, set_ptrs, finish1, hook, s_tbl, lane_const, row_blocks, s_aslot[wave], xb, (gq_t)gate);
       return;
     }
@@ -934,10 +1035,10 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
       s_raw[i - wlo][1][lane] = ac[1][0];
     };
     if (NORM)
-      stream_aligned<2, 8, kGateUpDepth, true, true, kLookahead>(
+      stream_aligned<2, 8, kGateUpDepth, true, kXRegs, kLookahead>(
           grab, set_ptrs, finish_raw, hook, s_tbl, lane_const, row_blocks, s_aslot[wave], xl, (gq_t)gate);
     else
-      stream_aligned<2, 8, kGateUpDepth, true, true, kLookahead>(
+      stream_aligned<2, 8, kGateUpDepth, true, kXRegs, kLookahead>(
           grab, set_ptrs, finish_raw, hook, s_tbl, lane_const, row_blocks, s_aslot[wave], xb, (gq_t)gate);
     __syncthreads();
     if (tid < 4 * nit) {
@@ -952,6 +1053,27 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
       int tile;
       const int a = item_expert(wlo + slot, tile);
       h_out[(size_t)s_rt.offsets[a] * F + tile * 4 + j] = swiglu_bf16(g, up);
+    }
+    return;
+  }
+  if (!NORM && xlds && !slow && nsq == 8) {
+    // Several tokens: the aligned stream over the workgroup's items, shared through the work
+    // counter, with the activations read from the workgroup's LDS copy of the tokens.
+    auto grab = [&]() -> int {
+      int t = 0;
+      if (lane == 0) t = __hip_atomic_fetch_add(&s_ticket, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      t = __builtin_amdgcn_readfirstlane(t) + wlo;
+      return t < whi ? t : -1;
+    };
+    const uint16_t *xl = reinterpret_cast<const uint16_t *>(s_xt);
+    if (bc) {
+      auto finish1 = [&](f32x4 (&ac)[2], int i) { finish_item(ac, i, 1); };
+      stream_aligned<2, 8, kGateUpDepth, true, kXLds, kLookahead>(
+          grab, set_ptrs, finish1, hook, s_tbl, lane_const, row_blocks, s_aslot[wave], xl, (gq_t)gate);
+    } else {
+      auto finish4 = [&](f32x4 (&ac)[2], int i) { finish_item(ac, i, 4); };
+      stream_aligned<2, 8, kGateUpDepth, false, kXLds, kLookahead>(
+          grab, set_ptrs, finish4, hook, s_tbl, lane_const, row_blocks, s_aslot[wave], xl, (gq_t)gate);
     }
     return;
   }
@@ -1081,9 +1203,11 @@ decode_down_kernel(const ExpertTable tab, const DecodeRoute *__restrict__ route,
   auto hook = [&]() {};
   const bool slow = s_rt.slow2 != 0;
   const int npairs = (ntl + 1) >> 1;
-  if (!slow && bc && nsq == 4) {
-    // Single token: units of two tiles (pair tp: tiles 2tp, 2tp+1) share the activation
-    // operand; the workgroup's units are shared through the work counter.
+  if (!slow && nsq == 4) {
+    // Units of two tiles (pair tp: tiles 2tp, 2tp+1) share the activation operand; the
+    // workgroup's units are shared through the work counter.  With BC (every active expert
+    // has one token) the lane holds a quarter of the token's chunk, else the whole chunk
+    // of its token row.
     const int n_pu = u * npairs * kparts;
     auto pair_fields = [&](int i, int &tp, int &kp) {
       kp = i % kparts;
@@ -1110,22 +1234,46 @@ decode_down_kernel(const ExpertTable tab, const DecodeRoute *__restrict__ route,
         P.wa[q] = (ga_t)s_eptr[e][1] + row * row_blocks + s_lo * 8 + (blk >> 1);
         P.ab[q] = (ga_t)s_eptr[e][1] + (size_t)(r0 + tl) * 4 * row_blocks + s_lo * 8;
       }
-      P.ap = (gx_t)h + (size_t)s_rt.offsets[a] * F + (size_t)s_lo * kStageVals + blk * 32 + lanej * 8;
+      const int jj = (!bc && lanej < s_rt.counts[a]) ? lanej : 0;
+      P.ap = (gx_t)h + (size_t)(s_rt.offsets[a] + jj) * F + (size_t)s_lo * kStageVals + blk * 32 +
+             (bc ? lanej * 8 : 0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) P.xo[i] = 0;  // unused (activations from global memory)
     };
-    auto finish2 = [&](f32x4 (&ac)[2], int i) {
-      const float v0 = lanes_sum16(ac[0][0]);
-      const float v1 = lanes_sum16(ac[1][0]);
+    // nrows: result rows that hold tokens (1 with BC, whose stream accumulates row 0 only).
+    auto finish2 = [&](f32x4 (&ac)[2], int i, int nrows) {
+      float v0[4], v1[4];
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        if (m < nrows) {
+          v0[m] = lanes_sum16(ac[0][m]);
+          v1[m] = lanes_sum16(ac[1][m]);
+        }
+      }
       if (blk == 0) {
         int tp, kp;
         const int a = pair_fields(i, tp, kp);
-        s_part[2 * tp][a][kp][lanej * 4] = v0;
-        if (2 * tp + 1 < ntl) s_part[2 * tp + 1][a][kp][lanej * 4] = v1;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          if (m < nrows) {
+            s_part[2 * tp][a][kp][lanej * 4 + m] = v0[m];
+            if (2 * tp + 1 < ntl) s_part[2 * tp + 1][a][kp][lanej * 4 + m] = v1[m];
+          }
+        }
       }
     };
     const uint32_t lane_const2[2] = {(uint32_t)lane << 2, (uint32_t)lane << 2};
-    stream_aligned<2, 4, 4, true, false, kLookahead>(grab, set_ptrs2, finish2, hook, s_tbl,
-                                                     lane_const2, row_blocks, s_aslot[wave], (gx_t)nullptr,
-                                                     (gq_t)h);
+    if (bc) {
+      auto fin = [&](f32x4 (&ac)[2], int i) { finish2(ac, i, 1); };
+      stream_aligned<2, 4, 4, true, kXGlobal, kLookahead>(grab, set_ptrs2, fin, hook, s_tbl,
+                                                       lane_const2, row_blocks, s_aslot[wave],
+                                                       (gx_t)nullptr, (gq_t)h);
+    } else {
+      auto fin = [&](f32x4 (&ac)[2], int i) { finish2(ac, i, 4); };
+      stream_aligned<2, 4, 4, false, kXGlobal, kLookahead>(grab, set_ptrs2, fin, hook, s_tbl,
+                                                        lane_const2, row_blocks, s_aslot[wave],
+                                                        (gx_t)nullptr, (gq_t)h);
+    }
   } else {
     // Each wave takes a contiguous part of the units.
     const int i0 = wave * n_units / kDecWaves;
