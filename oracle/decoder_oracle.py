@@ -143,14 +143,18 @@ class RefDecoder:
         return h + self._moe(L, rmsnorm(h, L["post"], s.rms_eps))
 
     @torch.no_grad()
-    def layer_parts(self, li: int, h: torch.Tensor, resid: torch.Tensor = None):
+    def layer_parts(self, li: int, h: torch.Tensor, resid: torch.Tensor = None, moe: bool = True):
         """Layer li split at its residual add, teacher-forced: the attention block's output
         for input h [T, H] at the current position (keys/values appended), and the MoE
         block's output (with its routing) on post_norm(resid), where resid is the caller's
         post-attention residual stream (default bf16(h + attention)).  Does not advance the
-        position.  Returns (attention [T, H], moe [T, H] bf16, (logits, w, idx))."""
+        position.  Returns (attention [T, H], moe [T, H] bf16, (logits, w, idx)); with
+        moe=False only the attention block runs (the key/value rows of a pass that is not
+        checked) and the last two are None."""
         s, L = self.s, self.layers[li]
         attn = self._attention(li, L, rmsnorm(h, L["inn"], s.rms_eps))
+        if not moe:
+            return attn, None, None
         if resid is None:
             resid = h + attn
         x2 = rmsnorm(resid, L["post"], s.rms_eps)

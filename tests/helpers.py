@@ -115,3 +115,33 @@ def assert_weights_close(w_got, w_want, lg_got_bits, lg_want_bits, rtol=1e-5, at
                 orc.bf16_to_f32(lg_want_bits).astype(np.float64)).max(axis=-1, keepdims=True)
     w_got, w_want = np.asarray(w_got, np.float64), np.asarray(w_want, np.float64)
     assert (np.abs(w_got - w_want) <= rtol * np.abs(w_want) + atol + 0.5 * dl).all()
+
+
+def record_parity(**fields) -> None:
+    """Appends one JSON line of measured parity figures (test, config, rel-L2, ...) to the
+    file named by $MOE_PARITY_LOG, when set; a no-op otherwise."""
+    import json
+    import os
+
+    path = os.environ.get("MOE_PARITY_LOG")
+    if not path:
+        return
+    with open(path, "a") as f:
+        f.write(json.dumps(fields, sort_keys=True) + "\n")
+
+
+def dequant_code_scaled(packed: np.ndarray, absmax: np.ndarray, numel: int, code=None) -> np.ndarray:
+    """float32 weights bf16(code[q]) * absmax[block] (an fp32 product, not rounded): the
+    effective weights of the decode, GEMV and mid-batch kernels, which round the codebook
+    value to bf16 and apply the block's absmax to fp32 partial sums.  A measuring device
+    for how much of a kernel's distance to the oracle (whose weights are
+    bf16(code * absmax), as the reference materialises them) comes from that weight form
+    rather than from summation order."""
+    code = orc.NF4_CODE if code is None else np.asarray(code, dtype=np.float32)
+    cb = orc.bf16_to_f32(orc.bf16_round(code))
+    p = np.asarray(packed, dtype=np.uint8).reshape(-1)
+    q = np.empty(2 * p.size, dtype=np.uint8)
+    q[0::2] = p >> 4
+    q[1::2] = p & 15
+    blk = np.repeat(np.asarray(absmax, dtype=np.float32).reshape(-1), orc.NF4_BLOCKSIZE)
+    return (cb[q[:numel]] * blk[:numel]).astype(np.float32)
