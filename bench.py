@@ -59,6 +59,10 @@ def parse_args():
     p.add_argument("--cache-policy", choices=["lru", "lfu", "arc"], default="lru",
                    help="offload mode's GPU-tier eviction policy (the reference's default: lru)")
     p.add_argument("--prefetch-depth", type=int, default=2)
+    p.add_argument("--copy-timeline", action="store_true",
+                   help="offload mode: time every host-to-device copy and every MoE layer's "
+                        "expert kernels with HIP events in the timed run, and report the host "
+                        "link's busy share and the copy/compute overlap over the decode steps")
     p.add_argument("--prefetch-prefix-mib", type=float, default=8.0,
                    help="offload mode with --prefetch next_router: copy only this many MiB of "
                         "each guessed expert ahead (a bounded prefix); 0: the whole image")
@@ -408,6 +412,11 @@ def _e2e(args) -> int:
     warm_s = time.time() - t_w
     # Timed: prefill (ttft), then exactly Ksteps decode steps between two synchronizations.
     copies0 = dict(eng.transfer_scheduler.copies) if args.offload else None
+    timeline = None
+    if args.offload and args.copy_timeline:
+        timeline = eng.transfer_scheduler.timeline = []
+        t_base = torch.cuda.Event(enable_timing=True)
+        t_base.record()
     res = eng.generate(ForwardRequest(prompt, max_new_tokens=Ksteps + 1))
     decode_ms = res.stage_timings["decode"]
     ms_per_step = decode_ms / Ksteps
@@ -499,8 +508,35 @@ def _e2e(args) -> int:
             "execute_next_staging_ms_max": round(max(staging), 4) if staging else None,
             "prefetch": None if pe is None else dict(pe.counts),
         }
+        if timeline is not None:
+            eng.transfer_scheduler.timeline = None
+            result["offload_stats"]["timeline"] = _copy_timeline(timeline, t_base, s.layers, Ksteps)
     print(json.dumps(result), flush=True)
     return 0
+
+
+def _copy_timeline(timeline, t_base, layers: int, steps: int) -> dict:
+    """Host-link and MoE-kernel intervals of the timed offload run (HIP events on the
+    transfer and compute streams, in ns from t_base), summarised over its decode steps: the
+    window runs from the end of the prompt pass's last MoE layer to the end of the last
+    step's.  See moeinfra_amd.profiling.interval_stats."""
+    import torch
+
+    from moeinfra_amd import profiling
+
+    torch.cuda.synchronize()
+    ns = lambda ev: int(round(t_base.elapsed_time(ev) * 1e6))
+    copies = [(ns(a), ns(b), int(n)) for kind, a, b, n in timeline if kind != "moe"]
+    moe = [(ns(a), ns(b)) for kind, a, b, _ in timeline if kind == "moe"]
+    if len(moe) != layers * (steps + 1):
+        raise RuntimeError(f"timeline holds {len(moe)} MoE layers, expected {layers * (steps + 1)}")
+    lo, hi = moe[layers - 1][1], moe[-1][1]
+    stats = profiling.interval_stats(copies, moe, lo, hi, steps)
+    stats = {k.replace("kernel", "moe_kernel"): round(v, 4) for k, v in stats.items()}
+    stats["note"] = ("HIP events: each host-to-device copy on the transfer stream, each MoE layer's "
+                     "expert kernels (permute, gate/up, down, combine) on the compute stream; "
+                     "moe_kernel_* counts only those kernels")
+    return stats
 
 
 class _HipEvents:

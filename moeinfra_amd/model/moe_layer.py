@@ -161,8 +161,15 @@ class MoELayer:
             if self._workspace is None or self._workspace.numel() < need or \
                     self._workspace.device != x.device:
                 self._workspace = torch.empty((need,), dtype=torch.uint8, device=x.device)
+            tl = getattr(self.transfer_scheduler, "timeline", None)
+            if tl is not None:
+                k0, k1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                k0.record()
             out, _, _, idx = ops.layer_forward(table, E, router.gate_weight.contiguous(), x, k,
                                                inter, bias=router.bias, workspace=self._workspace)
+            if tl is not None:
+                k1.record()
+                tl.append(("moe", k0, k1, self.layer_id))
             self.last_expert_indices = idx
             return out
         return self._forward_offload(x)
@@ -187,9 +194,17 @@ class MoELayer:
             first = next(iter(experts.values()))
             table = ops.expert_table([experts[e].c_struct() if e in experts else None
                                       for e in range(E)])
+            tl = getattr(self.transfer_scheduler, "timeline", None)
+            if tl is not None:           # the expert kernels start once the copies have landed
+                k0, k1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                k0.record()
             route = ops.permute(idx32, E)
             _, ypart = ops.expert_ffn(table, E, x, k, x.shape[1], first.intermediate_size, route)
-            return ops.combine(ypart, w, idx32, route["slot_pos"])
+            out = ops.combine(ypart, w, idx32, route["slot_pos"])
+            if tl is not None:
+                k1.record()
+                tl.append(("moe", k0, k1, self.layer_id))
+            return out
         finally:
             if not self.retain_transferred:
                 for e in unique:

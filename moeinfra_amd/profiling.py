@@ -12,8 +12,16 @@ launches, average duration and share of the busy time.
 min duration per kernel and grid over the whole trace (optionally only names containing
 SUBSTR).
 
-Only the ``kernels`` view of the database is read (columns name, grid_x, start, end in
-nanoseconds).
+``python -m moeinfra_amd.profiling copies DB [N] [MIN_MIB]`` (a run traced with
+``--kernel-trace --memory-copy-trace``, e.g. ``bench.py --offload``) prints, over the last N
+decode steps, the host-to-device copies of at least MIN_MIB MiB (default 1): count, bytes,
+the time the host link is busy with at least one of them (union of their intervals) as a
+share of the steps' wall time, the rate while busy, and how much of that copy time a
+kernel runs alongside (copy/compute overlap).
+
+Only the ``kernels`` view (columns name, grid_x, start, end in nanoseconds) and, for
+``copies``, the ``memory_copies`` view (start, end, size, src_agent_type, dst_agent_type)
+of the database are read.
 """
 from __future__ import annotations
 
@@ -89,7 +97,97 @@ def kernel_table(launches: Sequence[Launch], substr: str = "") -> List[Tuple[str
     return rows
 
 
+Copy = Tuple[int, int, int]  # (start ns, end ns, bytes)
+
+
+def read_h2d_copies(db_path: str, min_bytes: int = 1 << 20) -> List[Copy]:
+    """Host-to-device copies of at least min_bytes, by start time."""
+    con = sqlite3.connect(db_path)
+    try:
+        rows = con.execute("select start, end, size, src_agent_type, dst_agent_type from memory_copies "
+                           "order by start").fetchall()
+    finally:
+        con.close()
+    return [(int(a), int(b), int(n)) for a, b, n, src, dst in rows
+            if str(src).upper() == "CPU" and str(dst).upper() == "GPU" and int(n) >= min_bytes]
+
+
+def _union(iv: Sequence[Tuple[int, int]]) -> List[Tuple[int, int]]:
+    out: List[Tuple[int, int]] = []
+    for a, b in sorted(iv):
+        if out and a <= out[-1][1]:
+            out[-1] = (out[-1][0], max(out[-1][1], b))
+        else:
+            out.append((a, b))
+    return out
+
+
+def _overlap(u: Sequence[Tuple[int, int]], v: Sequence[Tuple[int, int]]) -> int:
+    """Total length of the intersection of two sorted disjoint interval lists."""
+    i = j = tot = 0
+    while i < len(u) and j < len(v):
+        a, b = max(u[i][0], v[j][0]), min(u[i][1], v[j][1])
+        if a < b:
+            tot += b - a
+        if u[i][1] < v[j][1]:
+            i += 1
+        else:
+            j += 1
+    return tot
+
+
+def interval_stats(copies: Sequence[Copy], compute: Sequence[Tuple[int, int]], lo: int, hi: int,
+                   steps: int) -> Dict[str, float]:
+    """Host-link use inside the window [lo, hi) (nanoseconds) that holds `steps` decode
+    steps: copies (start, end, bytes) and compute intervals are clipped to the window (a
+    clipped copy keeps its share of the bytes); the link is busy while at least one copy
+    runs.  Returns per-step figures, the busy share of the wall time, the rate while busy,
+    and the share of copy time during which compute runs (and vice versa)."""
+    clip = lambda a, b: (max(a, lo), min(b, hi))
+    cp = [(clip(a, b), n * (min(b, hi) - max(a, lo)) / max(1, b - a)) for a, b, n in copies
+          if b > lo and a < hi]
+    cu = _union([iv for iv, _ in cp])
+    ku = _union([clip(a, b) for a, b in compute if b > lo and a < hi])
+    busy = sum(b - a for a, b in cu)
+    kbusy = sum(b - a for a, b in ku)
+    moved = sum(n for _, n in cp)
+    both = _overlap(cu, ku)
+    wall = hi - lo
+    return {
+        "steps": float(steps),
+        "wall_ms_per_step": wall / 1e6 / steps,
+        "copies_per_step": len(cp) / steps,
+        "mb_per_step": moved / 1e6 / steps,
+        "link_busy_frac": busy / wall if wall else 0.0,
+        "gbps_while_busy": moved / busy if busy else 0.0,
+        "gbps_over_wall": moved / wall if wall else 0.0,
+        "kernel_busy_frac": kbusy / wall if wall else 0.0,
+        "copy_time_with_kernel_frac": both / busy if busy else 0.0,
+        "kernel_time_with_copy_frac": both / kbusy if kbusy else 0.0,
+    }
+
+
+def copy_table(launches: Sequence[Launch], copies: Sequence[Copy], last: int | None = None) -> Dict[str, float]:
+    """Host-link use over the last `last` decode steps (all complete steps if None): the
+    window runs from the first kernel of the first of those steps to the end of the last;
+    the compute intervals are every kernel's."""
+    steps = split_steps(launches, last)
+    if not steps:
+        raise ValueError(f"no complete decode step (no two {STEP_END_KERNEL} launches) in the trace")
+    return interval_stats(copies, [(a, b) for _, _, a, b in launches], steps[0][0][2],
+                          steps[-1][-1][3], len(steps))
+
+
 def _main(argv: Sequence[str]) -> int:
+    if len(argv) >= 2 and argv[0] == "copies":
+        last = int(argv[2]) if len(argv) > 2 else None
+        min_mib = float(argv[3]) if len(argv) > 3 else 1.0
+        t = copy_table(read_launches(argv[1]), read_h2d_copies(argv[1], int(min_mib * (1 << 20))), last)
+        print("| quantity | value |")
+        print("|---|---:|")
+        for k, v in t.items():
+            print(f"| {k} | {v:.4g} |")
+        return 0
     if len(argv) < 2 or argv[0] not in ("steps", "kernels"):
         print(__doc__)
         return 2

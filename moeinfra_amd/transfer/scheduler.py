@@ -80,6 +80,10 @@ class TransferScheduler:
         self._queued: dict[str, TransferRequest] = {}
         self._busy: dict[tuple, str] = {}          # (layer, expert, direction) -> request id
         self._async: dict[tuple[int, int], TransferHandle] = {}
+        #: When a list: each host-to-device copy appends (kind, start event, end event,
+        #: bytes) with timing events on the transfer stream ("image", "staged" or
+        #: "prefix"), for a timeline of the host link (observability; None costs nothing).
+        self.timeline: Optional[list] = None
         #: Copies issued so far, by source, and the bytes they moved over the host link
         #: ("prefix": bounded prefix copies, see start_prefix).
         self.copies = {"image": 0, "staged": 0, "prefix": 0, "bytes": 0}
@@ -210,11 +214,15 @@ class TransferScheduler:
             raise
         stream = self._transfer_stream
         timing = profile.get("_timing")
+        tl = self.timeline
         with torch.cuda.stream(stream):
             if fence is not None:
                 stream.wait_event(fence)
             if timing:
                 timing[0].record(stream)
+            if tl is not None:
+                t_start = torch.cuda.Event(enable_timing=True)
+                t_start.record(stream)
             if staging is None:                # the copy goes out before any host bookkeeping
                 region[done_bytes:].copy_(image[done_bytes:], non_blocking=True)
             else:
@@ -222,8 +230,10 @@ class TransferScheduler:
                 for f in layout.fields:
                     staged[f.projection][f.key].copy_(staging.tensors[f.projection][f.key],
                                                       non_blocking=True)
-            done = torch.cuda.Event(enable_timing=bool(timing))
+            done = torch.cuda.Event(enable_timing=bool(timing) or tl is not None)
             done.record(stream)
+        if tl is not None:
+            tl.append((profile["source"], t_start, done, layout.nbytes - done_bytes))
         views = layout.views(region)
         if staging is not None:
             self._staging_pool.mark_transfer_complete(staging, stream)
@@ -263,10 +273,17 @@ class TransferScheduler:
             return False
         region, fence, lease = slots.region(slot, layout.nbytes), slots.fence(slot), slots.lease(slot)
         stream = self._transfer_stream
+        tl = self.timeline
         with torch.cuda.stream(stream):
             if fence is not None:
                 stream.wait_event(fence)
+            if tl is not None:
+                t_start, t_end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                t_start.record(stream)
             region[:nbytes].copy_(image[:nbytes], non_blocking=True)
+            if tl is not None:
+                t_end.record(stream)
+                tl.append(("prefix", t_start, t_end, nbytes))
         self._prefixes[key] = (region, lease, nbytes)
         self.copies["prefix"] += 1
         self.copies["bytes"] += nbytes

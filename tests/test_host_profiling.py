@@ -48,3 +48,38 @@ def test_no_complete_step_is_an_error(tmp_path):
     launches = profiling.read_launches(_db(tmp_path, [("k()", 1, 0, 5)]))
     with pytest.raises(ValueError, match="argmax_finish_kernel"):
         profiling.step_table(profiling.split_steps(launches))
+
+
+def test_copy_table_by_hand(tmp_path):
+    """Two decode steps of 100 us; per step two 2 MB host-to-device copies, one entirely
+    under a kernel and one half under it, plus a small copy that is ignored."""
+    fin = "moe::(anonymous namespace)::argmax_finish_kernel(int)"
+    k = "void moe::(anonymous namespace)::decode_gateup_kernel<8, false>(moe::ExpertTable)"
+    p = tmp_path / "run_results.db"
+    con = sqlite3.connect(p)
+    con.execute("create table kernels (name text, grid_x int, start int, end int)")
+    con.execute("create table memory_copies (start int, end int, size int, src_agent_type text, "
+                "dst_agent_type text)")
+    kern = [(fin, 1, 0, 1_000)]
+    cps = []
+    for s in range(2):
+        t = 1_000 + 100_000 * s
+        kern += [(k, 256, t + 10_000, t + 50_000), (fin, 1, t + 95_000, t + 100_000)]
+        cps += [(t + 20_000, t + 40_000, 2_000_000, "CPU", "GPU"),   # under the kernel
+                (t + 40_000, t + 60_000, 2_000_000, "CPU", "GPU"),   # half under it
+                (t + 70_000, t + 71_000, 4096, "CPU", "GPU")]        # below the size floor
+    con.executemany("insert into kernels values (?, ?, ?, ?)", kern)
+    con.executemany("insert into memory_copies values (?, ?, ?, ?, ?)", cps)
+    con.commit()
+    con.close()
+    launches = profiling.read_launches(str(p))
+    copies = profiling.read_h2d_copies(str(p))
+    assert len(copies) == 4
+    t = profiling.copy_table(launches, copies)
+    assert t["steps"] == 2 and t["copies_per_step"] == 2
+    # window: first kernel of step 1 (t=11 us) to the end of step 2's finish (201 us)
+    wall = 201_000 - 11_000
+    assert t["link_busy_frac"] == pytest.approx(80_000 / wall)
+    assert t["gbps_while_busy"] == pytest.approx(8e6 / 80_000)
+    assert t["copy_time_with_kernel_frac"] == pytest.approx(60_000 / 80_000)
+    assert t["kernel_time_with_copy_frac"] == pytest.approx(60_000 / 90_000)
