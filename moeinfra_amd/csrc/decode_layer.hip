@@ -25,6 +25,8 @@
 //
 // Both kernels stream 4-row tiles through the register pipeline of the 4x4x4 MFMA GEMV
 // (gemv4_core.h), with the NF4 codebook table in LDS.
+#include <type_traits>
+
 #include "gemv4_core.h"
 #include "norm_row.h"
 
@@ -133,9 +135,9 @@ struct ItemPtr {
   gx_t ap;
   ga_t ab[NP];  // absmax of the item's first tile row at its first stage (aligned stream)
   // Activations staged in LDS (aligned stream, kXLds): the lane's 16-byte pieces of stage 0,
-  // in 16-byte units from the staging buffer's base (four pieces, one per token row of the
-  // lane, or one quarter with BC); stage s adds 64 s.
-  uint32_t xo[4];
+  // in 16-byte units from the staging buffer's base (four pieces per group of four token
+  // rows, the lane's row of each group, or one quarter with BC); stage s adds 64 s.
+  uint32_t xo[8];
 };
 
 // Where the aligned stream's activations come from.
@@ -313,7 +315,7 @@ __device__ __forceinline__ uint4 ld_x(const uint16_t *lds_p) {
   return *reinterpret_cast<const uint4 *>(lds_p);
 }
 
-template <int NP, int NSQ, int DEPTH, bool BC, int XM, bool LA, typename GrabFn,
+template <int NP, int NSQ, int DEPTH, bool BC, int XM, bool LA, int NG = 1, typename GrabFn,
           typename PtrFn, typename FinishFn, typename Hook, typename XPtr>
 __device__ __forceinline__ void stream_aligned(GrabFn &&grab, PtrFn &&set_ptrs,
                                                FinishFn &&finish, Hook &&hook,
@@ -324,9 +326,11 @@ __device__ __forceinline__ void stream_aligned(GrabFn &&grab, PtrFn &&set_ptrs,
   static_assert(DEPTH >= 2 && DEPTH <= NSQ && NSQ % DEPTH == 0, "depth must divide NSQ");
   static_assert(!LA || DEPTH >= 3, "lookahead needs depth >= 3");
   static_assert(XM != kXLds || LA, "LDS activations are read in the lookahead slot");
+  static_assert(NG == 1 || (XM == kXLds && !BC && NG <= 2), "token groups: LDS activations");
   constexpr bool XREG = XM == kXRegs;
   constexpr bool XLDS = XM == kXLds;
   constexpr int NX = XREG ? 1 : (BC ? 1 : 4);
+  constexpr int NXG = NX * NG;  // LDS activation pieces per lane and stage
   // First step that loads a stage of the next item.
   constexpr int kNext = NSQ - DEPTH + 1;
   const int lane = threadIdx.x & (kWave - 1);
@@ -372,16 +376,16 @@ __device__ __forceinline__ void stream_aligned(GrabFn &&grab, PtrFn &&set_ptrs,
       for (int i = 0; i < NX; ++i) st.xa[i] = ld_u4(px + 8 * i);
     }
   };
-  // kXLds: the current stage's activations (xc) and the next stage's (xn), read from LDS
-  // one step ahead; xoc holds the current item's piece offsets (P moves on to the next
-  // item at step kNext).
-  uint4 xc[XLDS ? NX : 1], xn[XLDS ? NX : 1];
-  uint32_t xoc[XLDS ? NX : 1];
-  auto lds_x = [&](uint4 (&dst)[XLDS ? NX : 1], const uint32_t (&xo)[XLDS ? NX : 1], int sg) {
+  // kXLds: the current stage's activations (xc), read from LDS right after the previous
+  // stage's products have used the registers; xoc holds the current item's piece offsets
+  // (P moves on to the next item at step kNext).
+  uint4 xc[XLDS ? NXG : 1];
+  uint32_t xoc[XLDS ? NXG : 1];
+  auto lds_x = [&](uint4 (&dst)[XLDS ? NXG : 1], const uint32_t (&xo)[XLDS ? NXG : 1], int sg) {
     if constexpr (XLDS) {
       const lx_t xl = (lx_t)xbase;
 #pragma unroll
-      for (int i = 0; i < NX; ++i) {
+      for (int i = 0; i < NXG; ++i) {
         const u32x4_t v = xl[xo[i] + 64 * sg];
         dst[i] = make_uint4(v.x, v.y, v.z, v.w);
       }
@@ -389,7 +393,7 @@ __device__ __forceinline__ void stream_aligned(GrabFn &&grab, PtrFn &&set_ptrs,
   };
   if constexpr (XLDS) {
 #pragma unroll
-    for (int i = 0; i < NX; ++i) xoc[i] = P.xo[i];
+    for (int i = 0; i < NXG; ++i) xoc[i] = P.xo[i];
     lds_x(xc, xoc, 0);
   }
   StageQ<NP, XM == kXGlobal ? NX : 0> st[DEPTH];
@@ -408,9 +412,10 @@ __device__ __forceinline__ void stream_aligned(GrabFn &&grab, PtrFn &&set_ptrs,
   ItemPtr<NP> Pn = P;
   if (nxt >= 0) set_ptrs(Pn, nxt);
 
-  f32x4 acc[NP];
+  // Per projection p and token group g: acc[p * NG + g].
+  f32x4 acc[NP * NG];
 #pragma unroll
-  for (int p = 0; p < NP; ++p) acc[p] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int p = 0; p < NP * NG; ++p) acc[p] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   s16x4 bq[LA ? NP : 1][8];
   if (LA) {
 #pragma unroll
@@ -447,42 +452,41 @@ __device__ __forceinline__ void stream_aligned(GrabFn &&grab, PtrFn &&set_ptrs,
       float scl[NP];
 #pragma unroll
       for (int p = 0; p < NP; ++p) scl[p] = aslot[p * kASlotFloats + j * kASlotRow + 8 * d + (blk >> 1)];
-      f32x4 t[NP];
+      f32x4 t[NP * NG];
 #pragma unroll
-      for (int p = 0; p < NP; ++p) t[p] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      for (int p = 0; p < NP * NG; ++p) t[p] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
       if (LA) {
         // Stage d+1 is in buffer (d+1) % DEPTH (for d = NSQ-1: the next item's stage 0, or
         // a re-read of this item's when it is the last one).
         const StageQ<NP, XM == kXGlobal ? NX : 0> &ns = st[(d + 1) % DEPTH];
-        if constexpr (XLDS) {
-          // Stage d + 1 of this item, or (d = NSQ - 1) stage 0 of the next one, whose
-          // pointers P holds since step kNext (the current item's again after the last).
-          if (d + 1 < NSQ) {
-            lds_x(xn, xoc, d + 1);
-          } else {
-            uint32_t xo_n[NX];
-#pragma unroll
-            for (int i = 0; i < NX; ++i) xo_n[i] = P.xo[i];
-            lds_x(xn, xo_n, 0);
-          }
-        }
         s16x4 bn[LA ? NP : 1][8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
 #pragma unroll
           for (int p = 0; p < NP; ++p) bn[p][i] = b_operand<false>(ns.q[p], i, tbl, lane_const[p], nullptr);
-          const s16x4 a = a_operand<BC>(xa, i);
 #pragma unroll
-          for (int p = 0; p < NP; ++p)
-            t[p] = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(a, bq[p][i], t[p], 0, 0, 0);
+          for (int g = 0; g < NG; ++g) {
+            const s16x4 a = a_operand<BC>(xa + g * NX, i);
+#pragma unroll
+            for (int p = 0; p < NP; ++p)
+              t[p * NG + g] = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(a, bq[p][i], t[p * NG + g], 0, 0, 0);
+          }
         }
 #pragma unroll
         for (int i = 0; i < 8; ++i)
 #pragma unroll
           for (int p = 0; p < NP; ++p) bq[p][i] = bn[p][i];
         if constexpr (XLDS) {
+          // Stage d + 1 of this item, or (d = NSQ - 1) stage 0 of the next one, whose
+          // pointers P holds since step kNext (the current item's again after the last).
+          if (d + 1 < NSQ) {
+            lds_x(xc, xoc, d + 1);
+          } else {
+            uint32_t xo_n[NXG];
 #pragma unroll
-          for (int i = 0; i < NX; ++i) xc[i] = xn[i];
+            for (int i = 0; i < NXG; ++i) xo_n[i] = P.xo[i];
+            lds_x(xc, xo_n, 0);
+          }
         }
       } else {
 #pragma unroll
@@ -496,20 +500,23 @@ __device__ __forceinline__ void stream_aligned(GrabFn &&grab, PtrFn &&set_ptrs,
       }
 #pragma unroll
       for (int p = 0; p < NP; ++p) {
-        if (BC)  // one token in every row: only row 0 is accumulated
-          acc[p][0] = fmaf(scl[p], t[p][0], acc[p][0]);
-        else
-          scale_acc(acc[p], t[p], scl[p]);
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+          if (BC)  // one token in every row: only row 0 is accumulated
+            acc[p][0] = fmaf(scl[p], t[p][0], acc[p][0]);
+          else
+            scale_acc(acc[p * NG + g], t[p * NG + g], scl[p]);
+        }
       }
     }
     finish(acc, cur);
 #pragma unroll
-    for (int p = 0; p < NP; ++p) acc[p] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int p = 0; p < NP * NG; ++p) acc[p] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     if (nxt < 0) break;
     store_abs();
     if constexpr (XLDS) {
 #pragma unroll
-      for (int i = 0; i < NX; ++i) xoc[i] = P.xo[i];
+      for (int i = 0; i < NXG; ++i) xoc[i] = P.xo[i];
     }
     cur = nxt;
     nxt = nxt2;
@@ -534,16 +541,26 @@ __device__ __forceinline__ void build_table_regs(uint32_t *tbl, const float (&c_
   const bool second = (tid & 8) != 0;  // replica 4*(tid%16) >= 32
   const int lo_nib = (tid >> 4) & 15;
   const int hi0 = tid >> 8;  // < HS
-  float lo = c_a[0];
+  // Selections on values (each array element read with a constant index), so that two
+  // different codebooks never turn into a select between the arrays themselves.
+  float lo_a = c_a[0], lo_b = c_b[0];
 #pragma unroll
-  for (int i = 0; i < 16; ++i)
-    if (i == lo_nib) lo = second ? c_b[i] : c_a[i];
+  for (int i = 1; i < 16; ++i) {
+    const float va = c_a[i], vb = c_b[i];
+    lo_a = i == lo_nib ? va : lo_a;
+    lo_b = i == lo_nib ? vb : lo_b;
+  }
+  const float lo = second ? lo_b : lo_a;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    float hi = second ? c_b[HS * r] : c_a[HS * r];
+    float hi_a = c_a[HS * r], hi_b = c_b[HS * r];
 #pragma unroll
-    for (int h = 1; h < HS; ++h)
-      if (hi0 == h) hi = second ? c_b[HS * r + h] : c_a[HS * r + h];
+    for (int h = 1; h < HS; ++h) {
+      const float va = c_a[HS * r + h], vb = c_b[HS * r + h];
+      hi_a = hi0 == h ? va : hi_a;
+      hi_b = hi0 == h ? vb : hi_b;
+    }
+    const float hi = second ? hi_b : hi_a;
     const uint32_t w = pack_bf16x2(hi, lo);
     *reinterpret_cast<uint4 *>(tbl + 4 * (tid + NT * r)) = make_uint4(w, w, w, w);
   }
@@ -983,7 +1000,7 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
     // The LDS copy: with BC quarter lanej of the token's chunk blk, else the whole chunk
     // of the lane's token row (the expert's first token again past its count).
 #pragma unroll
-    for (int i = 0; i < 4; ++i) P.xo[i] = xlds_piece(tok, H, 4 * blk + (bc ? lanej : i));
+    for (int i = 0; i < 8; ++i) P.xo[i] = xlds_piece(tok, H, 4 * blk + (bc ? lanej : (i & 3)));
   };
   // nrows: MFMA result rows that hold tokens (1 on the single-token path, whose other rows
   // are never accumulated).
@@ -1238,7 +1255,7 @@ decode_down_kernel(const ExpertTable tab, const DecodeRoute *__restrict__ route,
       P.ap = (gx_t)h + (size_t)(s_rt.offsets[a] + jj) * F + (size_t)s_lo * kStageVals + blk * 32 +
              (bc ? lanej * 8 : 0);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) P.xo[i] = 0;  // unused (activations from global memory)
+      for (int i = 0; i < 8; ++i) P.xo[i] = 0;  // unused (activations from global memory)
     };
     // nrows: result rows that hold tokens (1 with BC, whose stream accumulates row 0 only).
     auto finish2 = [&](f32x4 (&ac)[2], int i, int nrows) {
@@ -1328,6 +1345,164 @@ decode_down_kernel(const ExpertTable tab, const DecodeRoute *__restrict__ route,
   }
 }
 
+// Gate/up of mid-size batches (5 to 16 tokens, after the stand-alone routing and
+// grouping): the decode stream with one "virtual expert" per workgroup.  An active expert
+// with cnt routed rows is ceil(cnt / 8) virtual experts of up to 8 consecutive rows.  The
+// workgroups are dealt to the virtual experts in equal shares (grid / V each, V <= grid),
+// and each takes an equal share of its virtual expert's 4-row tiles; so a workgroup holds
+// one set of <= 8 token rows, which it stages in LDS once (swizzled as xlds_piece lays
+// out), and one expert, whose own w1 / w3 codebooks it builds its lookup table from.  The
+// waves share the tiles through the work counter and stream them through the aligned
+// pipeline, the rows in one or two groups of four MFMA rows; h rows are written as
+// h = bf16(silu(bf16(w1 x)) * bf16(w3 x)) (transfer/nf4_reconstruct.py:152-155 on the rows
+// model/moe_layer.py:174-186 gathers).
+constexpr int kMidRows = 8;       // rows of a virtual expert
+constexpr int kMidMaxH = 4096;
+
+template <int NSQ>
+__global__ void __launch_bounds__(kDecThreads, 1)
+mid_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x, int H, int F, int E,
+                  const Route rt, uint16_t *__restrict__ h_out) {
+  __shared__ __attribute__((aligned(16))) uint32_t s_tbl[kTableWords];
+  __shared__ uint4 s_xt[kMidRows * kMidMaxH / 8];
+  __shared__ __attribute__((aligned(16))) float s_aslot[kDecWaves][2 * kASlotFloats];
+  __shared__ int32_t s_ticket;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  if (tid == 0) s_ticket = 0;
+
+  // Virtual experts of every active expert (lane e holds expert e), counted in every wave.
+  // An absent expert (null pointers; the caller routes no token to it) counts no rows.
+  const int cnt = (lane < E && tab.e[lane < E ? lane : 0].w1_packed != nullptr) ? rt.counts[lane] : 0;
+  const int off = lane < E ? rt.offsets[lane] : 0;
+  const int nv = (cnt + kMidRows - 1) / kMidRows;
+  int incl = nv;
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const int t = __shfl_up(incl, o);
+    if (lane >= o) incl += t;
+  }
+  const int V = __builtin_amdgcn_readlane(incl, kWave - 1);
+  if (V == 0) return;  // uniform over the grid
+  const int G = gridDim.x, b = blockIdx.x;
+  const int v = (int)((int64_t)b * V / G);
+  const int b0 = (int)(((int64_t)v * G + V - 1) / V);
+  const int b1 = (int)(((int64_t)(v + 1) * G + V - 1) / V);
+  // The expert holding virtual expert v: the lowest lane whose inclusive count exceeds v.
+  const int e = __builtin_ctzll(__ballot(incl > v));
+  const int vj = v - (__builtin_amdgcn_readlane(incl, e) - __builtin_amdgcn_readlane(nv, e));
+  const int r0 = __builtin_amdgcn_readlane(off, e) + kMidRows * vj;  // first h row
+  const int n = min(kMidRows, __builtin_amdgcn_readlane(cnt, e) - kMidRows * vj);
+  const int tiles = F >> 2;
+  const int t_lo = (int)((int64_t)(b - b0) * tiles / (b1 - b0));
+  const int t_hi = (int)((int64_t)(b - b0 + 1) * tiles / (b1 - b0));
+
+  // Token ids of the rows (lanes 0..n-1 of every wave), the expert's codebooks and stream
+  // pointers (wave-uniform: scalar loads).
+  const int my_tok = lane < n ? rt.perm_tok[r0 + lane] : 0;
+  const moe_nf4_expert_t &ex = tab.e[e];
+  const float *c1 = (const float *)uniform_ptr(ex.w1_code);
+  const float *c3 = (const float *)uniform_ptr(ex.w3_code);
+  const void *pk[2] = {uniform_ptr(ex.w1_packed), uniform_ptr(ex.w3_packed)};
+  const void *pa[2] = {uniform_ptr(ex.w1_absmax), uniform_ptr(ex.w3_absmax)};
+  float ca[16], cb[16];
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    ca[q] = c1[q];
+    cb[q] = c3[q];
+  }
+  // The rows' tokens into LDS: piece q of the n x H block, row q / (H / 8).
+  const int ppr = H >> 3;  // 16-byte pieces per row
+  constexpr int kPer = kMidRows * kMidMaxH / 8 / kDecThreads;
+  uint4 xv[kPer];
+#pragma unroll
+  for (int r = 0; r < kPer; ++r) {
+    const int q = tid + kDecThreads * r;
+    const int m = q / ppr;
+    const int tok = __shfl(my_tok, m < kMidRows ? m : 0);
+    if (m < n) xv[r] = ld_u4((gx_t)x + (size_t)tok * H + (size_t)(q - m * ppr) * 8);
+  }
+  // Lookup table from the expert's codebooks: replicas 0-31 w1, 32-63 w3.
+  build_table_regs<kDecThreads>(s_tbl, ca, cb);
+#pragma unroll
+  for (int r = 0; r < kPer; ++r) {
+    const int q = tid + kDecThreads * r;
+    const int m = q / ppr;
+    if (m < n) s_xt[xlds_piece(m, H, q - m * ppr)] = xv[r];
+  }
+  __syncthreads();
+
+  const int lanej = lane & 3;
+  const int blk = lane >> 2;
+  const size_t row_bytes = (size_t)(H >> 1);
+  const size_t row_blocks = (size_t)(H >> 6);
+  const uint32_t lane_const[2] = {(uint32_t)(lane & 31) << 2, ((uint32_t)(lane & 31) << 2) | 128u};
+  auto grab = [&]() -> int {
+    int t = 0;
+    if (lane == 0) t = __hip_atomic_fetch_add(&s_ticket, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    t = __builtin_amdgcn_readfirstlane(t) + t_lo;
+    return t < t_hi ? t : -1;
+  };
+  const bool bc = n == 1;
+  auto set_ptrs = [&](ItemPtr<2> &P, int tile) {
+    const size_t row = (size_t)tile * 4 + lanej;
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      P.wq[p] = (gq_t)pk[p] + row * row_bytes + blk * 16;
+      P.wa[p] = (ga_t)pa[p] + row * row_blocks + (blk >> 1);
+      P.ab[p] = (ga_t)pa[p] + (size_t)tile * 4 * row_blocks;
+    }
+    P.ap = (gx_t)x;
+    // With BC quarter lanej of row 0's chunk blk; else the whole chunk of the lane's row in
+    // each group of four (row 0 again past the count).
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int m = 4 * (i >> 2) + lanej;
+      P.xo[i] = bc ? xlds_piece(0, H, 4 * blk + lanej)
+                   : xlds_piece(m < n ? m : 0, H, 4 * blk + (i & 3));
+    }
+  };
+  auto finish = [&](auto &ac, int tile, auto ng_tag) {
+    constexpr int NGF = decltype(ng_tag)::value;
+    const int nrows = bc ? 1 : 4;
+    float vs[2][NGF][4];
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+#pragma unroll
+      for (int g = 0; g < NGF; ++g)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (q < nrows) vs[p][g][q] = lanes_sum16(ac[p * NGF + g][q]);
+    if (blk == 0) {
+      const int row = tile * 4 + lanej;
+#pragma unroll
+      for (int g = 0; g < NGF; ++g)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int m = 4 * g + q;
+          if (q < nrows && m < n) h_out[(size_t)(r0 + m) * F + row] = swiglu_bf16(vs[0][g][q], vs[1][g][q]);
+        }
+    }
+  };
+  auto hook = [&]() {};
+  const uint16_t *xl = reinterpret_cast<const uint16_t *>(s_xt);
+  if (bc) {
+    auto fin = [&](f32x4 (&ac)[2], int i) { finish(ac, i, std::integral_constant<int, 1>{}); };
+    stream_aligned<2, NSQ, kGateUpDepth, true, kXLds, true, 1>(
+        grab, set_ptrs, fin, hook, s_tbl, lane_const, row_blocks, s_aslot[wave], xl, (gq_t)x);
+  } else if (n <= 4) {
+    auto fin = [&](f32x4 (&ac)[2], int i) { finish(ac, i, std::integral_constant<int, 1>{}); };
+    stream_aligned<2, NSQ, kGateUpDepth, false, kXLds, true, 1>(
+        grab, set_ptrs, fin, hook, s_tbl, lane_const, row_blocks, s_aslot[wave], xl, (gq_t)x);
+  } else {
+    auto fin = [&](f32x4 (&ac)[4], int i) { finish(ac, i, std::integral_constant<int, 2>{}); };
+    stream_aligned<2, NSQ, kGateUpDepth, false, kXLds, true, 2>(
+        grab, set_ptrs, fin, hook, s_tbl, lane_const, row_blocks, s_aslot[wave], xl, (gq_t)x);
+  }
+}
+
 }  // namespace
 
 // One workgroup per CU: each owns ceil(tiles / CUs) 4-row output tiles of the down GEMV.
@@ -1356,6 +1531,31 @@ bool decode_layer_supported(int64_t T, int32_t k, int32_t E, int32_t H, int32_t 
 }
 
 int64_t decode_route_bytes() { return (int64_t)sizeof(DecodeRoute); }
+
+// The mid-size gate/up path: up to 16 tokens (at most two virtual experts per expert),
+// hidden size 2048 or 4096 (four or eight pipeline stages per row), at most 32 experts.
+bool mid_gateup_supported(int64_t T, int32_t k, int32_t E, int32_t H, int32_t F) {
+  return T >= 1 && T <= 16 && k >= 1 && E >= 1 && E <= kWave / 2 && (H == 2048 || H == 4096) &&
+         F >= 4 && F % 4 == 0 && T * (int64_t)H * 2 >= 2048 &&
+         (int64_t)E + T * k / kMidRows + 1 <= device_cu_count();
+}
+
+int launch_mid_gateup(const void *tab_v, const void *x, int64_t T, int32_t k, int32_t H, int32_t F,
+                      int32_t E, const void *route_v, void *h_ws, hipStream_t s) {
+  MOE_REQUIRE(mid_gateup_supported(T, k, E, H, F), "shape not supported by the mid-size gate/up");
+  MOE_REQUIRE(((uintptr_t)x % 16) == 0, "x must be 16-byte aligned");
+  const ExpertTable &tab = *static_cast<const ExpertTable *>(tab_v);
+  const Route &rt = *static_cast<const Route *>(route_v);
+  const dim3 grid((unsigned)device_cu_count()), blk(kDecThreads);
+  if (H == 4096)
+    hipLaunchKernelGGL(mid_gateup_kernel<8>, grid, blk, 0, s, tab, (const uint16_t *)x, H, F, E,
+                       rt, (uint16_t *)h_ws);
+  else
+    hipLaunchKernelGGL(mid_gateup_kernel<4>, grid, blk, 0, s, tab, (const uint16_t *)x, H, F, E,
+                       rt, (uint16_t *)h_ws);
+  MOE_LAUNCH_CHECK();
+  return MOE_STATUS_OK;
+}
 int64_t decode_norm_bytes() { return (int64_t)sizeof(DecodeNorm); }
 
 // Workgroups of the gate/up kernel: one per CU at most; each takes an even share of the

@@ -453,6 +453,9 @@ int midbatch_splits(int64_t active_max, int32_t H, int32_t F);
 int launch_midbatch(const void *tab, const void *x, int64_t T, int64_t rows_total, int32_t H,
                     int32_t F, const void *route, void *h_ws, void *ypart, int32_t nsplit,
                     int phases, hipStream_t stream);
+bool mid_gateup_supported(int64_t T, int32_t k, int32_t E, int32_t H, int32_t F);
+int launch_mid_gateup(const void *tab, const void *x, int64_t T, int32_t k, int32_t H, int32_t F,
+                      int32_t E, const void *route, void *h_ws, hipStream_t s);
 
 // ypart planes a layer's down projection writes (the combine adds them): the streamed
 // mid-batch kernels split K of the down projection over workgroups when few experts would
@@ -508,6 +511,14 @@ int launch_expert_ffn(const moe_nf4_expert_t *experts, int32_t E, const void *x,
   if (nsplit == 1 && gemv4_supported(max_tokens_per_expert, H, F))
     return launch_gemv4(&tab, x, H, F, &rt, h_ws, ypart, phases, active_max, rows_total, fused,
                         stream);
+  // Mid-size batches (up to 16 tokens): gate/up as the decode stream with one virtual expert
+  // (<= 8 token rows of one expert, staged in LDS) per workgroup; the down projection takes
+  // the path chosen below.
+  if ((phases & 1) && fused == nullptr && mid_gateup_supported(T, k, E, H, F)) {
+    const int rc = launch_mid_gateup(&tab, x, T, k, H, F, E, &rt, h_ws, stream);
+    if (rc != MOE_STATUS_OK || !(phases & 2)) return rc;
+    phases &= ~1;
+  }
   // Many tokens per expert on average: the LDS-staged GEMM streams each weight tile once per
   // 128 tokens (the per-tile kernels below re-stream it every 16 or 32 tokens).
   if (fused == nullptr && rows_total >= kGemmMinRowsPerExpert * active_max &&

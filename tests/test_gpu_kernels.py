@@ -426,3 +426,60 @@ def test_layer_mid_batch_mixtral(cuda_device, T, skew):
     np.testing.assert_array_equal(idx.cpu().numpy()[ok], idx_o[ok])
     err = orc.rel_l2(orc.bf16_to_f32(bits(out)[ok]), orc.bf16_to_f32(want[ok]))
     assert err <= 1e-2, err
+
+
+# ------------------------------------------------------------------------------ mid-size gate/up
+# 5 to 16 tokens at hidden size 2048 or 4096: gate/up streams like the decode form, one
+# virtual expert (<= 8 rows of one expert, staged in LDS, lookup table from the expert's own
+# codebooks) per workgroup; an expert with more than 8 rows is two virtual experts.  Hidden
+# 2048 here (four stages per row; the Mixtral shape's eight are in the full-shape tests).
+def _check_layer(want, i_want, got, i_got, lg, bias=None):
+    tie = near_tie_rows(lg, bias=bias)
+    np.testing.assert_array_equal(i_got[~tie], i_want[~tie])
+    err = orc.rel_l2(orc.bf16_to_f32(got[~tie]), orc.bf16_to_f32(want[~tie]))
+    assert err <= 1e-2, err
+
+
+@pytest.mark.parametrize("H,F,E,T,seed,skew", [
+    (2048, 1024, 8, 5, 81, False),
+    (2048, 1536, 8, 12, 82, True),
+    (2048, 1024, 8, 16, 83, False),
+    (2048, 512, 4, 11, 84, False),     # four experts: most hold more than 4 rows, some > 8
+    (2048, 768, 16, 16, 85, True),
+])
+def test_layer_mid_gateup(cuda_device, H, F, E, T, seed, skew):
+    _check_layer(*_layer_case(cuda_device, H, F, E, T, seed, skew))
+
+
+def test_layer_mid_gateup_mixed_codebooks(cuda_device):
+    """Each workgroup builds its table from its own expert's w1 / w3 codebooks."""
+    codes = {e: (orc.NF4_CODE * np.float32(0.75 + 0.05 * e)).astype(np.float32)
+             for e in (1, 4, 6)}
+    _check_layer(*_layer_case(cuda_device, 2048, 1024, 8, 14, 86, codes=codes))
+
+
+@pytest.mark.parametrize("T", [9, 16])
+def test_layer_mid_gateup_hot_and_absent(cuda_device, T):
+    """One expert takes every token (+1e4 bias: 9 or 16 rows, two virtual experts, the
+    second of 1 or 8 rows) and one is absent from the table (-1e4: never routed)."""
+    from moeinfra_amd import ops
+    from moeinfra_amd._lib import MoeNf4Expert
+
+    H, F, E, hot, absent = 2048, 1024, 8, 2, 6
+    gate, experts, x = build_layer(H, F, E, T, 87 + T)
+    bias = torch.zeros(E, dtype=torch.float32)
+    bias[hot], bias[absent] = 1.0e4, -1.0e4
+    want, (lg_w, w_w, i_w) = oracle_layer(gate, experts, x, bias=bias)
+    assert (i_w == hot).any(axis=1).all() and not (i_w == absent).any()
+    structs = []
+    for e, ex in enumerate(experts):
+        if e == absent:
+            structs.append(MoeNf4Expert())
+        else:
+            ex.to(cuda_device)
+            structs.append(ex.c_struct())
+    table = ops.expert_table(structs)
+    out, _, w, idx = ops.layer_forward(table, E, gate.to(cuda_device), x.to(cuda_device), 2, F,
+                                       bias=bias.to(cuda_device))
+    torch.cuda.synchronize()
+    _check_layer(want, i_w, bits(out), idx.cpu().numpy(), lg_w, bias=bias.numpy())
