@@ -29,6 +29,18 @@ int launch_identity_route(int64_t T, int32_t *counts, int32_t *offsets, int32_t 
 int launch_reduce_splits(const float *ypart, int nsplit, int64_t numel, uint16_t *y,
                          hipStream_t stream);
 bool decode_layer_supported(int64_t T, int32_t k, int32_t E, int32_t H, int32_t F);
+bool mid_layer_supported(int64_t T, int32_t k, int32_t E, int32_t H, int32_t F);
+int launch_mid_layer_gateup(const moe_nf4_expert_t *experts, int32_t E, const void *x, int64_t T,
+                            int32_t k, int32_t H, int32_t F, void *h_ws, const void *route_out,
+                            hipStream_t stream);
+// Mirrors the layout of MidRouteOut (decode_layer.hip): eleven pointers.
+struct MidRouteArgs {
+  const void *gate;
+  const void *bias;
+  void *logits, *w, *idx64, *idx32, *counts, *offsets, *perm_tok, *slot_pos, *active;
+};
+static_assert(sizeof(MidRouteArgs) == 11 * sizeof(void *), "MidRouteOut layout");
+int64_t mid_route_out_bytes();
 int64_t decode_route_bytes();
 int launch_decode_layer(const moe_nf4_expert_t *experts, int32_t E, const void *gate,
                         const void *bias, const void *x, int64_t T, int32_t H, int32_t F,
@@ -178,9 +190,17 @@ int layer_forward(const moe_nf4_expert_t *experts, int32_t E, const void *gate_b
                                logits_bf16, weights_f32, idx_i64, at<void>(workspace, w.droute),
                                at<void>(workspace, w.h), s, ev, nullptr);
   if (ev) MOE_HIP_CHECK(hipEventRecord(ev[0], s));
+  const bool mid = mid_layer_supported(T, k, E, H, F);
   const bool small = route_small_supported(T, k);
   int rc;
-  if (small) {
+  if (mid) {
+    MOE_REQUIRE(mid_route_out_bytes() == (int64_t)sizeof(MidRouteArgs), "MidRouteOut layout");
+    // Routing and grouping inside the gate/up launch: events 0 and 1 back to back.
+    if (ev) MOE_HIP_CHECK(hipEventRecord(ev[1], s));
+    const MidRouteArgs ro{gate_bf16, bias_f32, logits_bf16, weights_f32, idx_i64, idx32, counts,
+                          offsets, perm_tok, slot_pos, active};
+    rc = launch_mid_layer_gateup(experts, E, x_bf16, T, k, H, F, at<void>(workspace, w.h), &ro, s);
+  } else if (small) {
     rc = launch_route_small(x_bf16, gate_bf16, bias_f32, T, H, E, k, logits_bf16, weights_f32,
                             idx_i64, idx32, counts, offsets, perm_tok, slot_pos, active, counter,
                             s);
@@ -191,11 +211,13 @@ int layer_forward(const moe_nf4_expert_t *experts, int32_t E, const void *gate_b
       rc = moe_permute(idx32, T, k, E, counts, offsets, perm_tok, slot_pos, active, s);
   }
   if (rc != MOE_STATUS_OK) return rc;
-  if (ev) MOE_HIP_CHECK(hipEventRecord(ev[1], s));
-  rc = launch_expert_ffn(experts, E, x_bf16, T, k, H, F, counts, offsets, perm_tok, active,
-                         at<void>(workspace, w.h), at<void>(workspace, w.ypart), w.nsplit, T, 1,
-                         s, nullptr);
-  if (rc != MOE_STATUS_OK) return rc;
+  if (!mid) {
+    if (ev) MOE_HIP_CHECK(hipEventRecord(ev[1], s));
+    rc = launch_expert_ffn(experts, E, x_bf16, T, k, H, F, counts, offsets, perm_tok, active,
+                           at<void>(workspace, w.h), at<void>(workspace, w.ypart), w.nsplit, T, 1,
+                           s, nullptr);
+    if (rc != MOE_STATUS_OK) return rc;
+  }
   if (ev) MOE_HIP_CHECK(hipEventRecord(ev[2], s));
   // The down projection can also fold the combine into its last workgroup (FusedCombine);
   // on MI355X the device-scope fences that needs cost more than the separate launch, so the

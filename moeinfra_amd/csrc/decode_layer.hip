@@ -137,7 +137,7 @@ struct ItemPtr {
   // Activations staged in LDS (aligned stream, kXLds): the lane's 16-byte pieces of stage 0,
   // in 16-byte units from the staging buffer's base (four pieces per group of four token
   // rows, the lane's row of each group, or one quarter with BC); stage s adds 64 s.
-  uint32_t xo[8];
+  uint32_t xo[16];
 };
 
 // Where the aligned stream's activations come from.
@@ -315,8 +315,8 @@ __device__ __forceinline__ uint4 ld_x(const uint16_t *lds_p) {
   return *reinterpret_cast<const uint4 *>(lds_p);
 }
 
-template <int NP, int NSQ, int DEPTH, bool BC, int XM, bool LA, int NG = 1, typename GrabFn,
-          typename PtrFn, typename FinishFn, typename Hook, typename XPtr>
+template <int NP, int NSQ, int DEPTH, bool BC, int XM, bool LA, int NG = 1, bool XFIX = false,
+          typename GrabFn, typename PtrFn, typename FinishFn, typename Hook, typename XPtr>
 __device__ __forceinline__ void stream_aligned(GrabFn &&grab, PtrFn &&set_ptrs,
                                                FinishFn &&finish, Hook &&hook,
                                                const uint32_t *tbl,
@@ -326,7 +326,7 @@ __device__ __forceinline__ void stream_aligned(GrabFn &&grab, PtrFn &&set_ptrs,
   static_assert(DEPTH >= 2 && DEPTH <= NSQ && NSQ % DEPTH == 0, "depth must divide NSQ");
   static_assert(!LA || DEPTH >= 3, "lookahead needs depth >= 3");
   static_assert(XM != kXLds || LA, "LDS activations are read in the lookahead slot");
-  static_assert(NG == 1 || (XM == kXLds && !BC && NG <= 2), "token groups: LDS activations");
+  static_assert(NG == 1 || (XM == kXLds && !BC && NG <= 4), "token groups: LDS activations");
   constexpr bool XREG = XM == kXRegs;
   constexpr bool XLDS = XM == kXLds;
   constexpr int NX = XREG ? 1 : (BC ? 1 : 4);
@@ -378,7 +378,8 @@ __device__ __forceinline__ void stream_aligned(GrabFn &&grab, PtrFn &&set_ptrs,
   };
   // kXLds: the current stage's activations (xc), read from LDS right after the previous
   // stage's products have used the registers; xoc holds the current item's piece offsets
-  // (P moves on to the next item at step kNext).
+  // (P moves on to the next item at step kNext).  XFIX: every item reads the same rows, so
+  // the first item's offsets serve all of them.
   uint4 xc[XLDS ? NXG : 1];
   uint32_t xoc[XLDS ? NXG : 1];
   auto lds_x = [&](uint4 (&dst)[XLDS ? NXG : 1], const uint32_t (&xo)[XLDS ? NXG : 1], int sg) {
@@ -481,6 +482,8 @@ __device__ __forceinline__ void stream_aligned(GrabFn &&grab, PtrFn &&set_ptrs,
           // pointers P holds since step kNext (the current item's again after the last).
           if (d + 1 < NSQ) {
             lds_x(xc, xoc, d + 1);
+          } else if (XFIX) {  // every item reads the same rows
+            lds_x(xc, xoc, 0);
           } else {
             uint32_t xo_n[NXG];
 #pragma unroll
@@ -514,7 +517,7 @@ __device__ __forceinline__ void stream_aligned(GrabFn &&grab, PtrFn &&set_ptrs,
     for (int p = 0; p < NP * NG; ++p) acc[p] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     if (nxt < 0) break;
     store_abs();
-    if constexpr (XLDS) {
+    if constexpr (XLDS && !XFIX) {
 #pragma unroll
       for (int i = 0; i < NXG; ++i) xoc[i] = P.xo[i];
     }
@@ -594,14 +597,23 @@ struct RouteSummary {
   uint32_t present;  // bit x: expert x has a slot
 };
 
-template <int EMAX, int NW>
-__device__ __forceinline__ RouteSummary route_wave(RouteHead &rh, int32_t (&sl_e)[kDecMaxSlots],
-                                           float (&sl_w)[kDecMaxSlots],
-                                           const float (*s_part)[kDecMaxTokens][EMAX],
-                                           const float *bias, int T, int E, int k,
-                                           uint16_t *logits_out) {
+// The per-token part of the routing, for tokens t0 + lane / 16 (those below T): lane
+// (t, e) sums expert e's NW wave partials s_part[w][t0 + t][e] in wave order, and lane j
+// of the row ends with choice j (expert my_win, renormalised weight my_wn), also stored at
+// slot (t0 + t) * k + j of sl_e / sl_w.
+struct RowRoute {
+  int my_win;
+  float my_wn;
+  bool valid, taken;
+};
+
+template <int EMAX, int NW, int TD>
+__device__ __forceinline__ RowRoute route_rows(int32_t *sl_e, float *sl_w,
+                                               const float (*s_part)[TD][EMAX], int t0,
+                                               const float *bias, int T, int E, int k,
+                                               uint16_t *logits_out) {
   const int lane = threadIdx.x & (kWave - 1);
-  const int t = lane >> 4;
+  const int t = t0 + (lane >> 4);
   const int e = lane & 15;
   const bool valid = t < T && e < E;
   float l = -INFINITY;
@@ -620,15 +632,16 @@ __device__ __forceinline__ RouteSummary route_wave(RouteHead &rh, int32_t (&sl_e
   bool taken = false;
   float wsum = 0.0f, my_w = 0.0f;
   int my_win = 0;
+  const int row = lane >> 4;
   for (int j = 0; j < k; ++j) {
     const bool cand = valid && !taken;
     const float best = row_max16(cand ? p : -1.0f);
     const uint64_t hit = __ballot(cand && p == best);
     const uint64_t any = __ballot(cand);
-    int win = __builtin_ctzll(((hit >> (16 * t)) & 0xffffull) | 0x10000ull);  // row's lowest
+    int win = __builtin_ctzll(((hit >> (16 * row)) & 0xffffull) | 0x10000ull);  // row's lowest
     // No lane equal to the maximum (NaN weights): the lowest untaken expert, as a strict
     // '>' scan starting from "no choice yet" picks.
-    if (win > 15) win = __builtin_ctzll(((any >> (16 * t)) & 0xffffull) | 0x10000ull);
+    if (win > 15) win = __builtin_ctzll(((any >> (16 * row)) & 0xffffull) | 0x10000ull);
     if (win > 15) win = 0;
     taken |= e == win;
     wsum += best;
@@ -642,6 +655,21 @@ __device__ __forceinline__ RouteSummary route_wave(RouteHead &rh, int32_t (&sl_e
     sl_e[t * k + e] = my_win;
     sl_w[t * k + e] = my_wn;
   }
+  return RowRoute{my_win, my_wn, valid, taken};
+}
+
+template <int EMAX, int NW>
+__device__ __forceinline__ RouteSummary route_wave(RouteHead &rh, int32_t (&sl_e)[kDecMaxSlots],
+                                           float (&sl_w)[kDecMaxSlots],
+                                           const float (*s_part)[kDecMaxTokens][EMAX],
+                                           const float *bias, int T, int E, int k,
+                                           uint16_t *logits_out) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const RowRoute rr = route_rows<EMAX, NW, kDecMaxTokens>(sl_e, sl_w, s_part, 0, bias, T, E, k,
+                                                          logits_out);
+  const int my_win = rr.my_win;
+  const float my_wn = rr.my_wn;
+  const bool valid = rr.valid, taken = rr.taken;
   if (T == 1) {
     // One token: its k slots have k distinct experts, so each active expert holds exactly
     // one slot, at the rank of its id among the chosen ones -- the same descriptor as the
@@ -1000,7 +1028,7 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
     // The LDS copy: with BC quarter lanej of the token's chunk blk, else the whole chunk
     // of the lane's token row (the expert's first token again past its count).
 #pragma unroll
-    for (int i = 0; i < 8; ++i) P.xo[i] = xlds_piece(tok, H, 4 * blk + (bc ? lanej : (i & 3)));
+    for (int i = 0; i < 16; ++i) P.xo[i] = xlds_piece(tok, H, 4 * blk + (bc ? lanej : (i & 3)));
   };
   // nrows: MFMA result rows that hold tokens (1 on the single-token path, whose other rows
   // are never accumulated).
@@ -1255,7 +1283,7 @@ decode_down_kernel(const ExpertTable tab, const DecodeRoute *__restrict__ route,
       P.ap = (gx_t)h + (size_t)(s_rt.offsets[a] + jj) * F + (size_t)s_lo * kStageVals + blk * 32 +
              (bc ? lanej * 8 : 0);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) P.xo[i] = 0;  // unused (activations from global memory)
+      for (int i = 0; i < 16; ++i) P.xo[i] = 0;  // unused (activations from global memory)
     };
     // nrows: result rows that hold tokens (1 with BC, whose stream accumulates row 0 only).
     auto finish2 = [&](f32x4 (&ac)[2], int i, int nrows) {
@@ -1359,24 +1387,188 @@ decode_down_kernel(const ExpertTable tab, const DecodeRoute *__restrict__ route,
 constexpr int kMidRows = 8;       // rows of a virtual expert
 constexpr int kMidMaxH = 4096;
 
-template <int NSQ>
+// The routing a mid-size gate/up launch computes itself (ROUTE): the gate, the optional
+// per-expert logit bias, and where workgroup 0 writes the router's outputs (logits may be
+// null) and the grouping the down projection and the combine read (the layout of
+// moe_permute: offsets [E + 1], active = {n, ids ascending}, slot_pos of every slot).
+struct MidRouteOut {
+  const uint16_t *gate;
+  const float *bias;
+  uint16_t *logits;
+  float *w;
+  int64_t *idx64;
+  int32_t *idx32;
+  int32_t *counts;
+  int32_t *offsets;
+  int32_t *perm_tok;
+  int32_t *slot_pos;
+  int32_t *active;
+};
+constexpr int kMidMaxT = 16;
+constexpr int kMidMaxSlots = kMidMaxT * 2;
+
+template <int NSQ, int EMAX, bool ROUTE>
 __global__ void __launch_bounds__(kDecThreads, 1)
-mid_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x, int H, int F, int E,
-                  const Route rt, uint16_t *__restrict__ h_out) {
+mid_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x, int T, int H, int F,
+                  int E, int k, const Route rt, const MidRouteOut ro, uint16_t *__restrict__ h_out) {
   __shared__ __attribute__((aligned(16))) uint32_t s_tbl[kTableWords];
+  // The staged token rows; before them (ROUTE) the waves' gate partials [wave][token][expert].
   __shared__ uint4 s_xt[kMidRows * kMidMaxH / 8];
   __shared__ __attribute__((aligned(16))) float s_aslot[kDecWaves][2 * kASlotFloats];
   __shared__ int32_t s_ticket;
+  // ROUTE: slot experts and weights, and the grouping (counts, offsets, sorted rows' tokens).
+  __shared__ int32_t s_sle[ROUTE ? kMidMaxSlots : 1];
+  __shared__ float s_slw[ROUTE ? kMidMaxSlots : 1];
+  __shared__ int32_t s_cnt[ROUTE ? kWave : 1], s_off[ROUTE ? kWave : 1];
+  __shared__ int32_t s_ptok[ROUTE ? kMidMaxSlots : 1];
+  static_assert(!ROUTE || kDecWaves * kMidMaxT * EMAX * 4 <= (int)sizeof(s_xt), "gate partials fit");
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   if (tid == 0) s_ticket = 0;
 
+  const int32_t *g_cnt = rt.counts, *g_off = rt.offsets, *g_ptok = rt.perm_tok;
+  // The lookup table from the NF4 codebook constants, built while the first loads are in
+  // flight; a workgroup whose expert has other codebooks rebuilds it below.
+  auto table_from_constants = [&]() {
+    float cst[16];
+#pragma unroll
+    for (int q = 0; q < 16; ++q) cst[q] = kNf4Code[q];
+    build_table_regs<kDecThreads>(s_tbl, cst, cst);
+  };
+  if constexpr (!ROUTE) table_from_constants();
+  if constexpr (ROUTE) {
+    // ---- gate products on the 4x4x4 MFMA: wave w takes the 128-value chunks w, w + 8, ...
+    // of H; lane (b = lane / 4, j = lane % 4) holds values 8b .. 8b+7 of a chunk of token
+    // 4q + j (A rows of token group q; tokens >= T repeat a valid row and are ignored) and of
+    // expert 4g + j (B columns).  A butterfly over the 16 blocks completes the wave's sums.
+    constexpr int G = EMAX / 4;
+    constexpr int Q = kMidMaxT / 4;
+    const int lj = lane & 3, lb = lane >> 2;
+    const int n_chunks = (H / 128 - wave + kDecWaves - 1) / kDecWaves;
+    gx_t xrow[Q], grow[G];
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+      const int t = 4 * q + lj;
+      xrow[q] = (gx_t)x + (size_t)(t < T ? t : T - 1) * H + (size_t)wave * 128 + 8 * lb;
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const int e = 4 * g + lj;
+      grow[g] = (gx_t)ro.gate + (size_t)(e < E ? e : E - 1) * H + (size_t)wave * 128 + 8 * lb;
+    }
+    f32x4 gacc[Q][G];
+#pragma unroll
+    for (int q = 0; q < Q; ++q)
+#pragma unroll
+      for (int g = 0; g < G; ++g) gacc[q][g] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    // Every chunk's loads go out at once (H <= 4096: at most four chunks per wave; a chunk
+    // past the wave's last re-reads chunk 0, unused), then the table is built under them.
+    constexpr int CH = kMidMaxH / 128 / kDecWaves;
+    uint4 xv[CH][Q], gv[CH][G];
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      const size_t co = (size_t)(c < n_chunks ? c : 0) * (128 * kDecWaves);
+#pragma unroll
+      for (int q = 0; q < Q; ++q)
+        xv[c][q] = (4 * q < T) ? ld_u4(xrow[q] + co) : uint4{0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int g = 0; g < G; ++g) gv[c][g] = ld_u4(grow[g] + co);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    table_from_constants();
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      if (c >= n_chunks) break;
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int q = 0; q < Q; ++q) {
+          const s16x4 av = h ? as_s16x4(xv[c][q].z, xv[c][q].w) : as_s16x4(xv[c][q].x, xv[c][q].y);
+#pragma unroll
+          for (int g = 0; g < G; ++g) {
+            const s16x4 bv = h ? as_s16x4(gv[c][g].z, gv[c][g].w) : as_s16x4(gv[c][g].x, gv[c][g].y);
+            gacc[q][g] = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(av, bv, gacc[q][g], 0, 0, 0);
+          }
+        }
+    }
+    float(*s_part)[kMidMaxT][EMAX] = reinterpret_cast<float(*)[kMidMaxT][EMAX]>(s_xt);
+#pragma unroll
+    for (int q = 0; q < Q; ++q)
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          const float v = lanes_sum16(gacc[q][g][m]);
+          const int e = 4 * g + lj;
+          if (lb == 0 && e < E && 4 * q + m < T) s_part[wave][4 * q + m][e] = v;
+        }
+    __syncthreads();
+    // ---- per-token routing: wave w routes tokens 4w .. 4w+3 (workgroup 0 writes logits).
+    if (4 * wave < T)
+      route_rows<EMAX, kDecWaves, kMidMaxT>(s_sle, s_slw, s_part, 4 * wave, ro.bias, T, E, k,
+                                            blockIdx.x == 0 ? ro.logits : nullptr);
+    __syncthreads();
+    // ---- grouping of the T k slots by expert (ascending expert, then slot), by wave 0.
+    if (wave == 0) {
+      const int ns = T * k;
+      const int se = lane < ns ? s_sle[lane] : -1;
+      int before = 0, rank = 0, run = 0, my_cnt = 0, my_off = 0, n_act = 0;
+      uint32_t present = 0;
+      for (int xe = 0; xe < E; ++xe) {
+        const uint64_t m = __ballot(se == xe);
+        const int c = __builtin_popcountll(m);
+        if (se == xe) {
+          before = run;
+          rank = __builtin_popcountll(m & ((1ull << lane) - 1ull));
+        }
+        if (lane == xe) {
+          my_cnt = c;
+          my_off = run;
+        }
+        if (c > 0) present |= 1u << xe;
+        run += c;
+      }
+      if (lane < E) {
+        s_cnt[lane] = my_cnt;
+        s_off[lane] = my_off;
+      }
+      if (lane < ns) s_ptok[before + rank] = lane / k;
+      n_act = __builtin_popcount(present);
+      if (blockIdx.x == 0) {
+        if (lane < ns) {
+          const int t = lane / k, j = lane - (lane / k) * k;
+          ro.w[t * k + j] = s_slw[lane];
+          ro.idx64[t * k + j] = se;
+          ro.idx32[t * k + j] = se;
+          ro.slot_pos[lane] = before + rank;
+          ro.perm_tok[before + rank] = t;
+        }
+        if (lane < E) {
+          ro.counts[lane] = my_cnt;
+          ro.offsets[lane] = my_off;
+        }
+        if (lane == 0) {
+          ro.offsets[E] = ns;
+          ro.active[0] = n_act;
+        }
+        // Active experts in ascending order: lane x writes its rank among the present ones.
+        if (lane < E && ((present >> lane) & 1u))
+          ro.active[1 + __builtin_popcount(present & ((1u << lane) - 1u))] = lane;
+      }
+    }
+    __syncthreads();  // the grouping is visible; the gate partials in s_xt are dead
+    g_cnt = s_cnt;
+    g_off = s_off;
+    g_ptok = s_ptok;
+  }
+
   // Virtual experts of every active expert (lane e holds expert e), counted in every wave.
   // An absent expert (null pointers; the caller routes no token to it) counts no rows.
-  const int cnt = (lane < E && tab.e[lane < E ? lane : 0].w1_packed != nullptr) ? rt.counts[lane] : 0;
-  const int off = lane < E ? rt.offsets[lane] : 0;
+  const int cnt = (lane < E && tab.e[lane < E ? lane : 0].w1_packed != nullptr) ? g_cnt[lane] : 0;
+  const int off = lane < E ? g_off[lane] : 0;
   const int nv = (cnt + kMidRows - 1) / kMidRows;
   int incl = nv;
 #pragma unroll
@@ -1401,18 +1593,18 @@ mid_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x, int H, 
 
   // Token ids of the rows (lanes 0..n-1 of every wave), the expert's codebooks and stream
   // pointers (wave-uniform: scalar loads).
-  const int my_tok = lane < n ? rt.perm_tok[r0 + lane] : 0;
+  const int my_tok = lane < n ? g_ptok[r0 + lane] : 0;
   const moe_nf4_expert_t &ex = tab.e[e];
   const float *c1 = (const float *)uniform_ptr(ex.w1_code);
   const float *c3 = (const float *)uniform_ptr(ex.w3_code);
   const void *pk[2] = {uniform_ptr(ex.w1_packed), uniform_ptr(ex.w3_packed)};
   const void *pa[2] = {uniform_ptr(ex.w1_absmax), uniform_ptr(ex.w3_absmax)};
-  float ca[16], cb[16];
+  // Lane q < 16 checks w1's code q, lanes 16..31 w3's, against the table's NF4 constants.
+  float ref_f = kNf4Code[0];
 #pragma unroll
-  for (int q = 0; q < 16; ++q) {
-    ca[q] = c1[q];
-    cb[q] = c3[q];
-  }
+  for (int q = 1; q < 16; ++q)
+    if ((lane & 15) == q) ref_f = kNf4Code[q];
+  const float cv = lane < 16 ? c1[lane & 15] : c3[lane & 15];
   // The rows' tokens into LDS: piece q of the n x H block, row q / (H / 8).
   const int ppr = H >> 3;  // 16-byte pieces per row
   constexpr int kPer = kMidRows * kMidMaxH / 8 / kDecThreads;
@@ -1424,8 +1616,20 @@ mid_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x, int H, 
     const int tok = __shfl(my_tok, m < kMidRows ? m : 0);
     if (m < n) xv[r] = ld_u4((gx_t)x + (size_t)tok * H + (size_t)(q - m * ppr) * 8);
   }
-  // Lookup table from the expert's codebooks: replicas 0-31 w1, 32-63 w3.
-  build_table_regs<kDecThreads>(s_tbl, ca, cb);
+  // An expert whose w1 / w3 codebooks differ bitwise from the NF4 constants gets a table of
+  // its own (replicas 0-31 w1, 32-63 w3); every wave has finished the routing's LDS work.
+  const bool differ =
+      __ballot(lane < 32 && __builtin_bit_cast(uint32_t, cv) != __builtin_bit_cast(uint32_t, ref_f)) != 0;
+  if (differ) {
+    float ca[16], cb[16];
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      ca[q] = c1[q];
+      cb[q] = c3[q];
+    }
+    __syncthreads();  // no wave still builds the constant table
+    build_table_regs<kDecThreads>(s_tbl, ca, cb);
+  }
 #pragma unroll
   for (int r = 0; r < kPer; ++r) {
     const int q = tid + kDecThreads * r;
@@ -1458,7 +1662,7 @@ mid_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x, int H, 
     // With BC quarter lanej of row 0's chunk blk; else the whole chunk of the lane's row in
     // each group of four (row 0 again past the count).
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < 16; ++i) {
       const int m = 4 * (i >> 2) + lanej;
       P.xo[i] = bc ? xlds_piece(0, H, 4 * blk + lanej)
                    : xlds_piece(m < n ? m : 0, H, 4 * blk + (i & 3));
@@ -1490,16 +1694,218 @@ mid_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x, int H, 
   const uint16_t *xl = reinterpret_cast<const uint16_t *>(s_xt);
   if (bc) {
     auto fin = [&](f32x4 (&ac)[2], int i) { finish(ac, i, std::integral_constant<int, 1>{}); };
-    stream_aligned<2, NSQ, kGateUpDepth, true, kXLds, true, 1>(
+    stream_aligned<2, NSQ, kGateUpDepth, true, kXLds, true, 1, true>(
         grab, set_ptrs, fin, hook, s_tbl, lane_const, row_blocks, s_aslot[wave], xl, (gq_t)x);
   } else if (n <= 4) {
     auto fin = [&](f32x4 (&ac)[2], int i) { finish(ac, i, std::integral_constant<int, 1>{}); };
-    stream_aligned<2, NSQ, kGateUpDepth, false, kXLds, true, 1>(
+    stream_aligned<2, NSQ, kGateUpDepth, false, kXLds, true, 1, true>(
         grab, set_ptrs, fin, hook, s_tbl, lane_const, row_blocks, s_aslot[wave], xl, (gq_t)x);
   } else {
     auto fin = [&](f32x4 (&ac)[4], int i) { finish(ac, i, std::integral_constant<int, 2>{}); };
-    stream_aligned<2, NSQ, kGateUpDepth, false, kXLds, true, 2>(
+    stream_aligned<2, NSQ, kGateUpDepth, false, kXLds, true, 2, true>(
         grab, set_ptrs, fin, hook, s_tbl, lane_const, row_blocks, s_aslot[wave], xl, (gq_t)x);
+  }
+}
+
+// Down projection of mid-size batches: the same virtual experts (<= 8 h rows of one
+// expert) with the K range of w2 (= F) split into parts of four 512-value stages.  The
+// workgroups are dealt to the (virtual expert, K part) pairs in equal shares, each taking an
+// equal share of the H / 4 output tiles; a workgroup stages its rows' K part of h in LDS
+// once (8 x 2048 bf16, swizzled as xlds_piece lays out) and streams its tiles; the fp32
+// sums go to ypart[part][row][c], which the combine adds in part order
+// (model/moe_layer.py:186-191 after the expert's w2).
+constexpr int kMidDownStages = 4;
+constexpr int kMidDownVals = kMidDownStages * kStageVals;  // K values of one part
+constexpr int kMidDownRows = 16;                           // rows of a down virtual expert
+
+__global__ void __launch_bounds__(kDecThreads, 1)
+mid_down_kernel(const ExpertTable tab, const uint16_t *__restrict__ h, int H, int F, int E,
+                int parts, int rows_total, const Route rt, float *__restrict__ ypart) {
+  constexpr int NSQ = kMidDownStages;
+  __shared__ __attribute__((aligned(16))) uint32_t s_tbl[kTableWords];
+  __shared__ uint4 s_ht[kMidDownRows * kMidDownVals / 8];
+  __shared__ __attribute__((aligned(16))) float s_aslot[kDecWaves][2 * kASlotFloats];
+  __shared__ int32_t s_ticket;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  if (tid == 0) s_ticket = 0;
+  const int cnt = (lane < E && tab.e[lane < E ? lane : 0].w2_packed != nullptr) ? rt.counts[lane] : 0;
+  const int off = lane < E ? rt.offsets[lane] : 0;
+  {
+    float cst[16];
+#pragma unroll
+    for (int q = 0; q < 16; ++q) cst[q] = kNf4Code[q];
+    build_table_regs<kDecThreads>(s_tbl, cst, cst);
+  }
+  const int nv = (cnt + kMidDownRows - 1) / kMidDownRows;
+  int incl = nv;
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const int t = __shfl_up(incl, o);
+    if (lane >= o) incl += t;
+  }
+  const int V = __builtin_amdgcn_readlane(incl, kWave - 1);
+  if (V == 0) return;  // uniform over the grid
+  const int VP = V * parts, G = gridDim.x, b = blockIdx.x;
+  const int pr = (int)((int64_t)b * VP / G);  // pair: virtual expert pr / parts, part pr % parts
+  const int b0 = (int)(((int64_t)pr * G + VP - 1) / VP);
+  const int b1 = (int)(((int64_t)(pr + 1) * G + VP - 1) / VP);
+  const int v = pr / parts, kp = pr - v * parts;
+  const int e = __builtin_ctzll(__ballot(incl > v));
+  const int vj = v - (__builtin_amdgcn_readlane(incl, e) - __builtin_amdgcn_readlane(nv, e));
+  const int r0 = __builtin_amdgcn_readlane(off, e) + kMidDownRows * vj;  // first h row
+  const int n = min(kMidDownRows, __builtin_amdgcn_readlane(cnt, e) - kMidDownRows * vj);
+  // Items are pairs of 4-row output tiles (an odd last tile is read twice, written once),
+  // or single tiles for more than 8 rows (four MFMA row groups: the registers of a second
+  // tile's stream do not fit beside them).
+  const int tiles = H >> 2;
+  const bool single = n > 8;
+  const int units = single ? tiles : (tiles + 1) >> 1;
+  const int t_lo = (int)((int64_t)(b - b0) * units / (b1 - b0));
+  const int t_hi = (int)((int64_t)(b - b0 + 1) * units / (b1 - b0));
+
+  const moe_nf4_expert_t &ex = tab.e[e];
+  const float *c2 = (const float *)uniform_ptr(ex.w2_code);
+  const void *pk = uniform_ptr(ex.w2_packed);
+  const void *pa = uniform_ptr(ex.w2_absmax);
+  float ref_f = kNf4Code[0];
+#pragma unroll
+  for (int q = 1; q < 16; ++q)
+    if ((lane & 15) == q) ref_f = kNf4Code[q];
+  const float cv = c2[lane & 15];
+  // The rows' K part of h into LDS: piece q of the n x kMidDownVals block.
+  constexpr int ppr = kMidDownVals / 8;
+  constexpr int kPer = kMidDownRows * ppr / kDecThreads;
+  uint4 hv[kPer];
+#pragma unroll
+  for (int r = 0; r < kPer; ++r) {
+    const int q = tid + kDecThreads * r;
+    const int m = q / ppr;
+    if (m < n)
+      hv[r] = ld_u4((gx_t)h + (size_t)(r0 + m) * F + (size_t)kp * kMidDownVals + (size_t)(q - m * ppr) * 8);
+  }
+  if (__ballot(lane < 16 && __builtin_bit_cast(uint32_t, cv) != __builtin_bit_cast(uint32_t, ref_f)) != 0) {
+    float cc[16];
+#pragma unroll
+    for (int q = 0; q < 16; ++q) cc[q] = c2[q];
+    __syncthreads();  // no wave still builds the constant table
+    build_table_regs<kDecThreads>(s_tbl, cc, cc);
+  }
+#pragma unroll
+  for (int r = 0; r < kPer; ++r) {
+    const int q = tid + kDecThreads * r;
+    const int m = q / ppr;
+    if (m < n) s_ht[xlds_piece(m, kMidDownVals, q - m * ppr)] = hv[r];
+  }
+  __syncthreads();
+
+  const int lanej = lane & 3;
+  const int blk = lane >> 2;
+  const size_t row_bytes = (size_t)(F >> 1);
+  const size_t row_blocks = (size_t)(F >> 6);
+  const uint32_t lane_const[2] = {(uint32_t)lane << 2, (uint32_t)lane << 2};
+  auto grab = [&]() -> int {
+    int t = 0;
+    if (lane == 0) t = __hip_atomic_fetch_add(&s_ticket, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    t = __builtin_amdgcn_readfirstlane(t) + t_lo;
+    return t < t_hi ? t : -1;
+  };
+  const bool bc = n == 1;
+  auto set_ptrs = [&](ItemPtr<2> &P, int tp) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int tl = min(2 * tp + q, tiles - 1);
+      const size_t row = (size_t)tl * 4 + lanej;
+      P.wq[q] = (gq_t)pk + row * row_bytes + (size_t)kp * (NSQ * 256) + blk * 16;
+      P.wa[q] = (ga_t)pa + row * row_blocks + (size_t)kp * (NSQ * 8) + (blk >> 1);
+      P.ab[q] = (ga_t)pa + (size_t)tl * 4 * row_blocks + (size_t)kp * (NSQ * 8);
+    }
+    P.ap = (gx_t)h;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int m = 4 * (i >> 2) + lanej;
+      P.xo[i] = bc ? xlds_piece(0, kMidDownVals, 4 * blk + lanej)
+                   : xlds_piece(m < n ? m : 0, kMidDownVals, 4 * blk + (i & 3));
+    }
+  };
+  auto finish = [&](auto &ac, int tp, auto ng_tag) {
+    constexpr int NGF = decltype(ng_tag)::value;
+    const int nrows = bc ? 1 : 4;
+    float vs[2][NGF][4];
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+#pragma unroll
+      for (int g = 0; g < NGF; ++g)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (q < nrows) vs[p][g][q] = lanes_sum16(ac[p * NGF + g][q]);
+    if (blk == 0) {
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        const int tl = 2 * tp + p;
+        if (tl < tiles) {
+          const int c = tl * 4 + lanej;
+#pragma unroll
+          for (int g = 0; g < NGF; ++g)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const int m = 4 * g + q;
+              if (q < nrows && m < n) ypart[((size_t)kp * rows_total + r0 + m) * H + c] = vs[p][g][q];
+            }
+        }
+      }
+    }
+  };
+  auto hook = [&]() {};
+  const uint16_t *xl = reinterpret_cast<const uint16_t *>(s_ht);
+  if (bc) {
+    auto fin = [&](f32x4 (&ac)[2], int i) { finish(ac, i, std::integral_constant<int, 1>{}); };
+    stream_aligned<2, NSQ, 4, true, kXLds, true, 1, true>(grab, set_ptrs, fin, hook, s_tbl, lane_const,
+                                                     row_blocks, s_aslot[wave], xl, (gq_t)h);
+  } else if (n <= 4) {
+    auto fin = [&](f32x4 (&ac)[2], int i) { finish(ac, i, std::integral_constant<int, 1>{}); };
+    stream_aligned<2, NSQ, 4, false, kXLds, true, 1, true>(grab, set_ptrs, fin, hook, s_tbl, lane_const,
+                                                      row_blocks, s_aslot[wave], xl, (gq_t)h);
+  } else if (n <= 8) {
+    auto fin = [&](f32x4 (&ac)[4], int i) { finish(ac, i, std::integral_constant<int, 2>{}); };
+    stream_aligned<2, NSQ, 4, false, kXLds, true, 2, true>(grab, set_ptrs, fin, hook, s_tbl, lane_const,
+                                                      row_blocks, s_aslot[wave], xl, (gq_t)h);
+  } else {
+    auto set_ptrs1 = [&](ItemPtr<1> &P, int tl) {
+      const size_t row = (size_t)tl * 4 + lanej;
+      P.wq[0] = (gq_t)pk + row * row_bytes + (size_t)kp * (NSQ * 256) + blk * 16;
+      P.wa[0] = (ga_t)pa + row * row_blocks + (size_t)kp * (NSQ * 8) + (blk >> 1);
+      P.ab[0] = (ga_t)pa + (size_t)tl * 4 * row_blocks + (size_t)kp * (NSQ * 8);
+      P.ap = (gx_t)h;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int m = 4 * (i >> 2) + lanej;
+        P.xo[i] = xlds_piece(m < n ? m : 0, kMidDownVals, 4 * blk + (i & 3));
+      }
+    };
+    auto fin = [&](f32x4 (&ac)[4], int tl) {
+      float vs[4][4];
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) vs[g][q] = lanes_sum16(ac[g][q]);
+      if (blk == 0) {
+        const int c = tl * 4 + lanej;
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int m = 4 * g + q;
+            if (m < n) ypart[((size_t)kp * rows_total + r0 + m) * H + c] = vs[g][q];
+          }
+      }
+    };
+    const uint32_t lane_const1[1] = {(uint32_t)lane << 2};
+    stream_aligned<1, NSQ, 4, false, kXLds, true, 4, true>(grab, set_ptrs1, fin, hook, s_tbl,
+                                                           lane_const1, row_blocks, s_aslot[wave],
+                                                           xl, (gq_t)h);
   }
 }
 
@@ -1531,28 +1937,71 @@ bool decode_layer_supported(int64_t T, int32_t k, int32_t E, int32_t H, int32_t 
 }
 
 int64_t decode_route_bytes() { return (int64_t)sizeof(DecodeRoute); }
+int64_t mid_route_out_bytes() { return (int64_t)sizeof(MidRouteOut); }
 
 // The mid-size gate/up path: up to 16 tokens (at most two virtual experts per expert),
 // hidden size 2048 or 4096 (four or eight pipeline stages per row), at most 32 experts.
 bool mid_gateup_supported(int64_t T, int32_t k, int32_t E, int32_t H, int32_t F) {
-  return T >= 1 && T <= 16 && k >= 1 && E >= 1 && E <= kWave / 2 && (H == 2048 || H == 4096) &&
-         F >= 4 && F % 4 == 0 && T * (int64_t)H * 2 >= 2048 &&
+  return T >= 1 && T <= kMidMaxT && k >= 1 && E >= 1 && E <= kWave / 2 &&
+         (H == 2048 || H == 4096) && F >= 4 && F % 4 == 0 && T * (int64_t)H * 2 >= 2048 &&
          (int64_t)E + T * k / kMidRows + 1 <= device_cu_count();
 }
 
-int launch_mid_gateup(const void *tab_v, const void *x, int64_t T, int32_t k, int32_t H, int32_t F,
-                      int32_t E, const void *route_v, void *h_ws, hipStream_t s) {
-  MOE_REQUIRE(mid_gateup_supported(T, k, E, H, F), "shape not supported by the mid-size gate/up");
-  MOE_REQUIRE(((uintptr_t)x % 16) == 0, "x must be 16-byte aligned");
+// The same path with the routing and grouping in the kernel (every workgroup routes the
+// tokens; workgroup 0 publishes the results): top-k <= 2 and at most 16 experts.
+bool mid_layer_supported(int64_t T, int32_t k, int32_t E, int32_t H, int32_t F) {
+  return mid_gateup_supported(T, k, E, H, F) && k <= 2 && E <= 16 && T * k <= kMidMaxSlots;
+}
+
+// The mid-size down projection: F a multiple of 4 x 512 (parts of four stages), at most 16
+// parts (the combine's plane limit), H a multiple of 4 and h at least 2 KB (the past-the-end
+// prefetches read it).
+bool mid_down_supported(int64_t T, int32_t k, int32_t E, int32_t H, int32_t F) {
+  return mid_gateup_supported(T, k, E, H, F) && F % kMidDownVals == 0 &&
+         F / kMidDownVals <= 16 && H % 4 == 0 && T * k * (int64_t)F * 2 >= 2048;
+}
+int mid_down_parts(int32_t F) { return F / kMidDownVals; }
+
+int launch_mid_down(const void *tab_v, const void *h, int64_t T, int32_t k, int32_t H, int32_t F,
+                    int32_t E, const void *route_v, void *ypart, int32_t parts, hipStream_t s) {
+  MOE_REQUIRE(mid_down_supported(T, k, E, H, F) && parts == mid_down_parts(F),
+              "shape not supported by the mid-size down projection");
+  MOE_REQUIRE(((uintptr_t)h % 16) == 0, "h must be 16-byte aligned");
   const ExpertTable &tab = *static_cast<const ExpertTable *>(tab_v);
   const Route &rt = *static_cast<const Route *>(route_v);
+  hipLaunchKernelGGL(mid_down_kernel, dim3((unsigned)device_cu_count()), dim3(kDecThreads), 0, s,
+                     tab, (const uint16_t *)h, H, F, E, parts, (int)(T * k), rt, (float *)ypart);
+  MOE_LAUNCH_CHECK();
+  return MOE_STATUS_OK;
+}
+
+int launch_mid_gateup(const void *tab_v, const void *x, int64_t T, int32_t k, int32_t H, int32_t F,
+                      int32_t E, const void *route_v, void *h_ws, hipStream_t s,
+                      const void *route_out) {
+  MOE_REQUIRE(route_out == nullptr ? mid_gateup_supported(T, k, E, H, F)
+                                   : mid_layer_supported(T, k, E, H, F),
+              "shape not supported by the mid-size gate/up");
+  MOE_REQUIRE(((uintptr_t)x % 16) == 0, "x must be 16-byte aligned");
+  const ExpertTable &tab = *static_cast<const ExpertTable *>(tab_v);
+  const Route rt = route_v ? *static_cast<const Route *>(route_v) : Route{};
+  const MidRouteOut ro = route_out ? *static_cast<const MidRouteOut *>(route_out) : MidRouteOut{};
+  if (route_out) {
+    MOE_REQUIRE(((uintptr_t)ro.gate % 16) == 0, "gate must be 16-byte aligned");
+    MOE_REQUIRE(ro.w && ro.idx64 && ro.idx32 && ro.counts && ro.offsets && ro.perm_tok &&
+                    ro.slot_pos && ro.active,
+                "null routing output");
+  }
   const dim3 grid((unsigned)device_cu_count()), blk(kDecThreads);
-  if (H == 4096)
-    hipLaunchKernelGGL(mid_gateup_kernel<8>, grid, blk, 0, s, tab, (const uint16_t *)x, H, F, E,
-                       rt, (uint16_t *)h_ws);
+  auto go = [&](auto kern) {
+    hipLaunchKernelGGL(kern, grid, blk, 0, s, tab, (const uint16_t *)x, (int)T, H, F, E, k, rt, ro,
+                       (uint16_t *)h_ws);
+  };
+  if (route_out == nullptr)
+    go(H == 4096 ? mid_gateup_kernel<8, 8, false> : mid_gateup_kernel<4, 8, false>);
+  else if (E <= 8)
+    go(H == 4096 ? mid_gateup_kernel<8, 8, true> : mid_gateup_kernel<4, 8, true>);
   else
-    hipLaunchKernelGGL(mid_gateup_kernel<4>, grid, blk, 0, s, tab, (const uint16_t *)x, H, F, E,
-                       rt, (uint16_t *)h_ws);
+    go(H == 4096 ? mid_gateup_kernel<8, 16, true> : mid_gateup_kernel<4, 16, true>);
   MOE_LAUNCH_CHECK();
   return MOE_STATUS_OK;
 }

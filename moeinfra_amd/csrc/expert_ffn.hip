@@ -454,8 +454,13 @@ int launch_midbatch(const void *tab, const void *x, int64_t T, int64_t rows_tota
                     int32_t F, const void *route, void *h_ws, void *ypart, int32_t nsplit,
                     int phases, hipStream_t stream);
 bool mid_gateup_supported(int64_t T, int32_t k, int32_t E, int32_t H, int32_t F);
+bool mid_down_supported(int64_t T, int32_t k, int32_t E, int32_t H, int32_t F);
+int mid_down_parts(int32_t F);
+int launch_mid_down(const void *tab, const void *h, int64_t T, int32_t k, int32_t H, int32_t F,
+                    int32_t E, const void *route, void *ypart, int32_t parts, hipStream_t s);
 int launch_mid_gateup(const void *tab, const void *x, int64_t T, int32_t k, int32_t H, int32_t F,
-                      int32_t E, const void *route, void *h_ws, hipStream_t s);
+                      int32_t E, const void *route, void *h_ws, hipStream_t s,
+                      const void *route_out);
 
 // ypart planes a layer's down projection writes (the combine adds them): the streamed
 // mid-batch kernels split K of the down projection over workgroups when few experts would
@@ -465,11 +470,37 @@ int choose_nsplit(int64_t T, int32_t k, int32_t E, int32_t H, int32_t F) {
   const int64_t rows = T * k;
   const int64_t active_max = rows < E ? rows : E;
   if (T <= 0 || gemv4_supported(T, H, F)) return 1;
+  if (mid_down_supported(T, k, E, H, F)) return mid_down_parts(F);
   if (rows >= kGemmMinRowsPerExpert * active_max && expert_gemm_supported(H, F) &&
       expert_gemm_rows_ok(T, rows, H, F))
     return expert_gemm_splits(rows, active_max, H, F);
   if (!midbatch_supported(H, F, 1) || !midbatch_rows_ok(T, rows, H, F)) return 1;
   return midbatch_splits(active_max, H, F);
+}
+
+bool mid_layer_supported(int64_t T, int32_t k, int32_t E, int32_t H, int32_t F);
+
+// Gate/up of a mid-size layer with the routing and grouping in the same launch (the
+// decode-stream kernel of launch_mid_gateup, every workgroup routing the tokens itself);
+// route_out (a MidRouteOut) names the gate, the bias and the routing outputs, which
+// workgroup 0 writes for the down projection and the combine.
+int launch_mid_layer_gateup(const moe_nf4_expert_t *experts, int32_t E, const void *x, int64_t T,
+                            int32_t k, int32_t H, int32_t F, void *h_ws, const void *route_out,
+                            hipStream_t stream) {
+  MOE_REQUIRE(E >= 1 && E <= MOE_MAX_EXPERTS, "num_experts must be in [1, %d]", MOE_MAX_EXPERTS);
+  MOE_REQUIRE(experts && x && h_ws && route_out, "null pointer");
+  MOE_REQUIRE(((uintptr_t)h_ws % 16) == 0, "h workspace must be 16-byte aligned");
+  ExpertTable tab;
+  for (int e = 0; e < MOE_MAX_EXPERTS; ++e) {
+    if (e < E) {
+      const int rc = check_expert(experts[e], e);
+      if (rc != MOE_STATUS_OK) return rc;
+      tab.e[e] = experts[e];
+    } else {
+      tab.e[e] = moe_nf4_expert_t{};
+    }
+  }
+  return launch_mid_gateup(&tab, x, T, k, H, F, E, nullptr, h_ws, stream, route_out);
 }
 
 // phases: bit 0 = gate/up (x -> h), bit 1 = down (h -> ypart).  Up to 4 tokens per expert
@@ -515,10 +546,15 @@ int launch_expert_ffn(const moe_nf4_expert_t *experts, int32_t E, const void *x,
   // (<= 8 token rows of one expert, staged in LDS) per workgroup; the down projection takes
   // the path chosen below.
   if ((phases & 1) && fused == nullptr && mid_gateup_supported(T, k, E, H, F)) {
-    const int rc = launch_mid_gateup(&tab, x, T, k, H, F, E, &rt, h_ws, stream);
+    const int rc = launch_mid_gateup(&tab, x, T, k, H, F, E, &rt, h_ws, stream, nullptr);
     if (rc != MOE_STATUS_OK || !(phases & 2)) return rc;
     phases &= ~1;
   }
+  // Its down projection: the same virtual experts over parts of four stages of F, when the
+  // caller's plane count is that part count.
+  if ((phases & 2) && fused == nullptr && mid_down_supported(T, k, E, H, F) &&
+      nsplit == mid_down_parts(F))
+    return launch_mid_down(&tab, h_ws, T, k, H, F, E, &rt, ypart, nsplit, stream);
   // Many tokens per expert on average: the LDS-staged GEMM streams each weight tile once per
   // 128 tokens (the per-tile kernels below re-stream it every 16 or 32 tokens).
   if (fused == nullptr && rows_total >= kGemmMinRowsPerExpert * active_max &&

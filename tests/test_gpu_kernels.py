@@ -440,15 +440,43 @@ def _check_layer(want, i_want, got, i_got, lg, bias=None):
     assert err <= 1e-2, err
 
 
+# F a multiple of 2048 also takes the mid-size down projection (virtual experts over parts
+# of 2048 values of F, one fp32 plane per part; 1 and 2 parts here).
 @pytest.mark.parametrize("H,F,E,T,seed,skew", [
     (2048, 1024, 8, 5, 81, False),
     (2048, 1536, 8, 12, 82, True),
     (2048, 1024, 8, 16, 83, False),
     (2048, 512, 4, 11, 84, False),     # four experts: most hold more than 4 rows, some > 8
     (2048, 768, 16, 16, 85, True),
+    (2048, 2048, 8, 7, 91, False),
+    (2048, 4096, 8, 16, 92, True),
+    (4096, 4096, 4, 13, 93, False),
 ])
 def test_layer_mid_gateup(cuda_device, H, F, E, T, seed, skew):
     _check_layer(*_layer_case(cuda_device, H, F, E, T, seed, skew))
+
+
+def test_expert_ffn_mid_size_external_route(cuda_device):
+    """The mid-size kernels behind the generic entry points (router and grouping launched
+    apart, as MoELayer's offload path does): gate/up from the given grouping, the down
+    projection into the library's default number of planes, then the combine."""
+    from moeinfra_amd import ops
+
+    H, F, E, T = 2048, 4096, 8, 14
+    gate, experts, x = build_layer(H, F, E, T, 94)
+    want, (lg_w, w_w, i_w) = oracle_layer(gate, experts, x)
+    for ex in experts:
+        ex.to(cuda_device)
+    table = ops.expert_table([ex.c_struct() for ex in experts])
+    xd = x.to(cuda_device)
+    idx32 = torch.empty((T, 2), dtype=torch.int32, device=cuda_device)
+    _, w, idx = ops.router_topk(xd, gate.to(cuda_device), 2, want_logits=False, idx32_out=idx32)
+    route = ops.permute(idx32, E)
+    assert ops.choose_nsplit(T, 2, E, H, F) == 2
+    _, ypart = ops.expert_ffn(table, E, xd, 2, H, F, route)
+    out = ops.combine(ypart, w, idx32, route["slot_pos"])
+    torch.cuda.synchronize()
+    _check_layer(want, i_w, bits(out), idx.cpu().numpy(), lg_w)
 
 
 def test_layer_mid_gateup_mixed_codebooks(cuda_device):
@@ -465,7 +493,7 @@ def test_layer_mid_gateup_hot_and_absent(cuda_device, T):
     from moeinfra_amd import ops
     from moeinfra_amd._lib import MoeNf4Expert
 
-    H, F, E, hot, absent = 2048, 1024, 8, 2, 6
+    H, F, E, hot, absent = 2048, 2048, 8, 2, 6
     gate, experts, x = build_layer(H, F, E, T, 87 + T)
     bias = torch.zeros(E, dtype=torch.float32)
     bias[hot], bias[absent] = 1.0e4, -1.0e4
