@@ -1941,8 +1941,14 @@ int64_t mid_route_out_bytes() { return (int64_t)sizeof(MidRouteOut); }
 
 // The mid-size gate/up path: up to 16 tokens (at most two virtual experts per expert),
 // hidden size 2048 or 4096 (four or eight pipeline stages per row), at most 32 experts.
+// Up to 16 tokens.  At 32 (Mixtral decode: ~8 rows per expert, 25-30 for a hot one) this
+// path measured slower than the 32-row tiles of the mid-batch kernels (Zipf 214 against
+// 162 us per layer, uniform 257 against 255): more than 8 rows take four MFMA row groups,
+// whose 64 LDS bytes of activations per lane, stage and group bound the stream.
+constexpr int kMidMaxTokens = 16;
+
 bool mid_gateup_supported(int64_t T, int32_t k, int32_t E, int32_t H, int32_t F) {
-  return T >= 1 && T <= kMidMaxT && k >= 1 && E >= 1 && E <= kWave / 2 &&
+  return T >= 1 && T <= kMidMaxTokens && k >= 1 && E >= 1 && E <= kWave / 2 &&
          (H == 2048 || H == 4096) && F >= 4 && F % 4 == 0 && T * (int64_t)H * 2 >= 2048 &&
          (int64_t)E + T * k / kMidRows + 1 <= device_cu_count();
 }
@@ -1950,7 +1956,8 @@ bool mid_gateup_supported(int64_t T, int32_t k, int32_t E, int32_t H, int32_t F)
 // The same path with the routing and grouping in the kernel (every workgroup routes the
 // tokens; workgroup 0 publishes the results): top-k <= 2 and at most 16 experts.
 bool mid_layer_supported(int64_t T, int32_t k, int32_t E, int32_t H, int32_t F) {
-  return mid_gateup_supported(T, k, E, H, F) && k <= 2 && E <= 16 && T * k <= kMidMaxSlots;
+  return mid_gateup_supported(T, k, E, H, F) && T <= kMidMaxT && k <= 2 && E <= 16 &&
+         T * k <= kMidMaxSlots;
 }
 
 // The mid-size down projection: F a multiple of 4 x 512 (parts of four stages), at most 16
