@@ -19,8 +19,13 @@ the time the host link is busy with at least one of them (union of their interva
 share of the steps' wall time, the rate while busy, and how much of that copy time a
 kernel runs alongside (copy/compute overlap).
 
+``python -m moeinfra_amd.profiling counters DB [SUBSTR]`` (a ``rocprofv3 --pmc ...`` run)
+prints the median of each counter per kernel (dispatches counted), e.g. FETCH_SIZE and
+WRITE_SIZE in KiB per dispatch.
+
 Only the ``kernels`` view (columns name, grid_x, start, end in nanoseconds) and, for
 ``copies``, the ``memory_copies`` view (start, end, size, src_agent_type, dst_agent_type)
+and, for ``counters``, the ``counters_collection`` view (kernel_name, counter_name, value)
 of the database are read.
 """
 from __future__ import annotations
@@ -178,7 +183,28 @@ def copy_table(launches: Sequence[Launch], copies: Sequence[Copy], last: int | N
                           steps[-1][-1][3], len(steps))
 
 
+def counter_table(db_path: str, substr: str = "") -> List[Tuple[str, str, int, float, float]]:
+    """(kernel, counter, dispatches, median value, mean value) per kernel and counter."""
+    con = sqlite3.connect(db_path)
+    try:
+        rows = con.execute("select kernel_name, counter_name, value from counters_collection").fetchall()
+    finally:
+        con.close()
+    by: Dict[Tuple[str, str], List[float]] = {}
+    for n, c, v in rows:
+        if substr and substr not in str(n):
+            continue
+        by.setdefault((short_name(str(n)), str(c)), []).append(float(v))
+    return sorted((n, c, len(v), st.median(v), st.mean(v)) for (n, c), v in by.items())
+
+
 def _main(argv: Sequence[str]) -> int:
+    if len(argv) >= 2 and argv[0] == "counters":
+        print("| kernel | counter | dispatches | median | mean |")
+        print("|---|---|---:|---:|---:|")
+        for n, c, cnt, med, mean in counter_table(argv[1], argv[2] if len(argv) > 2 else ""):
+            print(f"| {n} | {c} | {cnt} | {med:.1f} | {mean:.1f} |")
+        return 0
     if len(argv) >= 2 and argv[0] == "copies":
         last = int(argv[2]) if len(argv) > 2 else None
         min_mib = float(argv[3]) if len(argv) > 3 else 1.0

@@ -83,3 +83,15 @@ def test_copy_table_by_hand(tmp_path):
     assert t["gbps_while_busy"] == pytest.approx(8e6 / 80_000)
     assert t["copy_time_with_kernel_frac"] == pytest.approx(60_000 / 80_000)
     assert t["kernel_time_with_copy_frac"] == pytest.approx(60_000 / 90_000)
+
+
+def test_counter_table_by_hand(tmp_path):
+    p = tmp_path / "pmc_results.db"
+    con = sqlite3.connect(p)
+    con.execute("create table counters_collection (kernel_name text, counter_name text, value real)")
+    k = "void moe::(anonymous namespace)::mid_down_kernel(moe::ExpertTable)"
+    con.executemany("insert into counters_collection values (?, ?, ?)",
+                    [(k, "FETCH_SIZE", v) for v in (10.0, 30.0, 20.0)] + [("other()", "FETCH_SIZE", 5.0)])
+    con.commit()
+    con.close()
+    assert profiling.counter_table(str(p), "mid_down") == [("mid_down_kernel", "FETCH_SIZE", 3, 20.0, 20.0)]
