@@ -51,17 +51,20 @@ def test_workspace_sizes_are_host_functions():
 
 
 def test_down_splits_size_the_ypart_planes():
-    # The default K splits of the down projection: one plane for the decode forms, several
-    # for mid-size and batched layers, always a power of two that divides the NF4 blocks of
-    # F into whole 4-block absmax groups for the batched GEMM; the workspace holds that many
-    # fp32 ypart planes.
+    # The default K splits of the down projection: one plane for the decode forms; for the
+    # mid-size GEMV kernels (5-16 tokens) one plane per 2048 values of F; for the streamed
+    # mid-batch kernels and the batched GEMM a power of two that divides the NF4 blocks of F
+    # into whole 4-block absmax groups; the workspace holds that many fp32 ypart planes.
     lib = _lib.lib()
     H, F, E, k = 4096, 14336, 8, 2
     assert lib.moe_layer_down_splits(1, k, E, H, F) == 1
     assert lib.moe_layer_down_splits(-1, k, E, H, F) == -1
     for T in (1, 4, 16, 40, 300, 512, 4096):
         n = lib.moe_layer_down_splits(T, k, E, H, F)
-        assert 1 <= n <= 16 and n & (n - 1) == 0
+        if 5 <= T <= 16:
+            assert n == F // 2048
+        else:
+            assert 1 <= n <= 16 and n & (n - 1) == 0
         if T >= 300:  # the batched GEMM
             assert (F // 64) % n == 0 and (F // 64 // n) % 4 == 0
         ws = lib.moe_layer_workspace_bytes(T, k, E, H, F)
