@@ -1,6 +1,7 @@
 // Decode MoE layer in two launches: routing fused into the NF4 gate/up GEMV, and the
 // weighted combine fused into the NF4 down GEMV.  For T <= 4 tokens with T*k <= 8 routed
-// slots and E <= 16 experts (Mixtral decode: T = 1, k = 2, E = 8).
+// slots and E <= 16 experts (Mixtral decode: T = 1, k = 2, E = 8).  The mid-size kernels
+// (5 to 64 tokens, 16x16x32 MFMA) follow further down.
 //
 // Why: at batch 1 a Mixtral layer streams ~198 MB of NF4 weights; every extra kernel
 // boundary costs about a microsecond, and any chain of dependent global loads before a
@@ -1373,18 +1374,8 @@ decode_down_kernel(const ExpertTable tab, const DecodeRoute *__restrict__ route,
   }
 }
 
-// Gate/up of mid-size batches (5 to 16 tokens, after the stand-alone routing and
-// grouping): the decode stream with one "virtual expert" per workgroup.  An active expert
-// with cnt routed rows is ceil(cnt / 8) virtual experts of up to 8 consecutive rows.  The
-// workgroups are dealt to the virtual experts in equal shares (grid / V each, V <= grid),
-// and each takes an equal share of its virtual expert's 4-row tiles; so a workgroup holds
-// one set of <= 8 token rows, which it stages in LDS once (swizzled as xlds_piece lays
-// out), and one expert, whose own w1 / w3 codebooks it builds its lookup table from.  The
-// waves share the tiles through the work counter and stream them through the aligned
-// pipeline, the rows in one or two groups of four MFMA rows; h rows are written as
-// h = bf16(silu(bf16(w1 x)) * bf16(w3 x)) (transfer/nf4_reconstruct.py:152-155 on the rows
-// model/moe_layer.py:174-186 gathers).
-constexpr int kMidRows = 8;       // rows of a virtual expert
+// Largest hidden size of the in-kernel routing of mid-size launches (the gate products'
+// loads of one wave: at most four 128-value chunks).
 constexpr int kMidMaxH = 4096;
 
 // The routing a mid-size gate/up launch computes itself (ROUTE): the gate, the optional
@@ -1407,30 +1398,199 @@ struct MidRouteOut {
 constexpr int kMidMaxT = 16;
 constexpr int kMidMaxSlots = kMidMaxT * 2;
 
-template <int NSQ, int EMAX, bool ROUTE>
+// Routing of the T <= kMidMaxT tokens of a mid-size launch, recomputed in every workgroup
+// (the gate is small and stays in L2): the gate products, per-token routing (route_rows),
+// then the grouping of the T*k slots by expert into s_cnt / s_off / s_ptok (wave 0);
+// workgroup 0 also writes the router's outputs and the grouping (MidRouteOut).  s_scratch
+// holds the waves' gate partials (kDecWaves x kMidMaxT x EMAX floats) until the final
+// barrier; `table` builds the lookup table while the gate loads are in flight.
+template <int EMAX, typename TableFn>
+__device__ __forceinline__ void mid_route(const uint16_t *__restrict__ x, int T, int H, int E,
+                                          int k, const MidRouteOut &ro, float *s_scratch,
+                                          int32_t *s_sle, float *s_slw, int32_t *s_cnt,
+                                          int32_t *s_off, int32_t *s_ptok, TableFn &&table) {
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // ---- gate products on the 4x4x4 MFMA: wave w takes the 128-value chunks w, w + 8, ...
+  // of H; lane (b = lane / 4, j = lane % 4) holds values 8b .. 8b+7 of a chunk of token
+  // 4q + j (A rows of token group q; tokens >= T repeat a valid row and are ignored) and of
+  // expert 4g + j (B columns).  A butterfly over the 16 blocks completes the wave's sums.
+  constexpr int G = EMAX / 4;
+  constexpr int Q = kMidMaxT / 4;
+  const int lj = lane & 3, lb = lane >> 2;
+  const int n_chunks = (H / 128 - wave + kDecWaves - 1) / kDecWaves;
+  gx_t xrow[Q], grow[G];
+#pragma unroll
+  for (int q = 0; q < Q; ++q) {
+    const int t = 4 * q + lj;
+    xrow[q] = (gx_t)x + (size_t)(t < T ? t : T - 1) * H + (size_t)wave * 128 + 8 * lb;
+  }
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const int e = 4 * g + lj;
+    grow[g] = (gx_t)ro.gate + (size_t)(e < E ? e : E - 1) * H + (size_t)wave * 128 + 8 * lb;
+  }
+  f32x4 gacc[Q][G];
+#pragma unroll
+  for (int q = 0; q < Q; ++q)
+#pragma unroll
+    for (int g = 0; g < G; ++g) gacc[q][g] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  // Every chunk's loads go out at once (H <= 4096: at most four chunks per wave; a chunk
+  // past the wave's last re-reads chunk 0, unused), then the table is built under them.
+  constexpr int CH = kMidMaxH / 128 / kDecWaves;
+  uint4 xv[CH][Q], gv[CH][G];
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const size_t co = (size_t)(c < n_chunks ? c : 0) * (128 * kDecWaves);
+#pragma unroll
+    for (int q = 0; q < Q; ++q)
+      xv[c][q] = (4 * q < T) ? ld_u4(xrow[q] + co) : uint4{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int g = 0; g < G; ++g) gv[c][g] = ld_u4(grow[g] + co);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  table();
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    if (c >= n_chunks) break;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int q = 0; q < Q; ++q) {
+        const s16x4 av = h ? as_s16x4(xv[c][q].z, xv[c][q].w) : as_s16x4(xv[c][q].x, xv[c][q].y);
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          const s16x4 bv = h ? as_s16x4(gv[c][g].z, gv[c][g].w) : as_s16x4(gv[c][g].x, gv[c][g].y);
+          gacc[q][g] = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(av, bv, gacc[q][g], 0, 0, 0);
+        }
+      }
+  }
+  float(*s_part)[kMidMaxT][EMAX] = reinterpret_cast<float(*)[kMidMaxT][EMAX]>(s_scratch);
+#pragma unroll
+  for (int q = 0; q < Q; ++q)
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const float v = lanes_sum16(gacc[q][g][m]);
+        const int e = 4 * g + lj;
+        if (lb == 0 && e < E && 4 * q + m < T) s_part[wave][4 * q + m][e] = v;
+      }
+  __syncthreads();
+  // ---- per-token routing: wave w routes tokens 4w .. 4w+3 (workgroup 0 writes logits).
+  if (4 * wave < T)
+    route_rows<EMAX, kDecWaves, kMidMaxT>(s_sle, s_slw, s_part, 4 * wave, ro.bias, T, E, k,
+                                          blockIdx.x == 0 ? ro.logits : nullptr);
+  __syncthreads();
+  // ---- grouping of the T k slots by expert (ascending expert, then slot), by wave 0.
+  if (wave == 0) {
+    const int ns = T * k;
+    const int se = lane < ns ? s_sle[lane] : -1;
+    int before = 0, rank = 0, run = 0, my_cnt = 0, my_off = 0, n_act = 0;
+    uint32_t present = 0;
+    for (int xe = 0; xe < E; ++xe) {
+      const uint64_t m = __ballot(se == xe);
+      const int c = __builtin_popcountll(m);
+      if (se == xe) {
+        before = run;
+        rank = __builtin_popcountll(m & ((1ull << lane) - 1ull));
+      }
+      if (lane == xe) {
+        my_cnt = c;
+        my_off = run;
+      }
+      if (c > 0) present |= 1u << xe;
+      run += c;
+    }
+    if (lane < E) {
+      s_cnt[lane] = my_cnt;
+      s_off[lane] = my_off;
+    }
+    if (lane < ns) s_ptok[before + rank] = lane / k;
+    n_act = __builtin_popcount(present);
+    if (blockIdx.x == 0) {
+      if (lane < ns) {
+        const int t = lane / k, j = lane - (lane / k) * k;
+        ro.w[t * k + j] = s_slw[lane];
+        ro.idx64[t * k + j] = se;
+        ro.idx32[t * k + j] = se;
+        ro.slot_pos[lane] = before + rank;
+        ro.perm_tok[before + rank] = t;
+      }
+      if (lane < E) {
+        ro.counts[lane] = my_cnt;
+        ro.offsets[lane] = my_off;
+      }
+      if (lane == 0) {
+        ro.offsets[E] = ns;
+        ro.active[0] = n_act;
+      }
+      // Active experts in ascending order: lane x writes its rank among the present ones.
+      if (lane < E && ((present >> lane) & 1u))
+        ro.active[1 + __builtin_popcount(present & ((1u << lane) - 1u))] = lane;
+    }
+  }
+  __syncthreads();  // the grouping is visible; the gate partials are dead
+}
+
+// Gate/up of mid-size batches (5 to 64 tokens) on the 16x16x32 MFMA.  An active expert with
+// cnt routed rows is ceil(cnt / 16) "virtual experts" of up to 16 consecutive rows; the
+// workgroups are dealt to the virtual experts in equal shares (grid / V each, V <= grid),
+// and each takes an equal share of its virtual expert's tiles.  A workgroup takes its virtual expert's 16-row weight tiles one at a
+// time, and wave w covers values [w H/8, (w+1) H/8) of every tile's K range, so each wave
+// keeps its K slice of the expert's token rows in registers for the whole launch and no
+// activation passes through LDS.  The eight partial sums of a tile meet in LDS (one
+// LDS-only barrier per tile, two buffers), and 256 threads sum them in wave order and write
+// h = bf16(silu(bf16(w1 x)) * bf16(w3 x)) (transfer/nf4_reconstruct.py:152-155 on the rows
+// model/moe_layer.py:174-186 gathers).
+//
+// MFMA layout (v_mfma_f32_16x16x32_bf16): lane l = 16 kq + n supplies B[k in 8kq .. 8kq+7][n]
+// and A[n][k in 8kq .. 8kq+7], and holds D[4 kq + r][n] in register r.  The weights are B
+// (n: row of the tile), the tokens A.  Load s of a projection reads 16 rows x 64 bytes: lane
+// l the 16 bytes 64s + 16kq of row n (two loads per 128-byte line, back to back).  The 64
+// bytes are two NF4 blocks, 2s in lanes 0-31 and 2s+1 in lanes 32-63; two
+// v_permlane32_swap (which exchange the upper half of the first operand with the lower
+// half of the second) turn the lane's dwords d0..d3 into four MFMA operands that each lie
+// in one block: {d0, d2} and {d1, d3} of lanes 0-31 hold block 2s, those of lanes 32-63
+// block 2s+1.  Lane group kq of operand j covers block values kM16Off[kq] + 8 (j & 1) .. +7,
+// and the A operand of MFMA (s, j) holds the same values of the lane's token row.  The
+// absmax of a block (the lane's row) scales each pair of MFMA sums in fp32.
+constexpr int kM16Rows = 16;  // rows of a virtual expert = weight rows of a tile
+
+__device__ __forceinline__ int m16_off(int kq) { return ((kq & 1) << 5) | ((kq >> 1) << 4); }
+
+// Four packed bytes (values 2j, 2j+1 per byte) -> eight bf16 code values (B operand).
+__device__ __forceinline__ bf16x8 m16_lookup(const uint32_t *tbl, uint32_t w, uint32_t lane_const) {
+  uint32_t l[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    l[j] = lds_lookup(tbl, __builtin_amdgcn_perm(w, lane_const, 0x0c0c0400u + (j << 8)));
+  return as_bf16x8(l[0], l[1], l[2], l[3]);
+}
+
+template <int S, int EMAX, bool ROUTE>
 __global__ void __launch_bounds__(kDecThreads, 1)
-mid_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x, int T, int H, int F,
-                  int E, int k, const Route rt, const MidRouteOut ro, uint16_t *__restrict__ h_out) {
+mid16_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x, int T, int H, int F,
+                    int E, int k, const Route rt, const MidRouteOut ro,
+                    uint16_t *__restrict__ h_out) {
+  static_assert(S == 2 || S == 4, "H = 1024 S with S = 2 or 4");
   __shared__ __attribute__((aligned(16))) uint32_t s_tbl[kTableWords];
-  // The staged token rows; before them (ROUTE) the waves' gate partials [wave][token][expert].
-  __shared__ uint4 s_xt[kMidRows * kMidMaxH / 8];
-  __shared__ __attribute__((aligned(16))) float s_aslot[kDecWaves][2 * kASlotFloats];
-  __shared__ int32_t s_ticket;
-  // ROUTE: slot experts and weights, and the grouping (counts, offsets, sorted rows' tokens).
+  // The waves' partial sums of a tile [buffer][wave][projection][4 lane + r]; before the
+  // first tile (ROUTE) the waves' gate partials.
+  __shared__ __attribute__((aligned(16))) float s_red[2][kDecWaves][2][kWave * 4];
   __shared__ int32_t s_sle[ROUTE ? kMidMaxSlots : 1];
   __shared__ float s_slw[ROUTE ? kMidMaxSlots : 1];
   __shared__ int32_t s_cnt[ROUTE ? kWave : 1], s_off[ROUTE ? kWave : 1];
   __shared__ int32_t s_ptok[ROUTE ? kMidMaxSlots : 1];
-  static_assert(!ROUTE || kDecWaves * kMidMaxT * EMAX * 4 <= (int)sizeof(s_xt), "gate partials fit");
+  static_assert(!ROUTE || kDecWaves * kMidMaxT * EMAX * 4 <= (int)sizeof(s_red), "gate partials fit");
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  if (tid == 0) s_ticket = 0;
 
   const int32_t *g_cnt = rt.counts, *g_off = rt.offsets, *g_ptok = rt.perm_tok;
-  // The lookup table from the NF4 codebook constants, built while the first loads are in
-  // flight; a workgroup whose expert has other codebooks rebuilds it below.
   auto table_from_constants = [&]() {
     float cst[16];
 #pragma unroll
@@ -1439,137 +1599,17 @@ mid_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x, int T, 
   };
   if constexpr (!ROUTE) table_from_constants();
   if constexpr (ROUTE) {
-    // ---- gate products on the 4x4x4 MFMA: wave w takes the 128-value chunks w, w + 8, ...
-    // of H; lane (b = lane / 4, j = lane % 4) holds values 8b .. 8b+7 of a chunk of token
-    // 4q + j (A rows of token group q; tokens >= T repeat a valid row and are ignored) and of
-    // expert 4g + j (B columns).  A butterfly over the 16 blocks completes the wave's sums.
-    constexpr int G = EMAX / 4;
-    constexpr int Q = kMidMaxT / 4;
-    const int lj = lane & 3, lb = lane >> 2;
-    const int n_chunks = (H / 128 - wave + kDecWaves - 1) / kDecWaves;
-    gx_t xrow[Q], grow[G];
-#pragma unroll
-    for (int q = 0; q < Q; ++q) {
-      const int t = 4 * q + lj;
-      xrow[q] = (gx_t)x + (size_t)(t < T ? t : T - 1) * H + (size_t)wave * 128 + 8 * lb;
-    }
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const int e = 4 * g + lj;
-      grow[g] = (gx_t)ro.gate + (size_t)(e < E ? e : E - 1) * H + (size_t)wave * 128 + 8 * lb;
-    }
-    f32x4 gacc[Q][G];
-#pragma unroll
-    for (int q = 0; q < Q; ++q)
-#pragma unroll
-      for (int g = 0; g < G; ++g) gacc[q][g] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    // Every chunk's loads go out at once (H <= 4096: at most four chunks per wave; a chunk
-    // past the wave's last re-reads chunk 0, unused), then the table is built under them.
-    constexpr int CH = kMidMaxH / 128 / kDecWaves;
-    uint4 xv[CH][Q], gv[CH][G];
-#pragma unroll
-    for (int c = 0; c < CH; ++c) {
-      const size_t co = (size_t)(c < n_chunks ? c : 0) * (128 * kDecWaves);
-#pragma unroll
-      for (int q = 0; q < Q; ++q)
-        xv[c][q] = (4 * q < T) ? ld_u4(xrow[q] + co) : uint4{0u, 0u, 0u, 0u};
-#pragma unroll
-      for (int g = 0; g < G; ++g) gv[c][g] = ld_u4(grow[g] + co);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    table_from_constants();
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int c = 0; c < CH; ++c) {
-      if (c >= n_chunks) break;
-#pragma unroll
-      for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int q = 0; q < Q; ++q) {
-          const s16x4 av = h ? as_s16x4(xv[c][q].z, xv[c][q].w) : as_s16x4(xv[c][q].x, xv[c][q].y);
-#pragma unroll
-          for (int g = 0; g < G; ++g) {
-            const s16x4 bv = h ? as_s16x4(gv[c][g].z, gv[c][g].w) : as_s16x4(gv[c][g].x, gv[c][g].y);
-            gacc[q][g] = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(av, bv, gacc[q][g], 0, 0, 0);
-          }
-        }
-    }
-    float(*s_part)[kMidMaxT][EMAX] = reinterpret_cast<float(*)[kMidMaxT][EMAX]>(s_xt);
-#pragma unroll
-    for (int q = 0; q < Q; ++q)
-#pragma unroll
-      for (int g = 0; g < G; ++g)
-#pragma unroll
-        for (int m = 0; m < 4; ++m) {
-          const float v = lanes_sum16(gacc[q][g][m]);
-          const int e = 4 * g + lj;
-          if (lb == 0 && e < E && 4 * q + m < T) s_part[wave][4 * q + m][e] = v;
-        }
-    __syncthreads();
-    // ---- per-token routing: wave w routes tokens 4w .. 4w+3 (workgroup 0 writes logits).
-    if (4 * wave < T)
-      route_rows<EMAX, kDecWaves, kMidMaxT>(s_sle, s_slw, s_part, 4 * wave, ro.bias, T, E, k,
-                                            blockIdx.x == 0 ? ro.logits : nullptr);
-    __syncthreads();
-    // ---- grouping of the T k slots by expert (ascending expert, then slot), by wave 0.
-    if (wave == 0) {
-      const int ns = T * k;
-      const int se = lane < ns ? s_sle[lane] : -1;
-      int before = 0, rank = 0, run = 0, my_cnt = 0, my_off = 0, n_act = 0;
-      uint32_t present = 0;
-      for (int xe = 0; xe < E; ++xe) {
-        const uint64_t m = __ballot(se == xe);
-        const int c = __builtin_popcountll(m);
-        if (se == xe) {
-          before = run;
-          rank = __builtin_popcountll(m & ((1ull << lane) - 1ull));
-        }
-        if (lane == xe) {
-          my_cnt = c;
-          my_off = run;
-        }
-        if (c > 0) present |= 1u << xe;
-        run += c;
-      }
-      if (lane < E) {
-        s_cnt[lane] = my_cnt;
-        s_off[lane] = my_off;
-      }
-      if (lane < ns) s_ptok[before + rank] = lane / k;
-      n_act = __builtin_popcount(present);
-      if (blockIdx.x == 0) {
-        if (lane < ns) {
-          const int t = lane / k, j = lane - (lane / k) * k;
-          ro.w[t * k + j] = s_slw[lane];
-          ro.idx64[t * k + j] = se;
-          ro.idx32[t * k + j] = se;
-          ro.slot_pos[lane] = before + rank;
-          ro.perm_tok[before + rank] = t;
-        }
-        if (lane < E) {
-          ro.counts[lane] = my_cnt;
-          ro.offsets[lane] = my_off;
-        }
-        if (lane == 0) {
-          ro.offsets[E] = ns;
-          ro.active[0] = n_act;
-        }
-        // Active experts in ascending order: lane x writes its rank among the present ones.
-        if (lane < E && ((present >> lane) & 1u))
-          ro.active[1 + __builtin_popcount(present & ((1u << lane) - 1u))] = lane;
-      }
-    }
-    __syncthreads();  // the grouping is visible; the gate partials in s_xt are dead
+    mid_route<EMAX>(x, T, H, E, k, ro, &s_red[0][0][0][0], s_sle, s_slw, s_cnt, s_off, s_ptok,
+                    table_from_constants);
     g_cnt = s_cnt;
     g_off = s_off;
     g_ptok = s_ptok;
   }
 
   // Virtual experts of every active expert (lane e holds expert e), counted in every wave.
-  // An absent expert (null pointers; the caller routes no token to it) counts no rows.
   const int cnt = (lane < E && tab.e[lane < E ? lane : 0].w1_packed != nullptr) ? g_cnt[lane] : 0;
   const int off = lane < E ? g_off[lane] : 0;
-  const int nv = (cnt + kMidRows - 1) / kMidRows;
+  const int nv = (cnt + kM16Rows - 1) / kM16Rows;
   int incl = nv;
 #pragma unroll
   for (int o = 1; o < kWave; o <<= 1) {
@@ -1582,42 +1622,42 @@ mid_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x, int T, 
   const int v = (int)((int64_t)b * V / G);
   const int b0 = (int)(((int64_t)v * G + V - 1) / V);
   const int b1 = (int)(((int64_t)(v + 1) * G + V - 1) / V);
-  // The expert holding virtual expert v: the lowest lane whose inclusive count exceeds v.
   const int e = __builtin_ctzll(__ballot(incl > v));
   const int vj = v - (__builtin_amdgcn_readlane(incl, e) - __builtin_amdgcn_readlane(nv, e));
-  const int r0 = __builtin_amdgcn_readlane(off, e) + kMidRows * vj;  // first h row
-  const int n = min(kMidRows, __builtin_amdgcn_readlane(cnt, e) - kMidRows * vj);
-  const int tiles = F >> 2;
+  const int r0 = __builtin_amdgcn_readlane(off, e) + kM16Rows * vj;  // first h row
+  const int n = min(kM16Rows, __builtin_amdgcn_readlane(cnt, e) - kM16Rows * vj);
+  const int tiles = F / kM16Rows;
   const int t_lo = (int)((int64_t)(b - b0) * tiles / (b1 - b0));
   const int t_hi = (int)((int64_t)(b - b0 + 1) * tiles / (b1 - b0));
 
-  // Token ids of the rows (lanes 0..n-1 of every wave), the expert's codebooks and stream
-  // pointers (wave-uniform: scalar loads).
-  const int my_tok = lane < n ? g_ptok[r0 + lane] : 0;
   const moe_nf4_expert_t &ex = tab.e[e];
   const float *c1 = (const float *)uniform_ptr(ex.w1_code);
   const float *c3 = (const float *)uniform_ptr(ex.w3_code);
-  const void *pk[2] = {uniform_ptr(ex.w1_packed), uniform_ptr(ex.w3_packed)};
-  const void *pa[2] = {uniform_ptr(ex.w1_absmax), uniform_ptr(ex.w3_absmax)};
-  // Lane q < 16 checks w1's code q, lanes 16..31 w3's, against the table's NF4 constants.
+  const uint8_t *pk[2] = {(const uint8_t *)uniform_ptr(ex.w1_packed),
+                          (const uint8_t *)uniform_ptr(ex.w3_packed)};
+  const float *pa[2] = {(const float *)uniform_ptr(ex.w1_absmax),
+                        (const float *)uniform_ptr(ex.w3_absmax)};
+
+  // The wave's K slice of the token rows, as A operands (s, j): lane (m = lane & 15, kq) holds
+  // values kM16Off[kq] + 8 (j & 1) .. +7 of block 2s + (j >> 1) of the slice of token row m
+  // (the first row again past n).
+  const int nl = lane & 15, kq = lane >> 4;
+  const int tok = g_ptok[r0 + (nl < n ? nl : 0)];
+  constexpr int kSlice = 128 * S;  // values of a wave's K slice (H / 8)
+  const gx_t xrow = (gx_t)x + (size_t)tok * H + (size_t)wave * kSlice + m16_off(kq);
+  bf16x8 xa[S][4];
+#pragma unroll
+  for (int s = 0; s < S; ++s)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) xa[s][j] = as_bf16x8(ld_u4(xrow + 128 * s + 64 * (j >> 1) + 8 * (j & 1)));
+
+  // An expert whose w1 / w3 codebooks differ bitwise from the NF4 constants gets a table of
+  // its own (replicas 0-31 w1, 32-63 w3).
   float ref_f = kNf4Code[0];
 #pragma unroll
   for (int q = 1; q < 16; ++q)
     if ((lane & 15) == q) ref_f = kNf4Code[q];
   const float cv = lane < 16 ? c1[lane & 15] : c3[lane & 15];
-  // The rows' tokens into LDS: piece q of the n x H block, row q / (H / 8).
-  const int ppr = H >> 3;  // 16-byte pieces per row
-  constexpr int kPer = kMidRows * kMidMaxH / 8 / kDecThreads;
-  uint4 xv[kPer];
-#pragma unroll
-  for (int r = 0; r < kPer; ++r) {
-    const int q = tid + kDecThreads * r;
-    const int m = q / ppr;
-    const int tok = __shfl(my_tok, m < kMidRows ? m : 0);
-    if (m < n) xv[r] = ld_u4((gx_t)x + (size_t)tok * H + (size_t)(q - m * ppr) * 8);
-  }
-  // An expert whose w1 / w3 codebooks differ bitwise from the NF4 constants gets a table of
-  // its own (replicas 0-31 w1, 32-63 w3); every wave has finished the routing's LDS work.
   const bool differ =
       __ballot(lane < 32 && __builtin_bit_cast(uint32_t, cv) != __builtin_bit_cast(uint32_t, ref_f)) != 0;
   if (differ) {
@@ -1630,107 +1670,143 @@ mid_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x, int T, 
     __syncthreads();  // no wave still builds the constant table
     build_table_regs<kDecThreads>(s_tbl, ca, cb);
   }
-#pragma unroll
-  for (int r = 0; r < kPer; ++r) {
-    const int q = tid + kDecThreads * r;
-    const int m = q / ppr;
-    if (m < n) s_xt[xlds_piece(m, H, q - m * ppr)] = xv[r];
-  }
   __syncthreads();
+  if (t_lo >= t_hi) return;  // uniform over the workgroup
 
-  const int lanej = lane & 3;
-  const int blk = lane >> 2;
+  // Stream pointers of the lane (row nl of a tile, bytes 16 kq of the wave's slice).
   const size_t row_bytes = (size_t)(H >> 1);
   const size_t row_blocks = (size_t)(H >> 6);
   const uint32_t lane_const[2] = {(uint32_t)(lane & 31) << 2, ((uint32_t)(lane & 31) << 2) | 128u};
-  auto grab = [&]() -> int {
-    int t = 0;
-    if (lane == 0) t = __hip_atomic_fetch_add(&s_ticket, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    t = __builtin_amdgcn_readfirstlane(t) + t_lo;
-    return t < t_hi ? t : -1;
+  struct TileRegs {
+    u32x4 w[2][S];
+    f32x4 ab[2][S / 2];
   };
-  const bool bc = n == 1;
-  auto set_ptrs = [&](ItemPtr<2> &P, int tile) {
-    const size_t row = (size_t)tile * 4 + lanej;
+  auto load_tile = [&](TileRegs &R, int t) {
+    const size_t row = (size_t)t * kM16Rows + nl;
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
-      P.wq[p] = (gq_t)pk[p] + row * row_bytes + blk * 16;
-      P.wa[p] = (ga_t)pa[p] + row * row_blocks + (blk >> 1);
-      P.ab[p] = (ga_t)pa[p] + (size_t)tile * 4 * row_blocks;
-    }
-    P.ap = (gx_t)x;
-    // With BC quarter lanej of row 0's chunk blk; else the whole chunk of the lane's row in
-    // each group of four (row 0 again past the count).
+      const gq_t wp = (gq_t)pk[p] + row * row_bytes + (size_t)wave * (kSlice / 2) + 16 * kq;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int m = 4 * (i >> 2) + lanej;
-      P.xo[i] = bc ? xlds_piece(0, H, 4 * blk + lanej)
-                   : xlds_piece(m < n ? m : 0, H, 4 * blk + (i & 3));
+      for (int s = 0; s < S; ++s) R.w[p][s] = *reinterpret_cast<const MOE_GLOBAL u32x4 *>(wp + 64 * s);
+    }
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      const ga_t ap = (ga_t)pa[p] + row * row_blocks + (size_t)wave * (2 * S);
+#pragma unroll
+      for (int q = 0; q < S / 2; ++q) R.ab[p][q] = *reinterpret_cast<const MOE_GLOBAL f32x4 *>(ap + 4 * q);
     }
   };
-  auto finish = [&](auto &ac, int tile, auto ng_tag) {
-    constexpr int NGF = decltype(ng_tag)::value;
-    const int nrows = bc ? 1 : 4;
-    float vs[2][NGF][4];
+  // Tiles alternate between two register sets; each load of tile t + 2 goes out as soon as
+  // tile t's data in that slot is used, so two tiles of loads stay in flight.
+  auto load_w = [&](TileRegs &R, int t, int p, int s) {
+    const size_t row = (size_t)t * kM16Rows + nl;
+    R.w[p][s] = *reinterpret_cast<const MOE_GLOBAL u32x4 *>(
+        (gq_t)pk[p] + row * row_bytes + (size_t)wave * (kSlice / 2) + 16 * kq + 64 * s);
+  };
+  auto load_ab = [&](TileRegs &R, int t) {
+    const size_t row = (size_t)t * kM16Rows + nl;
 #pragma unroll
-    for (int p = 0; p < 2; ++p)
+    for (int p = 0; p < 2; ++p) {
+      const ga_t ap = (ga_t)pa[p] + row * row_blocks + (size_t)wave * (2 * S);
 #pragma unroll
-      for (int g = 0; g < NGF; ++g)
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          if (q < nrows) vs[p][g][q] = lanes_sum16(ac[p * NGF + g][q]);
-    if (blk == 0) {
-      const int row = tile * 4 + lanej;
-#pragma unroll
-      for (int g = 0; g < NGF; ++g)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int m = 4 * g + q;
-          if (q < nrows && m < n) h_out[(size_t)(r0 + m) * F + row] = swiglu_bf16(vs[0][g][q], vs[1][g][q]);
-        }
+      for (int q = 0; q < S / 2; ++q) R.ab[p][q] = *reinterpret_cast<const MOE_GLOBAL f32x4 *>(ap + 4 * q);
     }
   };
-  auto hook = [&]() {};
-  const uint16_t *xl = reinterpret_cast<const uint16_t *>(s_xt);
-  if (bc) {
-    auto fin = [&](f32x4 (&ac)[2], int i) { finish(ac, i, std::integral_constant<int, 1>{}); };
-    stream_aligned<2, NSQ, kGateUpDepth, true, kXLds, true, 1, true>(
-        grab, set_ptrs, fin, hook, s_tbl, lane_const, row_blocks, s_aslot[wave], xl, (gq_t)x);
-  } else if (n <= 4) {
-    auto fin = [&](f32x4 (&ac)[2], int i) { finish(ac, i, std::integral_constant<int, 1>{}); };
-    stream_aligned<2, NSQ, kGateUpDepth, false, kXLds, true, 1, true>(
-        grab, set_ptrs, fin, hook, s_tbl, lane_const, row_blocks, s_aslot[wave], xl, (gq_t)x);
-  } else {
-    auto fin = [&](f32x4 (&ac)[4], int i) { finish(ac, i, std::integral_constant<int, 2>{}); };
-    stream_aligned<2, NSQ, kGateUpDepth, false, kXLds, true, 2, true>(
-        grab, set_ptrs, fin, hook, s_tbl, lane_const, row_blocks, s_aslot[wave], xl, (gq_t)x);
+  int buf = 0;
+  // Tile t from R (then tile t_next's loads into R); h rows written when `live`.  The steps
+  // (projection p, load s) are software-pipelined: the table lookups of step i + 1 go out
+  // before the MFMAs of step i.
+  constexpr int kSteps = 2 * S;
+  auto tile_step = [&](TileRegs &R, int t, int t_next, bool live) {
+    auto lookups = [&](int i, bf16x8 (&bo)[4]) {
+      const int p = i / S, s = i % S;
+      const u32x4 w = R.w[p][s];
+      load_w(R, t_next, p, s);
+      const auto lo = __builtin_amdgcn_permlane32_swap(w[0], w[2], false, false);
+      const auto hi = __builtin_amdgcn_permlane32_swap(w[1], w[3], false, false);
+      bo[0] = m16_lookup(s_tbl, lo[0], lane_const[p]);
+      bo[1] = m16_lookup(s_tbl, hi[0], lane_const[p]);
+      bo[2] = m16_lookup(s_tbl, lo[1], lane_const[p]);
+      bo[3] = m16_lookup(s_tbl, hi[1], lane_const[p]);
+    };
+    f32x4 acc[2];
+    acc[0] = acc[1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    bf16x8 bc[4], bn[4];
+    lookups(0, bc);
+#pragma unroll
+    for (int i = 0; i < kSteps; ++i) {
+      const int p = i / S, s = i % S;
+      if (i + 1 < kSteps) lookups(i + 1, bn);
+      __builtin_amdgcn_sched_barrier(0);
+      f32x4 ta = f32x4{0.0f, 0.0f, 0.0f, 0.0f}, tb = ta;
+      ta = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[s][0], bc[0], ta, 0, 0, 0);
+      ta = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[s][1], bc[1], ta, 0, 0, 0);
+      tb = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[s][2], bc[2], tb, 0, 0, 0);
+      tb = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[s][3], bc[3], tb, 0, 0, 0);
+      const int ba = 2 * s;  // the blocks of load s: 2s (ta) and 2s + 1 (tb)
+      scale_acc(acc[p], ta, R.ab[p][ba >> 2][ba & 3]);
+      scale_acc(acc[p], tb, R.ab[p][(ba + 1) >> 2][(ba + 1) & 3]);
+      if (i + 1 < kSteps) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) bc[j] = bn[j];
+      }
+    }
+#pragma unroll
+    for (int p = 0; p < 2; ++p) *reinterpret_cast<f32x4 *>(&s_red[buf][wave][p][lane * 4]) = acc[p];
+    load_ab(R, t_next);
+    lds_barrier();
+    if (live && tid < kM16Rows * kM16Rows) {
+      // Token row m, tile row c: D[m][c] is register m & 3 of lane 16 (m >> 2) + c.
+      const int c = tid & 15, m = tid >> 4;
+      const int idx = (16 * (m >> 2) + c) * 4 + (m & 3);
+      float g = 0.0f, u = 0.0f;
+#pragma unroll
+      for (int w = 0; w < kDecWaves; ++w) {
+        g += s_red[buf][w][0][idx];
+        u += s_red[buf][w][1][idx];
+      }
+      if (m < n) h_out[(size_t)(r0 + m) * F + (size_t)t * kM16Rows + c] = swiglu_bf16(g, u);
+    }
+    buf ^= 1;
+  };
+  // Past the last tile the loads re-read it (L2, unused); an odd count ends with one more
+  // pass over the last tile whose h rows are not written.
+  const int last = t_hi - 1;
+  TileRegs A, B;
+  load_tile(A, t_lo);
+  load_tile(B, min(t_lo + 1, last));
+  for (int t = t_lo; t < t_hi; t += 2) {
+    tile_step(A, t, min(t + 2, last), true);
+    tile_step(B, min(t + 1, last), min(t + 3, last), t + 1 < t_hi);
   }
 }
 
-// Down projection of mid-size batches: the same virtual experts (<= 8 h rows of one
-// expert) with the K range of w2 (= F) split into parts of four 512-value stages.  The
-// workgroups are dealt to the (virtual expert, K part) pairs in equal shares, each taking an
-// equal share of the H / 4 output tiles; a workgroup stages its rows' K part of h in LDS
-// once (8 x 2048 bf16, swizzled as xlds_piece lays out) and streams its tiles; the fp32
-// sums go to ypart[part][row][c], which the combine adds in part order
-// (model/moe_layer.py:186-191 after the expert's w2).
-constexpr int kMidDownStages = 4;
-constexpr int kMidDownVals = kMidDownStages * kStageVals;  // K values of one part
-constexpr int kMidDownRows = 16;                           // rows of a down virtual expert
+// Down projection of mid-size batches on the 16x16x32 MFMA: virtual experts of up to 16 h
+// rows, F split into parts of 2048 values (one fp32 ypart plane per part, which the combine
+// adds in part order, model/moe_layer.py:186-191 after the expert's w2).  The workgroups are
+// dealt to the (virtual expert, part) pairs in equal shares, each taking an equal share of
+// the pair's 64-row output tiles one at a time; wave w covers values [256 w, 256 w + 256)
+// of the part, so its slice of the expert's h rows stays in registers.  The tile is four
+// 16-row MFMA column blocks, loaded and scaled as in mid16_gateup_kernel (two 64-byte loads
+// per row of a block: four NF4 blocks); the eight waves' partial sums meet in LDS.
+constexpr int kM16DownCols = 4;                      // 16-row column blocks of an output tile
+constexpr int kM16DownTile = 16 * kM16DownCols;      // output rows of a tile
+constexpr int kM16DownSlice = 256;                   // values of F of a wave's slice
+constexpr int kM16DownPlane = kDecWaves * kM16DownSlice;  // values of F of a part (2048)
+constexpr int kMidDownVals = kM16DownPlane;  // K values of one part (one ypart plane)
 
 __global__ void __launch_bounds__(kDecThreads, 1)
-mid_down_kernel(const ExpertTable tab, const uint16_t *__restrict__ h, int H, int F, int E,
-                int parts, int rows_total, const Route rt, float *__restrict__ ypart) {
-  constexpr int NSQ = kMidDownStages;
+mid16_down_kernel(const ExpertTable tab, const uint16_t *__restrict__ h, int H, int F, int E,
+                  int parts, int rows_total, const Route rt, float *__restrict__ ypart) {
   __shared__ __attribute__((aligned(16))) uint32_t s_tbl[kTableWords];
-  __shared__ uint4 s_ht[kMidDownRows * kMidDownVals / 8];
-  __shared__ __attribute__((aligned(16))) float s_aslot[kDecWaves][2 * kASlotFloats];
-  __shared__ int32_t s_ticket;
+  // Partial sums [buffer][wave][column block][r * 64 + lane] (16 floats of padding per block
+  // spread the reads of one wave over all banks).
+  constexpr int kPlane = 4 * kWave + 16;
+  __shared__ float s_red[2][kDecWaves][kM16DownCols][kPlane];
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  if (tid == 0) s_ticket = 0;
   const int cnt = (lane < E && tab.e[lane < E ? lane : 0].w2_packed != nullptr) ? rt.counts[lane] : 0;
   const int off = lane < E ? rt.offsets[lane] : 0;
   {
@@ -1739,7 +1815,7 @@ mid_down_kernel(const ExpertTable tab, const uint16_t *__restrict__ h, int H, in
     for (int q = 0; q < 16; ++q) cst[q] = kNf4Code[q];
     build_table_regs<kDecThreads>(s_tbl, cst, cst);
   }
-  const int nv = (cnt + kMidDownRows - 1) / kMidDownRows;
+  const int nv = (cnt + kM16Rows - 1) / kM16Rows;
   int incl = nv;
 #pragma unroll
   for (int o = 1; o < kWave; o <<= 1) {
@@ -1755,37 +1831,32 @@ mid_down_kernel(const ExpertTable tab, const uint16_t *__restrict__ h, int H, in
   const int v = pr / parts, kp = pr - v * parts;
   const int e = __builtin_ctzll(__ballot(incl > v));
   const int vj = v - (__builtin_amdgcn_readlane(incl, e) - __builtin_amdgcn_readlane(nv, e));
-  const int r0 = __builtin_amdgcn_readlane(off, e) + kMidDownRows * vj;  // first h row
-  const int n = min(kMidDownRows, __builtin_amdgcn_readlane(cnt, e) - kMidDownRows * vj);
-  // Items are pairs of 4-row output tiles (an odd last tile is read twice, written once),
-  // or single tiles for more than 8 rows (four MFMA row groups: the registers of a second
-  // tile's stream do not fit beside them).
-  const int tiles = H >> 2;
-  const bool single = n > 8;
-  const int units = single ? tiles : (tiles + 1) >> 1;
-  const int t_lo = (int)((int64_t)(b - b0) * units / (b1 - b0));
-  const int t_hi = (int)((int64_t)(b - b0 + 1) * units / (b1 - b0));
+  const int r0 = __builtin_amdgcn_readlane(off, e) + kM16Rows * vj;  // first h row
+  const int n = min(kM16Rows, __builtin_amdgcn_readlane(cnt, e) - kM16Rows * vj);
+  const int tiles = H / kM16DownTile;
+  const int t_lo = (int)((int64_t)(b - b0) * tiles / (b1 - b0));
+  const int t_hi = (int)((int64_t)(b - b0 + 1) * tiles / (b1 - b0));
 
   const moe_nf4_expert_t &ex = tab.e[e];
   const float *c2 = (const float *)uniform_ptr(ex.w2_code);
-  const void *pk = uniform_ptr(ex.w2_packed);
-  const void *pa = uniform_ptr(ex.w2_absmax);
+  const uint8_t *pk = (const uint8_t *)uniform_ptr(ex.w2_packed);
+  const float *pa = (const float *)uniform_ptr(ex.w2_absmax);
+
+  // The wave's slice of the h rows as A operands (s, j), laid out as in mid16_gateup_kernel.
+  const int nl = lane & 15, kq = lane >> 4;
+  const int k0 = kp * kM16DownPlane + wave * kM16DownSlice;  // first value of the slice
+  const gx_t hrow = (gx_t)h + (size_t)(r0 + (nl < n ? nl : 0)) * F + k0 + m16_off(kq);
+  bf16x8 ha[2][4];
+#pragma unroll
+  for (int s = 0; s < 2; ++s)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) ha[s][j] = as_bf16x8(ld_u4(hrow + 128 * s + 64 * (j >> 1) + 8 * (j & 1)));
+
   float ref_f = kNf4Code[0];
 #pragma unroll
   for (int q = 1; q < 16; ++q)
     if ((lane & 15) == q) ref_f = kNf4Code[q];
   const float cv = c2[lane & 15];
-  // The rows' K part of h into LDS: piece q of the n x kMidDownVals block.
-  constexpr int ppr = kMidDownVals / 8;
-  constexpr int kPer = kMidDownRows * ppr / kDecThreads;
-  uint4 hv[kPer];
-#pragma unroll
-  for (int r = 0; r < kPer; ++r) {
-    const int q = tid + kDecThreads * r;
-    const int m = q / ppr;
-    if (m < n)
-      hv[r] = ld_u4((gx_t)h + (size_t)(r0 + m) * F + (size_t)kp * kMidDownVals + (size_t)(q - m * ppr) * 8);
-  }
   if (__ballot(lane < 16 && __builtin_bit_cast(uint32_t, cv) != __builtin_bit_cast(uint32_t, ref_f)) != 0) {
     float cc[16];
 #pragma unroll
@@ -1793,119 +1864,103 @@ mid_down_kernel(const ExpertTable tab, const uint16_t *__restrict__ h, int H, in
     __syncthreads();  // no wave still builds the constant table
     build_table_regs<kDecThreads>(s_tbl, cc, cc);
   }
-#pragma unroll
-  for (int r = 0; r < kPer; ++r) {
-    const int q = tid + kDecThreads * r;
-    const int m = q / ppr;
-    if (m < n) s_ht[xlds_piece(m, kMidDownVals, q - m * ppr)] = hv[r];
-  }
   __syncthreads();
+  if (t_lo >= t_hi) return;  // uniform over the workgroup
 
-  const int lanej = lane & 3;
-  const int blk = lane >> 2;
   const size_t row_bytes = (size_t)(F >> 1);
   const size_t row_blocks = (size_t)(F >> 6);
-  const uint32_t lane_const[2] = {(uint32_t)lane << 2, (uint32_t)lane << 2};
-  auto grab = [&]() -> int {
-    int t = 0;
-    if (lane == 0) t = __hip_atomic_fetch_add(&s_ticket, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    t = __builtin_amdgcn_readfirstlane(t) + t_lo;
-    return t < t_hi ? t : -1;
+  // Both table halves hold w2's codebook: the lanes spread over all 64 replicas.
+  const uint32_t lane_const = ((uint32_t)(lane & 31) << 2) | ((lane & 32) ? 128u : 0u);
+  struct TileRegs {
+    u32x4 w[kM16DownCols][2];
+    f32x4 ab[kM16DownCols];
   };
-  const bool bc = n == 1;
-  auto set_ptrs = [&](ItemPtr<2> &P, int tp) {
+  auto load_w = [&](TileRegs &R, int t, int cb, int s) {
+    const size_t row = (size_t)t * kM16DownTile + 16 * cb + nl;
+    R.w[cb][s] = *reinterpret_cast<const MOE_GLOBAL u32x4 *>(
+        (gq_t)pk + row * row_bytes + (size_t)(k0 >> 1) + 16 * kq + 64 * s);
+  };
+  auto load_ab = [&](TileRegs &R, int t) {
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const int tl = min(2 * tp + q, tiles - 1);
-      const size_t row = (size_t)tl * 4 + lanej;
-      P.wq[q] = (gq_t)pk + row * row_bytes + (size_t)kp * (NSQ * 256) + blk * 16;
-      P.wa[q] = (ga_t)pa + row * row_blocks + (size_t)kp * (NSQ * 8) + (blk >> 1);
-      P.ab[q] = (ga_t)pa + (size_t)tl * 4 * row_blocks + (size_t)kp * (NSQ * 8);
-    }
-    P.ap = (gx_t)h;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int m = 4 * (i >> 2) + lanej;
-      P.xo[i] = bc ? xlds_piece(0, kMidDownVals, 4 * blk + lanej)
-                   : xlds_piece(m < n ? m : 0, kMidDownVals, 4 * blk + (i & 3));
+    for (int cb = 0; cb < kM16DownCols; ++cb) {
+      const size_t row = (size_t)t * kM16DownTile + 16 * cb + nl;
+      R.ab[cb] = *reinterpret_cast<const MOE_GLOBAL f32x4 *>((ga_t)pa + row * row_blocks + (k0 >> 6));
     }
   };
-  auto finish = [&](auto &ac, int tp, auto ng_tag) {
-    constexpr int NGF = decltype(ng_tag)::value;
-    const int nrows = bc ? 1 : 4;
-    float vs[2][NGF][4];
+  auto load_tile = [&](TileRegs &R, int t) {
 #pragma unroll
-    for (int p = 0; p < 2; ++p)
+    for (int cb = 0; cb < kM16DownCols; ++cb)
 #pragma unroll
-      for (int g = 0; g < NGF; ++g)
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          if (q < nrows) vs[p][g][q] = lanes_sum16(ac[p * NGF + g][q]);
-    if (blk == 0) {
-#pragma unroll
-      for (int p = 0; p < 2; ++p) {
-        const int tl = 2 * tp + p;
-        if (tl < tiles) {
-          const int c = tl * 4 + lanej;
-#pragma unroll
-          for (int g = 0; g < NGF; ++g)
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              const int m = 4 * g + q;
-              if (q < nrows && m < n) ypart[((size_t)kp * rows_total + r0 + m) * H + c] = vs[p][g][q];
-            }
-        }
-      }
-    }
+      for (int s = 0; s < 2; ++s) load_w(R, t, cb, s);
+    load_ab(R, t);
   };
-  auto hook = [&]() {};
-  const uint16_t *xl = reinterpret_cast<const uint16_t *>(s_ht);
-  if (bc) {
-    auto fin = [&](f32x4 (&ac)[2], int i) { finish(ac, i, std::integral_constant<int, 1>{}); };
-    stream_aligned<2, NSQ, 4, true, kXLds, true, 1, true>(grab, set_ptrs, fin, hook, s_tbl, lane_const,
-                                                     row_blocks, s_aslot[wave], xl, (gq_t)h);
-  } else if (n <= 4) {
-    auto fin = [&](f32x4 (&ac)[2], int i) { finish(ac, i, std::integral_constant<int, 1>{}); };
-    stream_aligned<2, NSQ, 4, false, kXLds, true, 1, true>(grab, set_ptrs, fin, hook, s_tbl, lane_const,
-                                                      row_blocks, s_aslot[wave], xl, (gq_t)h);
-  } else if (n <= 8) {
-    auto fin = [&](f32x4 (&ac)[4], int i) { finish(ac, i, std::integral_constant<int, 2>{}); };
-    stream_aligned<2, NSQ, 4, false, kXLds, true, 2, true>(grab, set_ptrs, fin, hook, s_tbl, lane_const,
-                                                      row_blocks, s_aslot[wave], xl, (gq_t)h);
-  } else {
-    auto set_ptrs1 = [&](ItemPtr<1> &P, int tl) {
-      const size_t row = (size_t)tl * 4 + lanej;
-      P.wq[0] = (gq_t)pk + row * row_bytes + (size_t)kp * (NSQ * 256) + blk * 16;
-      P.wa[0] = (ga_t)pa + row * row_blocks + (size_t)kp * (NSQ * 8) + (blk >> 1);
-      P.ab[0] = (ga_t)pa + (size_t)tl * 4 * row_blocks + (size_t)kp * (NSQ * 8);
-      P.ap = (gx_t)h;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int m = 4 * (i >> 2) + lanej;
-        P.xo[i] = xlds_piece(m < n ? m : 0, kMidDownVals, 4 * blk + (i & 3));
-      }
+  int buf = 0;
+  constexpr int kSteps = 2 * kM16DownCols;
+  // Tile t from R (then tile t_next's loads into R); ypart rows written when `live`.  The
+  // table lookups of step i + 1 go out before the MFMAs of step i.
+  auto tile_step = [&](TileRegs &R, int t, int t_next, bool live) {
+    auto lookups = [&](int i, bf16x8 (&bo)[4]) {
+      const int cb = i >> 1, s = i & 1;
+      const u32x4 w = R.w[cb][s];
+      load_w(R, t_next, cb, s);
+      const auto lo = __builtin_amdgcn_permlane32_swap(w[0], w[2], false, false);
+      const auto hi = __builtin_amdgcn_permlane32_swap(w[1], w[3], false, false);
+      bo[0] = m16_lookup(s_tbl, lo[0], lane_const);
+      bo[1] = m16_lookup(s_tbl, hi[0], lane_const);
+      bo[2] = m16_lookup(s_tbl, lo[1], lane_const);
+      bo[3] = m16_lookup(s_tbl, hi[1], lane_const);
     };
-    auto fin = [&](f32x4 (&ac)[4], int tl) {
-      float vs[4][4];
+    f32x4 acc[kM16DownCols];
 #pragma unroll
-      for (int g = 0; g < 4; ++g)
+    for (int cb = 0; cb < kM16DownCols; ++cb) acc[cb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    bf16x8 bc[4], bn[4];
+    lookups(0, bc);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) vs[g][q] = lanes_sum16(ac[g][q]);
-      if (blk == 0) {
-        const int c = tl * 4 + lanej;
+    for (int i = 0; i < kSteps; ++i) {
+      const int cb = i >> 1, s = i & 1;
+      if (i + 1 < kSteps) lookups(i + 1, bn);
+      __builtin_amdgcn_sched_barrier(0);
+      f32x4 ta = f32x4{0.0f, 0.0f, 0.0f, 0.0f}, tb = ta;
+      ta = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ha[s][0], bc[0], ta, 0, 0, 0);
+      ta = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ha[s][1], bc[1], ta, 0, 0, 0);
+      tb = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ha[s][2], bc[2], tb, 0, 0, 0);
+      tb = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ha[s][3], bc[3], tb, 0, 0, 0);
+      scale_acc(acc[cb], ta, R.ab[cb][2 * s]);
+      scale_acc(acc[cb], tb, R.ab[cb][2 * s + 1]);
+      if (i + 1 < kSteps) {
 #pragma unroll
-        for (int g = 0; g < 4; ++g)
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const int m = 4 * g + q;
-            if (m < n) ypart[((size_t)kp * rows_total + r0 + m) * H + c] = vs[g][q];
-          }
+        for (int j = 0; j < 4; ++j) bc[j] = bn[j];
       }
-    };
-    const uint32_t lane_const1[1] = {(uint32_t)lane << 2};
-    stream_aligned<1, NSQ, 4, false, kXLds, true, 4, true>(grab, set_ptrs1, fin, hook, s_tbl,
-                                                           lane_const1, row_blocks, s_aslot[wave],
-                                                           xl, (gq_t)h);
+    }
+#pragma unroll
+    for (int cb = 0; cb < kM16DownCols; ++cb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) s_red[buf][wave][cb][r * kWave + lane] = acc[cb][r];
+    load_ab(R, t_next);
+    lds_barrier();
+    if (live) {
+      // Output row c of the tile, token rows m and m + 8: D[m][c % 16] of block c / 16 is
+      // register m & 3 of lane 16 (m >> 2) + c % 16.
+      const int c = tid & (kM16DownTile - 1);
+#pragma unroll
+      for (int hm = 0; hm < 2; ++hm) {
+        const int m = (tid >> 6) + 8 * hm;
+        const int idx = (m & 3) * kWave + 16 * (m >> 2) + (c & 15);
+        float y = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kDecWaves; ++w) y += s_red[buf][w][c >> 4][idx];
+        if (m < n) ypart[((size_t)kp * rows_total + r0 + m) * H + (size_t)t * kM16DownTile + c] = y;
+      }
+    }
+    buf ^= 1;
+  };
+  const int last = t_hi - 1;
+  TileRegs A, B;
+  load_tile(A, t_lo);
+  load_tile(B, min(t_lo + 1, last));
+  for (int t = t_lo; t < t_hi; t += 2) {
+    tile_step(A, t, min(t + 2, last), true);
+    tile_step(B, min(t + 1, last), min(t + 3, last), t + 1 < t_hi);
   }
 }
 
@@ -1939,18 +1994,17 @@ bool decode_layer_supported(int64_t T, int32_t k, int32_t E, int32_t H, int32_t 
 int64_t decode_route_bytes() { return (int64_t)sizeof(DecodeRoute); }
 int64_t mid_route_out_bytes() { return (int64_t)sizeof(MidRouteOut); }
 
-// The mid-size gate/up path: up to 16 tokens (at most two virtual experts per expert),
-// hidden size 2048 or 4096 (four or eight pipeline stages per row), at most 32 experts.
-// Up to 16 tokens.  At 32 (Mixtral decode: ~8 rows per expert, 25-30 for a hot one) this
-// path measured slower than the 32-row tiles of the mid-batch kernels (Zipf 214 against
-// 162 us per layer, uniform 257 against 255): more than 8 rows take four MFMA row groups,
-// whose 64 LDS bytes of activations per lane, stage and group bound the stream.
-constexpr int kMidMaxTokens = 16;
+// The mid-size path: up to 64 tokens, hidden size 2048 or 4096 (a wave's K slice of 256 or
+// 512 values), F a multiple of 16, at most 32 experts.  At 64 tokens (Mixtral, ~16 rows per
+// expert) it still measured ahead of the 32-row tiles of the streamed mid-batch kernels
+// (uniform 278 against 281 us per layer, Zipf 216 against 238), at 32 and 40 tokens by
+// 20-24 % (uniform 216 / 215 against 270 / 271).
+constexpr int kMidMaxTokens = 64;
 
 bool mid_gateup_supported(int64_t T, int32_t k, int32_t E, int32_t H, int32_t F) {
   return T >= 1 && T <= kMidMaxTokens && k >= 1 && E >= 1 && E <= kWave / 2 &&
-         (H == 2048 || H == 4096) && F >= 4 && F % 4 == 0 && T * (int64_t)H * 2 >= 2048 &&
-         (int64_t)E + T * k / kMidRows + 1 <= device_cu_count();
+         (H == 2048 || H == 4096) && F >= kM16Rows && F % kM16Rows == 0 &&
+         T * (int64_t)H * 2 >= 2048 && (int64_t)E + T * k / kM16Rows + 1 <= device_cu_count();
 }
 
 // The same path with the routing and grouping in the kernel (every workgroup routes the
@@ -1960,12 +2014,11 @@ bool mid_layer_supported(int64_t T, int32_t k, int32_t E, int32_t H, int32_t F) 
          T * k <= kMidMaxSlots;
 }
 
-// The mid-size down projection: F a multiple of 4 x 512 (parts of four stages), at most 16
-// parts (the combine's plane limit), H a multiple of 4 and h at least 2 KB (the past-the-end
-// prefetches read it).
+// The mid-size down projection: F a multiple of 2048 (the parts), at most 16 parts (the
+// combine's plane limit), H a multiple of the 64-row output tile.
 bool mid_down_supported(int64_t T, int32_t k, int32_t E, int32_t H, int32_t F) {
   return mid_gateup_supported(T, k, E, H, F) && F % kMidDownVals == 0 &&
-         F / kMidDownVals <= 16 && H % 4 == 0 && T * k * (int64_t)F * 2 >= 2048;
+         F / kMidDownVals <= 16 && H % kM16DownTile == 0;
 }
 int mid_down_parts(int32_t F) { return F / kMidDownVals; }
 
@@ -1976,7 +2029,7 @@ int launch_mid_down(const void *tab_v, const void *h, int64_t T, int32_t k, int3
   MOE_REQUIRE(((uintptr_t)h % 16) == 0, "h must be 16-byte aligned");
   const ExpertTable &tab = *static_cast<const ExpertTable *>(tab_v);
   const Route &rt = *static_cast<const Route *>(route_v);
-  hipLaunchKernelGGL(mid_down_kernel, dim3((unsigned)device_cu_count()), dim3(kDecThreads), 0, s,
+  hipLaunchKernelGGL(mid16_down_kernel, dim3((unsigned)device_cu_count()), dim3(kDecThreads), 0, s,
                      tab, (const uint16_t *)h, H, F, E, parts, (int)(T * k), rt, (float *)ypart);
   MOE_LAUNCH_CHECK();
   return MOE_STATUS_OK;
@@ -2004,11 +2057,11 @@ int launch_mid_gateup(const void *tab_v, const void *x, int64_t T, int32_t k, in
                        (uint16_t *)h_ws);
   };
   if (route_out == nullptr)
-    go(H == 4096 ? mid_gateup_kernel<8, 8, false> : mid_gateup_kernel<4, 8, false>);
+    go(H == 4096 ? mid16_gateup_kernel<4, 8, false> : mid16_gateup_kernel<2, 8, false>);
   else if (E <= 8)
-    go(H == 4096 ? mid_gateup_kernel<8, 8, true> : mid_gateup_kernel<4, 8, true>);
+    go(H == 4096 ? mid16_gateup_kernel<4, 8, true> : mid16_gateup_kernel<2, 8, true>);
   else
-    go(H == 4096 ? mid_gateup_kernel<8, 16, true> : mid_gateup_kernel<4, 16, true>);
+    go(H == 4096 ? mid16_gateup_kernel<4, 16, true> : mid16_gateup_kernel<2, 16, true>);
   MOE_LAUNCH_CHECK();
   return MOE_STATUS_OK;
 }

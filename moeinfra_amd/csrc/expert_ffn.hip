@@ -542,15 +542,15 @@ int launch_expert_ffn(const moe_nf4_expert_t *experts, int32_t E, const void *x,
   if (nsplit == 1 && gemv4_supported(max_tokens_per_expert, H, F))
     return launch_gemv4(&tab, x, H, F, &rt, h_ws, ypart, phases, active_max, rows_total, fused,
                         stream);
-  // Mid-size batches (up to 16 tokens): gate/up as the decode stream with one virtual expert
-  // (<= 8 token rows of one expert, staged in LDS) per workgroup; the down projection takes
-  // the path chosen below.
+  // Mid-size batches (up to 64 tokens): gate/up on 16-row weight tiles of "virtual experts"
+  // (<= 16 token rows of one expert) with each wave's K slice of the tokens in registers
+  // (decode_layer.hip); the down projection takes the path chosen below.
   if ((phases & 1) && fused == nullptr && mid_gateup_supported(T, k, E, H, F)) {
     const int rc = launch_mid_gateup(&tab, x, T, k, H, F, E, &rt, h_ws, stream, nullptr);
     if (rc != MOE_STATUS_OK || !(phases & 2)) return rc;
     phases &= ~1;
   }
-  // Its down projection: the same virtual experts over parts of four stages of F, when the
+  // Its down projection: the same virtual experts over parts of 2048 values of F, when the
   // caller's plane count is that part count.
   if ((phases & 2) && fused == nullptr && mid_down_supported(T, k, E, H, F) &&
       nsplit == mid_down_parts(F))
