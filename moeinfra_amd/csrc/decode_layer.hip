@@ -1638,42 +1638,10 @@ mid16_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x, int T
   const float *pa[2] = {(const float *)uniform_ptr(ex.w1_absmax),
                         (const float *)uniform_ptr(ex.w3_absmax)};
 
-  // The wave's K slice of the token rows, as A operands (s, j): lane (m = lane & 15, kq) holds
-  // values kM16Off[kq] + 8 (j & 1) .. +7 of block 2s + (j >> 1) of the slice of token row m
-  // (the first row again past n).
+  // Stream pointers of the lane (row nl of a tile, bytes 16 kq of the wave's slice); the
+  // first two tiles' loads go out before the activations' and the barrier below.
   const int nl = lane & 15, kq = lane >> 4;
-  const int tok = g_ptok[r0 + (nl < n ? nl : 0)];
   constexpr int kSlice = 128 * S;  // values of a wave's K slice (H / 8)
-  const gx_t xrow = (gx_t)x + (size_t)tok * H + (size_t)wave * kSlice + m16_off(kq);
-  bf16x8 xa[S][4];
-#pragma unroll
-  for (int s = 0; s < S; ++s)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) xa[s][j] = as_bf16x8(ld_u4(xrow + 128 * s + 64 * (j >> 1) + 8 * (j & 1)));
-
-  // An expert whose w1 / w3 codebooks differ bitwise from the NF4 constants gets a table of
-  // its own (replicas 0-31 w1, 32-63 w3).
-  float ref_f = kNf4Code[0];
-#pragma unroll
-  for (int q = 1; q < 16; ++q)
-    if ((lane & 15) == q) ref_f = kNf4Code[q];
-  const float cv = lane < 16 ? c1[lane & 15] : c3[lane & 15];
-  const bool differ =
-      __ballot(lane < 32 && __builtin_bit_cast(uint32_t, cv) != __builtin_bit_cast(uint32_t, ref_f)) != 0;
-  if (differ) {
-    float ca[16], cb[16];
-#pragma unroll
-    for (int q = 0; q < 16; ++q) {
-      ca[q] = c1[q];
-      cb[q] = c3[q];
-    }
-    __syncthreads();  // no wave still builds the constant table
-    build_table_regs<kDecThreads>(s_tbl, ca, cb);
-  }
-  __syncthreads();
-  if (t_lo >= t_hi) return;  // uniform over the workgroup
-
-  // Stream pointers of the lane (row nl of a tile, bytes 16 kq of the wave's slice).
   const size_t row_bytes = (size_t)(H >> 1);
   const size_t row_blocks = (size_t)(H >> 6);
   const uint32_t lane_const[2] = {(uint32_t)(lane & 31) << 2, ((uint32_t)(lane & 31) << 2) | 128u};
@@ -1681,23 +1649,6 @@ mid16_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x, int T
     u32x4 w[2][S];
     f32x4 ab[2][S / 2];
   };
-  auto load_tile = [&](TileRegs &R, int t) {
-    const size_t row = (size_t)t * kM16Rows + nl;
-#pragma unroll
-    for (int p = 0; p < 2; ++p) {
-      const gq_t wp = (gq_t)pk[p] + row * row_bytes + (size_t)wave * (kSlice / 2) + 16 * kq;
-#pragma unroll
-      for (int s = 0; s < S; ++s) R.w[p][s] = *reinterpret_cast<const MOE_GLOBAL u32x4 *>(wp + 64 * s);
-    }
-#pragma unroll
-    for (int p = 0; p < 2; ++p) {
-      const ga_t ap = (ga_t)pa[p] + row * row_blocks + (size_t)wave * (2 * S);
-#pragma unroll
-      for (int q = 0; q < S / 2; ++q) R.ab[p][q] = *reinterpret_cast<const MOE_GLOBAL f32x4 *>(ap + 4 * q);
-    }
-  };
-  // Tiles alternate between two register sets; each load of tile t + 2 goes out as soon as
-  // tile t's data in that slot is used, so two tiles of loads stay in flight.
   auto load_w = [&](TileRegs &R, int t, int p, int s) {
     const size_t row = (size_t)t * kM16Rows + nl;
     R.w[p][s] = *reinterpret_cast<const MOE_GLOBAL u32x4 *>(
@@ -1712,22 +1663,80 @@ mid16_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x, int T
       for (int q = 0; q < S / 2; ++q) R.ab[p][q] = *reinterpret_cast<const MOE_GLOBAL f32x4 *>(ap + 4 * q);
     }
   };
+  auto load_tile = [&](TileRegs &R, int t) {
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+#pragma unroll
+      for (int s = 0; s < S; ++s) load_w(R, t, p, s);
+    load_ab(R, t);
+  };
+  // Past the last tile the loads re-read it (L2, unused); a workgroup without tiles (more
+  // workgroups than tiles) reads the expert's first tile and stops at the barrier.
+  const int last = t_hi > t_lo ? t_hi - 1 : 0;
+  TileRegs A, B;
+  load_tile(A, min(t_lo, last));
+
+  // The wave's K slice of the token rows, as A operands (s, j): lane (m = lane & 15, kq) holds
+  // values kM16Off[kq] + 8 (j & 1) .. +7 of block 2s + (j >> 1) of the slice of token row m
+  // (the first row again past n).
+  const int tok = g_ptok[r0 + (nl < n ? nl : 0)];
+  const gx_t xrow = (gx_t)x + (size_t)tok * H + (size_t)wave * kSlice + m16_off(kq);
+  bf16x8 xa[S][4];
+#pragma unroll
+  for (int s = 0; s < S; ++s)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) xa[s][j] = as_bf16x8(ld_u4(xrow + 128 * s + 64 * (j >> 1) + 8 * (j & 1)));
+  load_tile(B, min(t_lo + 1, last));
+
+  // An expert whose w1 / w3 codebooks differ bitwise from the NF4 constants gets a table of
+  // its own (replicas 0-31 w1, 32-63 w3).  LDS-only barriers: the weight loads stay in flight.
+  float ref_f = kNf4Code[0];
+#pragma unroll
+  for (int q = 1; q < 16; ++q)
+    if ((lane & 15) == q) ref_f = kNf4Code[q];
+  const float cv = lane < 16 ? c1[lane & 15] : c3[lane & 15];
+  const bool differ =
+      __ballot(lane < 32 && __builtin_bit_cast(uint32_t, cv) != __builtin_bit_cast(uint32_t, ref_f)) != 0;
+  if (differ) {
+    float ca[16], cb[16];
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      ca[q] = c1[q];
+      cb[q] = c3[q];
+    }
+    lds_barrier();  // no wave still builds the constant table
+    build_table_regs<kDecThreads>(s_tbl, ca, cb);
+  }
+  lds_barrier();
+  if (t_lo >= t_hi) return;  // uniform over the workgroup
+
   int buf = 0;
   // Tile t from R (then tile t_next's loads into R); h rows written when `live`.  The steps
   // (projection p, load s) are software-pipelined: the table lookups of step i + 1 go out
   // before the MFMAs of step i.
   constexpr int kSteps = 2 * S;
   auto tile_step = [&](TileRegs &R, int t, int t_next, bool live) {
+    // The slot's next load goes out only after its last use (the lookup addresses), so that
+    // it can take the same registers: a load into other registers would need a copy at the
+    // loop's back edge, which waits for it.
     auto lookups = [&](int i, bf16x8 (&bo)[4]) {
       const int p = i / S, s = i % S;
       const u32x4 w = R.w[p][s];
-      load_w(R, t_next, p, s);
       const auto lo = __builtin_amdgcn_permlane32_swap(w[0], w[2], false, false);
       const auto hi = __builtin_amdgcn_permlane32_swap(w[1], w[3], false, false);
-      bo[0] = m16_lookup(s_tbl, lo[0], lane_const[p]);
-      bo[1] = m16_lookup(s_tbl, hi[0], lane_const[p]);
-      bo[2] = m16_lookup(s_tbl, lo[1], lane_const[p]);
-      bo[3] = m16_lookup(s_tbl, hi[1], lane_const[p]);
+      const uint32_t src[4] = {lo[0], hi[0], lo[1], hi[1]};
+      uint32_t addr[4][4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          addr[q][j] = __builtin_amdgcn_perm(src[q], lane_const[p], 0x0c0c0400u + (j << 8));
+      __builtin_amdgcn_sched_barrier(0);
+      load_w(R, t_next, p, s);
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        bo[q] = as_bf16x8(lds_lookup(s_tbl, addr[q][0]), lds_lookup(s_tbl, addr[q][1]),
+                          lds_lookup(s_tbl, addr[q][2]), lds_lookup(s_tbl, addr[q][3]));
     };
     f32x4 acc[2];
     acc[0] = acc[1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -1769,12 +1778,7 @@ mid16_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x, int T
     }
     buf ^= 1;
   };
-  // Past the last tile the loads re-read it (L2, unused); an odd count ends with one more
-  // pass over the last tile whose h rows are not written.
-  const int last = t_hi - 1;
-  TileRegs A, B;
-  load_tile(A, t_lo);
-  load_tile(B, min(t_lo + 1, last));
+  // An odd count ends with one more pass over the last tile whose h rows are not written.
   for (int t = t_lo; t < t_hi; t += 2) {
     tile_step(A, t, min(t + 2, last), true);
     tile_step(B, min(t + 1, last), min(t + 3, last), t + 1 < t_hi);
@@ -1842,31 +1846,8 @@ mid16_down_kernel(const ExpertTable tab, const uint16_t *__restrict__ h, int H, 
   const uint8_t *pk = (const uint8_t *)uniform_ptr(ex.w2_packed);
   const float *pa = (const float *)uniform_ptr(ex.w2_absmax);
 
-  // The wave's slice of the h rows as A operands (s, j), laid out as in mid16_gateup_kernel.
   const int nl = lane & 15, kq = lane >> 4;
-  const int k0 = kp * kM16DownPlane + wave * kM16DownSlice;  // first value of the slice
-  const gx_t hrow = (gx_t)h + (size_t)(r0 + (nl < n ? nl : 0)) * F + k0 + m16_off(kq);
-  bf16x8 ha[2][4];
-#pragma unroll
-  for (int s = 0; s < 2; ++s)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) ha[s][j] = as_bf16x8(ld_u4(hrow + 128 * s + 64 * (j >> 1) + 8 * (j & 1)));
-
-  float ref_f = kNf4Code[0];
-#pragma unroll
-  for (int q = 1; q < 16; ++q)
-    if ((lane & 15) == q) ref_f = kNf4Code[q];
-  const float cv = c2[lane & 15];
-  if (__ballot(lane < 16 && __builtin_bit_cast(uint32_t, cv) != __builtin_bit_cast(uint32_t, ref_f)) != 0) {
-    float cc[16];
-#pragma unroll
-    for (int q = 0; q < 16; ++q) cc[q] = c2[q];
-    __syncthreads();  // no wave still builds the constant table
-    build_table_regs<kDecThreads>(s_tbl, cc, cc);
-  }
-  __syncthreads();
-  if (t_lo >= t_hi) return;  // uniform over the workgroup
-
+  const int k0 = kp * kM16DownPlane + wave * kM16DownSlice;  // first value of the wave's slice
   const size_t row_bytes = (size_t)(F >> 1);
   const size_t row_blocks = (size_t)(F >> 6);
   // Both table halves hold w2's codebook: the lanes spread over all 64 replicas.
@@ -1894,21 +1875,59 @@ mid16_down_kernel(const ExpertTable tab, const uint16_t *__restrict__ h, int H, 
       for (int s = 0; s < 2; ++s) load_w(R, t, cb, s);
     load_ab(R, t);
   };
+  // The first two tiles' loads go out before the h rows' and the barrier below (past the last
+  // tile the loads re-read it; a workgroup without tiles reads the first and stops there).
+  const int last = t_hi > t_lo ? t_hi - 1 : 0;
+  TileRegs A, B;
+  load_tile(A, min(t_lo, last));
+
+  // The wave's slice of the h rows as A operands (s, j), laid out as in mid16_gateup_kernel.
+  const gx_t hrow = (gx_t)h + (size_t)(r0 + (nl < n ? nl : 0)) * F + k0 + m16_off(kq);
+  bf16x8 ha[2][4];
+#pragma unroll
+  for (int s = 0; s < 2; ++s)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) ha[s][j] = as_bf16x8(ld_u4(hrow + 128 * s + 64 * (j >> 1) + 8 * (j & 1)));
+  load_tile(B, min(t_lo + 1, last));
+
+  float ref_f = kNf4Code[0];
+#pragma unroll
+  for (int q = 1; q < 16; ++q)
+    if ((lane & 15) == q) ref_f = kNf4Code[q];
+  const float cv = c2[lane & 15];
+  if (__ballot(lane < 16 && __builtin_bit_cast(uint32_t, cv) != __builtin_bit_cast(uint32_t, ref_f)) != 0) {
+    float cc[16];
+#pragma unroll
+    for (int q = 0; q < 16; ++q) cc[q] = c2[q];
+    lds_barrier();  // no wave still builds the constant table
+    build_table_regs<kDecThreads>(s_tbl, cc, cc);
+  }
+  lds_barrier();  // LDS only: the weight loads stay in flight
+  if (t_lo >= t_hi) return;  // uniform over the workgroup
+
   int buf = 0;
   constexpr int kSteps = 2 * kM16DownCols;
   // Tile t from R (then tile t_next's loads into R); ypart rows written when `live`.  The
   // table lookups of step i + 1 go out before the MFMAs of step i.
   auto tile_step = [&](TileRegs &R, int t, int t_next, bool live) {
-    auto lookups = [&](int i, bf16x8 (&bo)[4]) {
+    auto lookups = [&](int i, bf16x8 (&bo)[4]) {  // the next load after the last use
       const int cb = i >> 1, s = i & 1;
       const u32x4 w = R.w[cb][s];
-      load_w(R, t_next, cb, s);
       const auto lo = __builtin_amdgcn_permlane32_swap(w[0], w[2], false, false);
       const auto hi = __builtin_amdgcn_permlane32_swap(w[1], w[3], false, false);
-      bo[0] = m16_lookup(s_tbl, lo[0], lane_const);
-      bo[1] = m16_lookup(s_tbl, hi[0], lane_const);
-      bo[2] = m16_lookup(s_tbl, lo[1], lane_const);
-      bo[3] = m16_lookup(s_tbl, hi[1], lane_const);
+      const uint32_t src[4] = {lo[0], hi[0], lo[1], hi[1]};
+      uint32_t addr[4][4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          addr[q][j] = __builtin_amdgcn_perm(src[q], lane_const, 0x0c0c0400u + (j << 8));
+      __builtin_amdgcn_sched_barrier(0);
+      load_w(R, t_next, cb, s);
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        bo[q] = as_bf16x8(lds_lookup(s_tbl, addr[q][0]), lds_lookup(s_tbl, addr[q][1]),
+                          lds_lookup(s_tbl, addr[q][2]), lds_lookup(s_tbl, addr[q][3]));
     };
     f32x4 acc[kM16DownCols];
 #pragma unroll
@@ -1954,10 +1973,6 @@ mid16_down_kernel(const ExpertTable tab, const uint16_t *__restrict__ h, int H, 
     }
     buf ^= 1;
   };
-  const int last = t_hi - 1;
-  TileRegs A, B;
-  load_tile(A, t_lo);
-  load_tile(B, min(t_lo + 1, last));
   for (int t = t_lo; t < t_hi; t += 2) {
     tile_step(A, t, min(t + 2, last), true);
     tile_step(B, min(t + 1, last), min(t + 3, last), t + 1 < t_hi);
