@@ -30,6 +30,7 @@ int launch_reduce_splits(const float *ypart, int nsplit, int64_t numel, uint16_t
                          hipStream_t stream);
 bool decode_layer_supported(int64_t T, int32_t k, int32_t E, int32_t H, int32_t F);
 bool mid_layer_supported(int64_t T, int32_t k, int32_t E, int32_t H, int32_t F);
+bool mid_group_supported(int64_t T, int32_t k, int32_t E, int32_t H, int32_t F);
 int launch_mid_layer_gateup(const moe_nf4_expert_t *experts, int32_t E, const void *x, int64_t T,
                             int32_t k, int32_t H, int32_t F, void *h_ws, const void *route_out,
                             hipStream_t stream);
@@ -191,6 +192,8 @@ int layer_forward(const moe_nf4_expert_t *experts, int32_t E, const void *gate_b
                                at<void>(workspace, w.h), s, ev, nullptr);
   if (ev) MOE_HIP_CHECK(hipEventRecord(ev[0], s));
   const bool mid = mid_layer_supported(T, k, E, H, F);
+  // Above that size the mid-size gate/up groups the router's slots itself (no permute launch).
+  const bool mid_group = !mid && mid_group_supported(T, k, E, H, F);
   const bool small = route_small_supported(T, k);
   int rc;
   if (mid) {
@@ -200,6 +203,15 @@ int layer_forward(const moe_nf4_expert_t *experts, int32_t E, const void *gate_b
     const MidRouteArgs ro{gate_bf16, bias_f32, logits_bf16, weights_f32, idx_i64, idx32, counts,
                           offsets, perm_tok, slot_pos, active};
     rc = launch_mid_layer_gateup(experts, E, x_bf16, T, k, H, F, at<void>(workspace, w.h), &ro, s);
+  } else if (mid_group) {
+    rc = moe_router_topk(x_bf16, gate_bf16, bias_f32, T, H, E, k, logits_bf16, weights_f32,
+                         idx_i64, idx32, s);
+    if (rc == MOE_STATUS_OK) {
+      if (ev) MOE_HIP_CHECK(hipEventRecord(ev[1], s));
+      const MidRouteArgs ro{nullptr, nullptr, nullptr, nullptr, nullptr, idx32, counts,
+                            offsets, perm_tok, slot_pos, active};
+      rc = launch_mid_layer_gateup(experts, E, x_bf16, T, k, H, F, at<void>(workspace, w.h), &ro, s);
+    }
   } else if (small) {
     rc = launch_route_small(x_bf16, gate_bf16, bias_f32, T, H, E, k, logits_bf16, weights_f32,
                             idx_i64, idx32, counts, offsets, perm_tok, slot_pos, active, counter,
@@ -211,7 +223,7 @@ int layer_forward(const moe_nf4_expert_t *experts, int32_t E, const void *gate_b
       rc = moe_permute(idx32, T, k, E, counts, offsets, perm_tok, slot_pos, active, s);
   }
   if (rc != MOE_STATUS_OK) return rc;
-  if (!mid) {
+  if (!mid && !mid_group) {
     if (ev) MOE_HIP_CHECK(hipEventRecord(ev[1], s));
     rc = launch_expert_ffn(experts, E, x_bf16, T, k, H, F, counts, offsets, perm_tok, active,
                            at<void>(workspace, w.h), at<void>(workspace, w.ypart), w.nsplit, T, 1,

@@ -1378,10 +1378,11 @@ decode_down_kernel(const ExpertTable tab, const DecodeRoute *__restrict__ route,
 // loads of one wave: at most four 128-value chunks).
 constexpr int kMidMaxH = 4096;
 
-// The routing a mid-size gate/up launch computes itself (ROUTE): the gate, the optional
-// per-expert logit bias, and where workgroup 0 writes the router's outputs (logits may be
-// null) and the grouping the down projection and the combine read (the layout of
-// moe_permute: offsets [E + 1], active = {n, ids ascending}, slot_pos of every slot).
+// The routing a mid-size gate/up launch computes itself: the gate, the optional per-expert
+// logit bias, and where workgroup 0 writes the router's outputs (logits may be null) and the
+// grouping the down projection and the combine read (the layout of moe_permute: offsets
+// [E + 1], active = {n, ids ascending}, slot_pos of every slot).  With a null gate the
+// launch only groups the slots of a separate router launch, read from idx32.
 struct MidRouteOut {
   const uint16_t *gate;
   const float *bias;
@@ -1397,6 +1398,69 @@ struct MidRouteOut {
 };
 constexpr int kMidMaxT = 16;
 constexpr int kMidMaxSlots = kMidMaxT * 2;
+constexpr int kMidGroupMaxSlots = 2 * kWave;  // slots the in-launch grouping takes
+// How a mid-size gate/up launch gets its grouping: from the caller (Route), by routing the
+// tokens itself, or by grouping the slots of a separate router launch.
+constexpr int kRtExternal = 0, kRtRoute = 1, kRtGroup = 2;
+
+// Grouping of ns <= 2 * kWave routed slots (slot s = t k + j routed to expert se) by expert,
+// ascending expert then slot (the order of moe_permute), by one wave: lane l holds slots l
+// and l + 64.  Fills s_cnt / s_off (rows and first row of every expert) and s_ptok (token
+// of every grouped row); with `publish`, also writes counts, offsets [E + 1], active =
+// {n, ids ascending}, slot_pos [ns] and perm_tok of ro.  Returns the grouped row of each of
+// the lane's slots in pos.
+__device__ __forceinline__ void mid_group(const int (&se)[2], int ns, int k, int E, int32_t *s_cnt,
+                                          int32_t *s_off, int32_t *s_ptok, bool publish,
+                                          const MidRouteOut &ro, int (&pos)[2]) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const uint64_t lt = (1ull << lane) - 1ull;
+  int run = 0, my_cnt = 0, my_off = 0;
+  uint32_t present = 0;
+  pos[0] = pos[1] = 0;
+  for (int xe = 0; xe < E; ++xe) {
+    const uint64_t m0 = __ballot(se[0] == xe), m1 = __ballot(se[1] == xe);
+    const int c0 = __builtin_popcountll(m0);
+    const int c = c0 + __builtin_popcountll(m1);
+    if (se[0] == xe) pos[0] = run + __builtin_popcountll(m0 & lt);
+    if (se[1] == xe) pos[1] = run + c0 + __builtin_popcountll(m1 & lt);
+    if (lane == xe) {
+      my_cnt = c;
+      my_off = run;
+    }
+    if (c > 0) present |= 1u << xe;
+    run += c;
+  }
+  if (lane < E) {
+    s_cnt[lane] = my_cnt;
+    s_off[lane] = my_off;
+  }
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int sl = lane + kWave * h;
+    if (sl < ns) s_ptok[pos[h]] = sl / k;
+  }
+  if (publish) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int sl = lane + kWave * h;
+      if (sl < ns) {
+        ro.slot_pos[sl] = pos[h];
+        ro.perm_tok[pos[h]] = sl / k;
+      }
+    }
+    if (lane < E) {
+      ro.counts[lane] = my_cnt;
+      ro.offsets[lane] = my_off;
+    }
+    if (lane == 0) {
+      ro.offsets[E] = ns;
+      ro.active[0] = __builtin_popcount(present);
+    }
+    // Active experts in ascending order: lane x writes its rank among the present ones.
+    if (lane < E && ((present >> lane) & 1u))
+      ro.active[1 + __builtin_popcount(present & ((1u << lane) - 1u))] = lane;
+  }
+}
 
 // Routing of the T <= kMidMaxT tokens of a mid-size launch, recomputed in every workgroup
 // (the gate is small and stays in L2): the gate products, per-token routing (route_rows),
@@ -1484,52 +1548,18 @@ __device__ __forceinline__ void mid_route(const uint16_t *__restrict__ x, int T,
     route_rows<EMAX, kDecWaves, kMidMaxT>(s_sle, s_slw, s_part, 4 * wave, ro.bias, T, E, k,
                                           blockIdx.x == 0 ? ro.logits : nullptr);
   __syncthreads();
-  // ---- grouping of the T k slots by expert (ascending expert, then slot), by wave 0.
+  // ---- grouping of the T k slots by expert (ascending expert, then slot), by wave 0;
+  // workgroup 0 also writes the router's outputs.
   if (wave == 0) {
     const int ns = T * k;
-    const int se = lane < ns ? s_sle[lane] : -1;
-    int before = 0, rank = 0, run = 0, my_cnt = 0, my_off = 0, n_act = 0;
-    uint32_t present = 0;
-    for (int xe = 0; xe < E; ++xe) {
-      const uint64_t m = __ballot(se == xe);
-      const int c = __builtin_popcountll(m);
-      if (se == xe) {
-        before = run;
-        rank = __builtin_popcountll(m & ((1ull << lane) - 1ull));
-      }
-      if (lane == xe) {
-        my_cnt = c;
-        my_off = run;
-      }
-      if (c > 0) present |= 1u << xe;
-      run += c;
-    }
-    if (lane < E) {
-      s_cnt[lane] = my_cnt;
-      s_off[lane] = my_off;
-    }
-    if (lane < ns) s_ptok[before + rank] = lane / k;
-    n_act = __builtin_popcount(present);
-    if (blockIdx.x == 0) {
-      if (lane < ns) {
-        const int t = lane / k, j = lane - (lane / k) * k;
-        ro.w[t * k + j] = s_slw[lane];
-        ro.idx64[t * k + j] = se;
-        ro.idx32[t * k + j] = se;
-        ro.slot_pos[lane] = before + rank;
-        ro.perm_tok[before + rank] = t;
-      }
-      if (lane < E) {
-        ro.counts[lane] = my_cnt;
-        ro.offsets[lane] = my_off;
-      }
-      if (lane == 0) {
-        ro.offsets[E] = ns;
-        ro.active[0] = n_act;
-      }
-      // Active experts in ascending order: lane x writes its rank among the present ones.
-      if (lane < E && ((present >> lane) & 1u))
-        ro.active[1 + __builtin_popcount(present & ((1u << lane) - 1u))] = lane;
+    const int se[2] = {lane < ns ? s_sle[lane] : -1, -1};
+    int pos[2];
+    mid_group(se, ns, k, E, s_cnt, s_off, s_ptok, blockIdx.x == 0, ro, pos);
+    if (blockIdx.x == 0 && lane < ns) {
+      const int t = lane / k, j = lane - (lane / k) * k;
+      ro.w[t * k + j] = s_slw[lane];
+      ro.idx64[t * k + j] = se[0];
+      ro.idx32[t * k + j] = se[0];
     }
   }
   __syncthreads();  // the grouping is visible; the gate partials are dead
@@ -1570,7 +1600,7 @@ __device__ __forceinline__ bf16x8 m16_lookup(const uint32_t *tbl, uint32_t w, ui
   return as_bf16x8(l[0], l[1], l[2], l[3]);
 }
 
-template <int S, int EMAX, bool ROUTE>
+template <int S, int EMAX, int RT>
 __global__ void __launch_bounds__(kDecThreads, 1)
 mid16_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x, int T, int H, int F,
                     int E, int k, const Route rt, const MidRouteOut ro,
@@ -1580,10 +1610,11 @@ mid16_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x, int T
   // The waves' partial sums of a tile [buffer][wave][projection][4 lane + r]; before the
   // first tile (ROUTE) the waves' gate partials.
   __shared__ __attribute__((aligned(16))) float s_red[2][kDecWaves][2][kWave * 4];
+  constexpr bool ROUTE = RT == kRtRoute;
   __shared__ int32_t s_sle[ROUTE ? kMidMaxSlots : 1];
   __shared__ float s_slw[ROUTE ? kMidMaxSlots : 1];
-  __shared__ int32_t s_cnt[ROUTE ? kWave : 1], s_off[ROUTE ? kWave : 1];
-  __shared__ int32_t s_ptok[ROUTE ? kMidMaxSlots : 1];
+  __shared__ int32_t s_cnt[RT != kRtExternal ? kWave : 1], s_off[RT != kRtExternal ? kWave : 1];
+  __shared__ int32_t s_ptok[ROUTE ? kMidMaxSlots : RT == kRtGroup ? kMidGroupMaxSlots : 1];
   static_assert(!ROUTE || kDecWaves * kMidMaxT * EMAX * 4 <= (int)sizeof(s_red), "gate partials fit");
 
   const int tid = threadIdx.x;
@@ -1601,6 +1632,17 @@ mid16_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x, int T
   if constexpr (ROUTE) {
     mid_route<EMAX>(x, T, H, E, k, ro, &s_red[0][0][0][0], s_sle, s_slw, s_cnt, s_off, s_ptok,
                     table_from_constants);
+  }
+  if constexpr (RT == kRtGroup) {  // the router's slots, grouped by wave 0
+    if (wave == 0) {
+      const int ns = T * k;
+      const int se[2] = {lane < ns ? ro.idx32[lane] : -1, lane + kWave < ns ? ro.idx32[lane + kWave] : -1};
+      int pos[2];
+      mid_group(se, ns, k, E, s_cnt, s_off, s_ptok, blockIdx.x == 0, ro, pos);
+    }
+    __syncthreads();
+  }
+  if constexpr (RT != kRtExternal) {
     g_cnt = s_cnt;
     g_off = s_off;
     g_ptok = s_ptok;
@@ -2029,6 +2071,11 @@ bool mid_layer_supported(int64_t T, int32_t k, int32_t E, int32_t H, int32_t F) 
          T * k <= kMidMaxSlots;
 }
 
+// With the grouping of a separate router launch's slots in the kernel: T * k <= 128.
+bool mid_group_supported(int64_t T, int32_t k, int32_t E, int32_t H, int32_t F) {
+  return mid_gateup_supported(T, k, E, H, F) && T * k <= kMidGroupMaxSlots;
+}
+
 // The mid-size down projection: F a multiple of 2048 (the parts), at most 16 parts (the
 // combine's plane limit), H a multiple of the 64-row output tile.
 bool mid_down_supported(int64_t T, int32_t k, int32_t E, int32_t H, int32_t F) {
@@ -2053,30 +2100,35 @@ int launch_mid_down(const void *tab_v, const void *h, int64_t T, int32_t k, int3
 int launch_mid_gateup(const void *tab_v, const void *x, int64_t T, int32_t k, int32_t H, int32_t F,
                       int32_t E, const void *route_v, void *h_ws, hipStream_t s,
                       const void *route_out) {
-  MOE_REQUIRE(route_out == nullptr ? mid_gateup_supported(T, k, E, H, F)
-                                   : mid_layer_supported(T, k, E, H, F),
+  const MidRouteOut ro = route_out ? *static_cast<const MidRouteOut *>(route_out) : MidRouteOut{};
+  const int mode = route_out == nullptr ? kRtExternal : ro.gate ? kRtRoute : kRtGroup;
+  MOE_REQUIRE(mode == kRtExternal ? mid_gateup_supported(T, k, E, H, F)
+                  : mode == kRtRoute ? mid_layer_supported(T, k, E, H, F)
+                                     : mid_group_supported(T, k, E, H, F),
               "shape not supported by the mid-size gate/up");
   MOE_REQUIRE(((uintptr_t)x % 16) == 0, "x must be 16-byte aligned");
   const ExpertTable &tab = *static_cast<const ExpertTable *>(tab_v);
   const Route rt = route_v ? *static_cast<const Route *>(route_v) : Route{};
-  const MidRouteOut ro = route_out ? *static_cast<const MidRouteOut *>(route_out) : MidRouteOut{};
-  if (route_out) {
+  if (mode == kRtRoute) {
     MOE_REQUIRE(((uintptr_t)ro.gate % 16) == 0, "gate must be 16-byte aligned");
-    MOE_REQUIRE(ro.w && ro.idx64 && ro.idx32 && ro.counts && ro.offsets && ro.perm_tok &&
-                    ro.slot_pos && ro.active,
-                "null routing output");
+    MOE_REQUIRE(ro.w && ro.idx64, "null routing output");
   }
+  if (mode != kRtExternal)
+    MOE_REQUIRE(ro.idx32 && ro.counts && ro.offsets && ro.perm_tok && ro.slot_pos && ro.active,
+                "null routing output");
   const dim3 grid((unsigned)device_cu_count()), blk(kDecThreads);
   auto go = [&](auto kern) {
     hipLaunchKernelGGL(kern, grid, blk, 0, s, tab, (const uint16_t *)x, (int)T, H, F, E, k, rt, ro,
                        (uint16_t *)h_ws);
   };
-  if (route_out == nullptr)
-    go(H == 4096 ? mid16_gateup_kernel<4, 8, false> : mid16_gateup_kernel<2, 8, false>);
+  if (mode == kRtExternal)
+    go(H == 4096 ? mid16_gateup_kernel<4, 8, kRtExternal> : mid16_gateup_kernel<2, 8, kRtExternal>);
+  else if (mode == kRtGroup)
+    go(H == 4096 ? mid16_gateup_kernel<4, 8, kRtGroup> : mid16_gateup_kernel<2, 8, kRtGroup>);
   else if (E <= 8)
-    go(H == 4096 ? mid16_gateup_kernel<4, 8, true> : mid16_gateup_kernel<2, 8, true>);
+    go(H == 4096 ? mid16_gateup_kernel<4, 8, kRtRoute> : mid16_gateup_kernel<2, 8, kRtRoute>);
   else
-    go(H == 4096 ? mid16_gateup_kernel<4, 16, true> : mid16_gateup_kernel<2, 16, true>);
+    go(H == 4096 ? mid16_gateup_kernel<4, 16, kRtRoute> : mid16_gateup_kernel<2, 16, kRtRoute>);
   MOE_LAUNCH_CHECK();
   return MOE_STATUS_OK;
 }

@@ -320,9 +320,10 @@ down_kernel(const ExpertTable tab, int H, int F, Route rt, const uint16_t *__res
 }
 
 // ----------------------------------------------------------------------------- combine
-// Workgroup (t, c) combines columns [1024c, 1024c + 1024) of token t; each thread owns
-// 4 consecutive columns.
-constexpr int kCombineThreads = 256;
+// Workgroup (t, c) combines columns [256c, 256c + 256) of token t; each thread owns 4
+// consecutive columns.  One wave per workgroup: a 40-token layer then has 640 workgroups,
+// enough loads in flight for the K-split planes' few megabytes.
+constexpr int kCombineThreads = 64;
 constexpr int kCombineCols = kCombineThreads * 4;
 
 __global__ void __launch_bounds__(kCombineThreads)
@@ -356,6 +357,7 @@ combine_kernel(const float *__restrict__ ypart, int nsplit, int64_t rows_total,
     if (pos < 0 || pos >= rows_total) continue;
     const float w = wts[t * k + j];
     float4 y = *reinterpret_cast<const float4 *>(ypart + (size_t)pos * H + c);
+#pragma unroll 4
     for (int s = 1; s < nsplit; ++s) {
       const float4 v = *reinterpret_cast<const float4 *>(ypart + s * split_stride + (size_t)pos * H + c);
       y.x += v.x;
@@ -480,10 +482,11 @@ int choose_nsplit(int64_t T, int32_t k, int32_t E, int32_t H, int32_t F) {
 
 bool mid_layer_supported(int64_t T, int32_t k, int32_t E, int32_t H, int32_t F);
 
-// Gate/up of a mid-size layer with the routing and grouping in the same launch (the
-// decode-stream kernel of launch_mid_gateup, every workgroup routing the tokens itself);
-// route_out (a MidRouteOut) names the gate, the bias and the routing outputs, which
-// workgroup 0 writes for the down projection and the combine.
+// Gate/up of a mid-size layer with the routing and grouping in the same launch (every
+// workgroup of launch_mid_gateup routing the tokens itself) or, with a null gate, only the
+// grouping of a separate router launch's slots (idx32); route_out (a MidRouteOut) names the
+// gate, the bias and the routing outputs, which workgroup 0 writes for the down projection
+// and the combine.
 int launch_mid_layer_gateup(const moe_nf4_expert_t *experts, int32_t E, const void *x, int64_t T,
                             int32_t k, int32_t H, int32_t F, void *h_ws, const void *route_out,
                             hipStream_t stream) {

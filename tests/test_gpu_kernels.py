@@ -441,8 +441,14 @@ def _check_layer(want, i_want, got, i_got, lg, bias=None):
 
 
 # F a multiple of 2048 also takes the mid-size down projection (virtual experts over parts
-# of 2048 values of F, one fp32 plane per part; 1 and 2 parts here).
+# of 2048 values of F, one fp32 plane per part; 1 and 2 parts here).  Above 16 tokens the
+# gate/up launch groups the slots of a separate router launch (up to 128 slots: T = 64,
+# k = 2), and experts with more than 16 rows split into several virtual experts.
 @pytest.mark.parametrize("H,F,E,T,seed,skew", [
+    (2048, 1024, 8, 24, 95, False),
+    (2048, 2048, 16, 40, 96, True),
+    (2048, 1024, 8, 64, 97, True),
+    (4096, 2048, 8, 33, 98, True),
     (2048, 1024, 8, 5, 81, False),
     (2048, 1536, 8, 12, 82, True),
     (2048, 1024, 8, 16, 83, False),
