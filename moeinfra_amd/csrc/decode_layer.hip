@@ -1462,17 +1462,16 @@ __device__ __forceinline__ void mid_group(const int (&se)[2], int ns, int k, int
   }
 }
 
-// Routing of the T <= kMidMaxT tokens of a mid-size launch, recomputed in every workgroup
-// (the gate is small and stays in L2): the gate products, per-token routing (route_rows),
-// then the grouping of the T*k slots by expert into s_cnt / s_off / s_ptok (wave 0);
-// workgroup 0 also writes the router's outputs and the grouping (MidRouteOut).  s_scratch
-// holds the waves' gate partials (kDecWaves x kMidMaxT x EMAX floats) until the final
-// barrier; `table` builds the lookup table while the gate loads are in flight.
+// Routing of T <= kMidMaxT tokens by one workgroup (the gate is small and stays in L2): the
+// gate products into s_scratch (the waves' partials, kDecWaves x kMidMaxT x EMAX floats),
+// then per-token routing (route_rows: slot experts and weights into s_sle / s_slw, logits
+// [T][E] written when `logits` is not null).  `table` builds the lookup table while the gate
+// loads are in flight.  Ends with a workgroup barrier.
 template <int EMAX, typename TableFn>
-__device__ __forceinline__ void mid_route(const uint16_t *__restrict__ x, int T, int H, int E,
-                                          int k, const MidRouteOut &ro, float *s_scratch,
-                                          int32_t *s_sle, float *s_slw, int32_t *s_cnt,
-                                          int32_t *s_off, int32_t *s_ptok, TableFn &&table) {
+__device__ __forceinline__ void mid_gate_route(const uint16_t *__restrict__ x, int T, int H, int E,
+                                               int k, const uint16_t *gate, const float *bias,
+                                               uint16_t *logits, float *s_scratch, int32_t *s_sle,
+                                               float *s_slw, TableFn &&table) {
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1493,7 +1492,7 @@ __device__ __forceinline__ void mid_route(const uint16_t *__restrict__ x, int T,
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     const int e = 4 * g + lj;
-    grow[g] = (gx_t)ro.gate + (size_t)(e < E ? e : E - 1) * H + (size_t)wave * 128 + 8 * lb;
+    grow[g] = (gx_t)gate + (size_t)(e < E ? e : E - 1) * H + (size_t)wave * 128 + 8 * lb;
   }
   f32x4 gacc[Q][G];
 #pragma unroll
@@ -1545,9 +1544,22 @@ __device__ __forceinline__ void mid_route(const uint16_t *__restrict__ x, int T,
   __syncthreads();
   // ---- per-token routing: wave w routes tokens 4w .. 4w+3 (workgroup 0 writes logits).
   if (4 * wave < T)
-    route_rows<EMAX, kDecWaves, kMidMaxT>(s_sle, s_slw, s_part, 4 * wave, ro.bias, T, E, k,
-                                          blockIdx.x == 0 ? ro.logits : nullptr);
+    route_rows<EMAX, kDecWaves, kMidMaxT>(s_sle, s_slw, s_part, 4 * wave, bias, T, E, k, logits);
   __syncthreads();
+}
+
+// Routing of the T <= kMidMaxT tokens of a mid-size launch in every workgroup
+// (mid_gate_route), then the grouping of the T*k slots by expert into s_cnt / s_off / s_ptok
+// (wave 0); workgroup 0 also writes the router's outputs and the grouping (MidRouteOut).
+template <int EMAX, typename TableFn>
+__device__ __forceinline__ void mid_route(const uint16_t *__restrict__ x, int T, int H, int E,
+                                          int k, const MidRouteOut &ro, float *s_scratch,
+                                          int32_t *s_sle, float *s_slw, int32_t *s_cnt,
+                                          int32_t *s_off, int32_t *s_ptok, TableFn &&table) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  mid_gate_route<EMAX>(x, T, H, E, k, ro.gate, ro.bias, blockIdx.x == 0 ? ro.logits : nullptr,
+                       s_scratch, s_sle, s_slw, table);
   // ---- grouping of the T k slots by expert (ascending expert, then slot), by wave 0;
   // workgroup 0 also writes the router's outputs.
   if (wave == 0) {
