@@ -1579,9 +1579,9 @@ __device__ __forceinline__ void mid_route(const uint16_t *__restrict__ x, int T,
 
 // Gate/up of mid-size batches (5 to 64 tokens) on the 16x16x32 MFMA.  An active expert with
 // cnt routed rows is ceil(cnt / 16) "virtual experts" of up to 16 consecutive rows; the
-// workgroups are dealt to the virtual experts in equal shares (grid / V each, V <= grid),
-// and each takes an equal share of its virtual expert's tiles.  A workgroup takes its virtual expert's 16-row weight tiles one at a
-// time, and wave w covers values [w H/8, (w+1) H/8) of every tile's K range, so each wave
+// workgroups are dealt to them by m16_share (the virtual experts of one expert side by side
+// on one XCD, over the same tiles).  A workgroup takes its virtual expert's 16-row weight
+// tiles one at a time, and wave w covers values [w H/8, (w+1) H/8) of every tile's K range, so each wave
 // keeps its K slice of the expert's token rows in registers for the whole launch and no
 // activation passes through LDS.  The eight partial sums of a tile meet in LDS (one
 // LDS-only barrier per tile, two buffers), and 256 threads sum them in wave order and write
@@ -1612,6 +1612,74 @@ __device__ __forceinline__ bf16x8 m16_lookup(const uint32_t *tbl, uint32_t w, ui
   return as_bf16x8(l[0], l[1], l[2], l[3]);
 }
 
+// The workgroup's share of a mid-size launch.  An active expert with cnt routed rows is
+// nv = ceil(cnt / 16) virtual experts; a unit is (virtual expert, part) with `parts` parts
+// of `tiles` tiles each.  The virtual experts of one expert (siblings) read the same weight
+// tiles, so they are dealt together: expert e receives a budget of workgroups proportional to
+// its units, cut into shares of nv workgroups, one per sibling, that take the same tile range
+// of the same part.  Sibling workgroups are adjacent in an XCD-major numbering of the grid
+// (workgroup b runs on XCD b mod 8), so they run side by side on one XCD and the siblings
+// after the first find the tiles in that XCD's L2 rather than in HBM.  Workgroups past the
+// last share get no tiles (t_lo == t_hi).  Requires V * parts <= gridDim.x (V = sum of nv).
+struct M16Share {
+  int e, vj, part, t_lo, t_hi;
+};
+__device__ __forceinline__ M16Share m16_share(int nv, int parts, int tiles) {
+  const int lane = threadIdx.x & (kWave - 1);
+  int incl = nv;
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const int t = __shfl_up(incl, o);
+    if (lane >= o) incl += t;
+  }
+  const int V = __builtin_amdgcn_readlane(incl, kWave - 1);
+  const int G = gridDim.x, b = blockIdx.x;
+  const int L = (G % 8 == 0) ? (b % 8) * (G / 8) + b / 8 : b;
+  // 32-bit arithmetic throughout (G, V and parts are small; 64-bit division is a long
+  // software sequence on the GPU).
+  const uint32_t U = (uint32_t)V * (uint32_t)parts;
+  // Shares of the lane's expert (>= parts when U <= G) and the workgroups they take.
+  const int budget = nv > 0 ? (int)((uint32_t)G * (uint32_t)nv * (uint32_t)parts / U) : 0;
+  const int shares = nv > 0 ? (int)((uint32_t)budget / (uint32_t)nv) : 0;
+  const int used = nv * shares;
+  int end = used;
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const int t = __shfl_up(end, o);
+    if (lane >= o) end += t;
+  }
+  const uint64_t past = __ballot(end > L);
+  M16Share r;
+  if (past == 0) {  // an idle workgroup: no tiles (the first active expert keeps loads valid)
+    r.e = __builtin_ctzll(__ballot(nv > 0));
+    r.vj = r.part = r.t_lo = r.t_hi = 0;
+    return r;
+  }
+  const int e = __builtin_ctzll(past);
+  const int m = __builtin_amdgcn_readlane(nv, e);
+  const int st = __builtin_amdgcn_readlane(shares, e);
+  const int o = L - (__builtin_amdgcn_readlane(end, e) - __builtin_amdgcn_readlane(used, e));
+  const int q = (int)((uint32_t)o / (uint32_t)m);  // the expert's share index; sibling o % m
+  const int Q = (int)((uint32_t)st / (uint32_t)parts), R = st - Q * parts;
+  int p, s, sp;  // parts < R take Q + 1 shares, the rest Q
+  if (q < R * (Q + 1)) {
+    p = (int)((uint32_t)q / (uint32_t)(Q + 1));
+    s = q - p * (Q + 1);
+    sp = Q + 1;
+  } else {
+    const int q2 = q - R * (Q + 1);
+    p = R + (int)((uint32_t)q2 / (uint32_t)Q);
+    s = q2 - (p - R) * Q;
+    sp = Q;
+  }
+  r.e = e;
+  r.vj = o - q * m;
+  r.part = p;
+  r.t_lo = (int)((uint32_t)s * (uint32_t)tiles / (uint32_t)sp);
+  r.t_hi = (int)((uint32_t)(s + 1) * (uint32_t)tiles / (uint32_t)sp);
+  return r;
+}
+
 template <int S, int EMAX, int RT>
 __global__ void __launch_bounds__(kDecThreads, 1)
 mid16_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x, int T, int H, int F,
@@ -1632,6 +1700,8 @@ mid16_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x, int T
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // Lane e: expert e is resident (its table entry, read now, under the routing).
+  const bool resident = lane < E && tab.e[lane < E ? lane : 0].w1_packed != nullptr;
 
   const int32_t *g_cnt = rt.counts, *g_off = rt.offsets, *g_ptok = rt.perm_tok;
   auto table_from_constants = [&]() {
@@ -1661,28 +1731,15 @@ mid16_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x, int T
   }
 
   // Virtual experts of every active expert (lane e holds expert e), counted in every wave.
-  const int cnt = (lane < E && tab.e[lane < E ? lane : 0].w1_packed != nullptr) ? g_cnt[lane] : 0;
+  const int cnt = resident ? g_cnt[lane] : 0;
   const int off = lane < E ? g_off[lane] : 0;
   const int nv = (cnt + kM16Rows - 1) / kM16Rows;
-  int incl = nv;
-#pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) {
-    const int t = __shfl_up(incl, o);
-    if (lane >= o) incl += t;
-  }
-  const int V = __builtin_amdgcn_readlane(incl, kWave - 1);
-  if (V == 0) return;  // uniform over the grid
-  const int G = gridDim.x, b = blockIdx.x;
-  const int v = (int)((int64_t)b * V / G);
-  const int b0 = (int)(((int64_t)v * G + V - 1) / V);
-  const int b1 = (int)(((int64_t)(v + 1) * G + V - 1) / V);
-  const int e = __builtin_ctzll(__ballot(incl > v));
-  const int vj = v - (__builtin_amdgcn_readlane(incl, e) - __builtin_amdgcn_readlane(nv, e));
+  if (__ballot(nv > 0) == 0) return;  // uniform over the grid
+  const M16Share sh = m16_share(nv, 1, F / kM16Rows);
+  const int e = sh.e, vj = sh.vj;
   const int r0 = __builtin_amdgcn_readlane(off, e) + kM16Rows * vj;  // first h row
   const int n = min(kM16Rows, __builtin_amdgcn_readlane(cnt, e) - kM16Rows * vj);
-  const int tiles = F / kM16Rows;
-  const int t_lo = (int)((int64_t)(b - b0) * tiles / (b1 - b0));
-  const int t_hi = (int)((int64_t)(b - b0 + 1) * tiles / (b1 - b0));
+  const int t_lo = sh.t_lo, t_hi = sh.t_hi;
 
   const moe_nf4_expert_t &ex = tab.e[e];
   const float *c1 = (const float *)uniform_ptr(ex.w1_code);
@@ -1842,8 +1899,8 @@ mid16_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x, int T
 // Down projection of mid-size batches on the 16x16x32 MFMA: virtual experts of up to 16 h
 // rows, F split into parts of 2048 values (one fp32 ypart plane per part, which the combine
 // adds in part order, model/moe_layer.py:186-191 after the expert's w2).  The workgroups are
-// dealt to the (virtual expert, part) pairs in equal shares, each taking an equal share of
-// the pair's 64-row output tiles one at a time; wave w covers values [256 w, 256 w + 256)
+// dealt to the (virtual expert, part) pairs by m16_share, each taking its share of the
+// pair's 64-row output tiles one at a time; wave w covers values [256 w, 256 w + 256)
 // of the part, so its slice of the expert's h rows stays in registers.  The tile is four
 // 16-row MFMA column blocks, loaded and scaled as in mid16_gateup_kernel (two 64-byte loads
 // per row of a block: four NF4 blocks); the eight waves' partial sums meet in LDS.
@@ -1865,35 +1922,25 @@ mid16_down_kernel(const ExpertTable tab, const uint16_t *__restrict__ h, int H, 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int cnt = (lane < E && tab.e[lane < E ? lane : 0].w2_packed != nullptr) ? rt.counts[lane] : 0;
+  // The counts, offsets and residency loads go out together (one round trip, under the
+  // table build).
+  const int cnt_raw = lane < E ? rt.counts[lane] : 0;
   const int off = lane < E ? rt.offsets[lane] : 0;
+  const bool resident = lane < E && tab.e[lane < E ? lane : 0].w2_packed != nullptr;
   {
     float cst[16];
 #pragma unroll
     for (int q = 0; q < 16; ++q) cst[q] = kNf4Code[q];
     build_table_regs<kDecThreads>(s_tbl, cst, cst);
   }
+  const int cnt = resident ? cnt_raw : 0;
   const int nv = (cnt + kM16Rows - 1) / kM16Rows;
-  int incl = nv;
-#pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) {
-    const int t = __shfl_up(incl, o);
-    if (lane >= o) incl += t;
-  }
-  const int V = __builtin_amdgcn_readlane(incl, kWave - 1);
-  if (V == 0) return;  // uniform over the grid
-  const int VP = V * parts, G = gridDim.x, b = blockIdx.x;
-  const int pr = (int)((int64_t)b * VP / G);  // pair: virtual expert pr / parts, part pr % parts
-  const int b0 = (int)(((int64_t)pr * G + VP - 1) / VP);
-  const int b1 = (int)(((int64_t)(pr + 1) * G + VP - 1) / VP);
-  const int v = pr / parts, kp = pr - v * parts;
-  const int e = __builtin_ctzll(__ballot(incl > v));
-  const int vj = v - (__builtin_amdgcn_readlane(incl, e) - __builtin_amdgcn_readlane(nv, e));
+  if (__ballot(nv > 0) == 0) return;  // uniform over the grid
+  const M16Share sh = m16_share(nv, parts, H / kM16DownTile);
+  const int e = sh.e, vj = sh.vj, kp = sh.part;
   const int r0 = __builtin_amdgcn_readlane(off, e) + kM16Rows * vj;  // first h row
   const int n = min(kM16Rows, __builtin_amdgcn_readlane(cnt, e) - kM16Rows * vj);
-  const int tiles = H / kM16DownTile;
-  const int t_lo = (int)((int64_t)(b - b0) * tiles / (b1 - b0));
-  const int t_hi = (int)((int64_t)(b - b0 + 1) * tiles / (b1 - b0));
+  const int t_lo = sh.t_lo, t_hi = sh.t_hi;
 
   const moe_nf4_expert_t &ex = tab.e[e];
   const float *c2 = (const float *)uniform_ptr(ex.w2_code);
@@ -2090,9 +2137,12 @@ bool mid_group_supported(int64_t T, int32_t k, int32_t E, int32_t H, int32_t F) 
 
 // The mid-size down projection: F a multiple of 2048 (the parts), at most 16 parts (the
 // combine's plane limit), H a multiple of the 64-row output tile.
+// Every (virtual expert, part) pair needs a workgroup of its own: at most E + T k / 16
+// virtual experts.
 bool mid_down_supported(int64_t T, int32_t k, int32_t E, int32_t H, int32_t F) {
   return mid_gateup_supported(T, k, E, H, F) && F % kMidDownVals == 0 &&
-         F / kMidDownVals <= 16 && H % kM16DownTile == 0;
+         F / kMidDownVals <= 16 && H % kM16DownTile == 0 &&
+         ((int64_t)E + T * k / kM16Rows) * (F / kMidDownVals) <= device_cu_count();
 }
 int mid_down_parts(int32_t F) { return F / kMidDownVals; }
 
