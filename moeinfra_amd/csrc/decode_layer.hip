@@ -1467,80 +1467,45 @@ __device__ __forceinline__ void mid_group(const int (&se)[2], int ns, int k, int
 // then per-token routing (route_rows: slot experts and weights into s_sle / s_slw, logits
 // [T][E] written when `logits` is not null).  `table` builds the lookup table while the gate
 // loads are in flight.  Ends with a workgroup barrier.
-template <int EMAX, typename TableFn>
+//
+// Gate products on the 16x16x32 MFMA (H = 1024 S): wave w takes values [w H/8, (w+1) H/8)
+// of H, 4S MFMAs of 32 values.  Lane l = 16 kq + n supplies values 8kq .. 8kq+7 of each 32
+// of token n (A rows; tokens >= T repeat token T - 1) and of expert n (B columns; experts
+// >= E repeat expert E - 1), and ends with the wave's sum D[token 4 kq + r][expert n] in
+// register r, stored as it is.
+template <int EMAX, int S, typename TableFn>
 __device__ __forceinline__ void mid_gate_route(const uint16_t *__restrict__ x, int T, int H, int E,
                                                int k, const uint16_t *gate, const float *bias,
                                                uint16_t *logits, float *s_scratch, int32_t *s_sle,
                                                float *s_slw, TableFn &&table) {
+  static_assert(EMAX <= 16, "one MFMA column per expert");
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  // ---- gate products on the 4x4x4 MFMA: wave w takes the 128-value chunks w, w + 8, ...
-  // of H; lane (b = lane / 4, j = lane % 4) holds values 8b .. 8b+7 of a chunk of token
-  // 4q + j (A rows of token group q; tokens >= T repeat a valid row and are ignored) and of
-  // expert 4g + j (B columns).  A butterfly over the 16 blocks completes the wave's sums.
-  constexpr int G = EMAX / 4;
-  constexpr int Q = kMidMaxT / 4;
-  const int lj = lane & 3, lb = lane >> 2;
-  const int n_chunks = (H / 128 - wave + kDecWaves - 1) / kDecWaves;
-  gx_t xrow[Q], grow[G];
+  constexpr int NM = 4 * S;  // MFMAs of the wave's K slice
+  const int n = lane & 15, kq = lane >> 4;
+  const size_t k0 = (size_t)wave * (128 * S) + 8 * kq;
+  const gx_t xr = (gx_t)x + (size_t)(n < T ? n : T - 1) * H + k0;
+  const gx_t gr = (gx_t)gate + (size_t)(n < E ? n : E - 1) * H + k0;
+  // Every load goes out at once, then the table is built under them.
+  bf16x8 xa[NM], ga[NM];
 #pragma unroll
-  for (int q = 0; q < Q; ++q) {
-    const int t = 4 * q + lj;
-    xrow[q] = (gx_t)x + (size_t)(t < T ? t : T - 1) * H + (size_t)wave * 128 + 8 * lb;
-  }
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const int e = 4 * g + lj;
-    grow[g] = (gx_t)gate + (size_t)(e < E ? e : E - 1) * H + (size_t)wave * 128 + 8 * lb;
-  }
-  f32x4 gacc[Q][G];
-#pragma unroll
-  for (int q = 0; q < Q; ++q)
-#pragma unroll
-    for (int g = 0; g < G; ++g) gacc[q][g] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  // Every chunk's loads go out at once (H <= 4096: at most four chunks per wave; a chunk
-  // past the wave's last re-reads chunk 0, unused), then the table is built under them.
-  constexpr int CH = kMidMaxH / 128 / kDecWaves;
-  uint4 xv[CH][Q], gv[CH][G];
-#pragma unroll
-  for (int c = 0; c < CH; ++c) {
-    const size_t co = (size_t)(c < n_chunks ? c : 0) * (128 * kDecWaves);
-#pragma unroll
-    for (int q = 0; q < Q; ++q)
-      xv[c][q] = (4 * q < T) ? ld_u4(xrow[q] + co) : uint4{0u, 0u, 0u, 0u};
-#pragma unroll
-    for (int g = 0; g < G; ++g) gv[c][g] = ld_u4(grow[g] + co);
+  for (int i = 0; i < NM; ++i) {
+    xa[i] = as_bf16x8(ld_u4(xr + 32 * i));
+    ga[i] = as_bf16x8(ld_u4(gr + 32 * i));
   }
   __builtin_amdgcn_sched_barrier(0);
   table();
   __builtin_amdgcn_sched_barrier(0);
+  f32x4 d = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-  for (int c = 0; c < CH; ++c) {
-    if (c >= n_chunks) break;
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int q = 0; q < Q; ++q) {
-        const s16x4 av = h ? as_s16x4(xv[c][q].z, xv[c][q].w) : as_s16x4(xv[c][q].x, xv[c][q].y);
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-          const s16x4 bv = h ? as_s16x4(gv[c][g].z, gv[c][g].w) : as_s16x4(gv[c][g].x, gv[c][g].y);
-          gacc[q][g] = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(av, bv, gacc[q][g], 0, 0, 0);
-        }
-      }
-  }
+  for (int i = 0; i < NM; ++i) d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[i], ga[i], d, 0, 0, 0);
   float(*s_part)[kMidMaxT][EMAX] = reinterpret_cast<float(*)[kMidMaxT][EMAX]>(s_scratch);
+  if (n < E) {
 #pragma unroll
-  for (int q = 0; q < Q; ++q)
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        const float v = lanes_sum16(gacc[q][g][m]);
-        const int e = 4 * g + lj;
-        if (lb == 0 && e < E && 4 * q + m < T) s_part[wave][4 * q + m][e] = v;
-      }
+    for (int r = 0; r < 4; ++r)
+      if (4 * kq + r < T) s_part[wave][4 * kq + r][n] = d[r];
+  }
   __syncthreads();
   // ---- per-token routing: wave w routes tokens 4w .. 4w+3 (workgroup 0 writes logits).
   if (4 * wave < T)
@@ -1551,14 +1516,14 @@ __device__ __forceinline__ void mid_gate_route(const uint16_t *__restrict__ x, i
 // Routing of the T <= kMidMaxT tokens of a mid-size launch in every workgroup
 // (mid_gate_route), then the grouping of the T*k slots by expert into s_cnt / s_off / s_ptok
 // (wave 0); workgroup 0 also writes the router's outputs and the grouping (MidRouteOut).
-template <int EMAX, typename TableFn>
+template <int EMAX, int S, typename TableFn>
 __device__ __forceinline__ void mid_route(const uint16_t *__restrict__ x, int T, int H, int E,
                                           int k, const MidRouteOut &ro, float *s_scratch,
                                           int32_t *s_sle, float *s_slw, int32_t *s_cnt,
                                           int32_t *s_off, int32_t *s_ptok, TableFn &&table) {
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  mid_gate_route<EMAX>(x, T, H, E, k, ro.gate, ro.bias, blockIdx.x == 0 ? ro.logits : nullptr,
+  mid_gate_route<EMAX, S>(x, T, H, E, k, ro.gate, ro.bias, blockIdx.x == 0 ? ro.logits : nullptr,
                        s_scratch, s_sle, s_slw, table);
   // ---- grouping of the T k slots by expert (ascending expert, then slot), by wave 0;
   // workgroup 0 also writes the router's outputs.
@@ -1620,18 +1585,27 @@ __device__ __forceinline__ bf16x8 m16_lookup(const uint32_t *tbl, uint32_t w, ui
 // of the same part.  Sibling workgroups are adjacent in an XCD-major numbering of the grid
 // (workgroup b runs on XCD b mod 8), so they run side by side on one XCD and the siblings
 // after the first find the tiles in that XCD's L2 rather than in HBM.  Workgroups past the
-// last share get no tiles (t_lo == t_hi).  Requires V * parts <= gridDim.x (V = sum of nv).
+// last share get no tiles (t_lo == t_hi).  Requires V * parts <= gridDim.x (V = sum of nv)
+// and nv = 0 on lanes >= E.
 struct M16Share {
   int e, vj, part, t_lo, t_hi;
 };
-__device__ __forceinline__ M16Share m16_share(int nv, int parts, int tiles) {
+// Inclusive prefix sum over lanes 0 .. n-1 (n <= 64, wave-uniform; lanes >= n hold 0): a
+// readlane per lane, which for the few experts here is shorter than a shuffle scan's chain
+// of LDS permutes.
+__device__ __forceinline__ int lanes_incl_scan(int v, int n) {
   const int lane = threadIdx.x & (kWave - 1);
-  int incl = nv;
-#pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) {
-    const int t = __shfl_up(incl, o);
-    if (lane >= o) incl += t;
+  int acc = 0;
+  for (int j = 0; j < n; ++j) {
+    const int vj = __builtin_amdgcn_readlane(v, j);
+    if (j <= lane) acc += vj;
   }
+  return acc;
+}
+
+__device__ __forceinline__ M16Share m16_share(int nv, int parts, int tiles, int E) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int incl = lanes_incl_scan(nv, E);
   const int V = __builtin_amdgcn_readlane(incl, kWave - 1);
   const int G = gridDim.x, b = blockIdx.x;
   const int L = (G % 8 == 0) ? (b % 8) * (G / 8) + b / 8 : b;
@@ -1642,13 +1616,8 @@ __device__ __forceinline__ M16Share m16_share(int nv, int parts, int tiles) {
   const int budget = nv > 0 ? (int)((uint32_t)G * (uint32_t)nv * (uint32_t)parts / U) : 0;
   const int shares = nv > 0 ? (int)((uint32_t)budget / (uint32_t)nv) : 0;
   const int used = nv * shares;
-  int end = used;
-#pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) {
-    const int t = __shfl_up(end, o);
-    if (lane >= o) end += t;
-  }
-  const uint64_t past = __ballot(end > L);
+  const int end = lanes_incl_scan(used, E);
+  const uint64_t past = __ballot(lane < E && end > L);
   M16Share r;
   if (past == 0) {  // an idle workgroup: no tiles (the first active expert keeps loads valid)
     r.e = __builtin_ctzll(__ballot(nv > 0));
@@ -1712,7 +1681,7 @@ mid16_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x, int T
   };
   if constexpr (!ROUTE) table_from_constants();
   if constexpr (ROUTE) {
-    mid_route<EMAX>(x, T, H, E, k, ro, &s_red[0][0][0][0], s_sle, s_slw, s_cnt, s_off, s_ptok,
+    mid_route<EMAX, S>(x, T, H, E, k, ro, &s_red[0][0][0][0], s_sle, s_slw, s_cnt, s_off, s_ptok,
                     table_from_constants);
   }
   if constexpr (RT == kRtGroup) {  // the router's slots, grouped by wave 0
@@ -1735,7 +1704,7 @@ mid16_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x, int T
   const int off = lane < E ? g_off[lane] : 0;
   const int nv = (cnt + kM16Rows - 1) / kM16Rows;
   if (__ballot(nv > 0) == 0) return;  // uniform over the grid
-  const M16Share sh = m16_share(nv, 1, F / kM16Rows);
+  const M16Share sh = m16_share(nv, 1, F / kM16Rows, E);
   const int e = sh.e, vj = sh.vj;
   const int r0 = __builtin_amdgcn_readlane(off, e) + kM16Rows * vj;  // first h row
   const int n = min(kM16Rows, __builtin_amdgcn_readlane(cnt, e) - kM16Rows * vj);
@@ -1936,7 +1905,7 @@ mid16_down_kernel(const ExpertTable tab, const uint16_t *__restrict__ h, int H, 
   const int cnt = resident ? cnt_raw : 0;
   const int nv = (cnt + kM16Rows - 1) / kM16Rows;
   if (__ballot(nv > 0) == 0) return;  // uniform over the grid
-  const M16Share sh = m16_share(nv, parts, H / kM16DownTile);
+  const M16Share sh = m16_share(nv, parts, H / kM16DownTile, E);
   const int e = sh.e, vj = sh.vj, kp = sh.part;
   const int r0 = __builtin_amdgcn_readlane(off, e) + kM16Rows * vj;  // first h row
   const int n = min(kM16Rows, __builtin_amdgcn_readlane(cnt, e) - kM16Rows * vj);
