@@ -104,10 +104,19 @@ def gemm_form(t: int, k: int, e: int, h: int, f: int) -> bool:
     return not decode_form(t, k, e, h, f) and t * k >= 32 * min(t * k, e)
 
 
+def mid_form(t: int, k: int, e: int, h: int, f: int, cus: int = 256) -> bool:
+    """Whether the layer call runs the mid-size kernels (5-64 tokens, virtual experts of
+    16 rows on 16-row weight tiles; hidden size 2048 or 4096)."""
+    return (not decode_form(t, k, e, h, f) and 5 <= t <= 64 and h in (2048, 4096)
+            and f % 16 == 0 and e <= 32 and t * h * 2 >= 2048 and e + t * k // 16 + 1 <= cus)
+
+
 def midbatch_form(t: int, k: int, e: int, h: int, f: int) -> bool:
     """Whether the layer call runs the streamed mid-batch kernels (more than 4 and fewer
-    than 32 rows per routed expert, shapes with whole 512-wide tiles)."""
+    than 32 rows per routed expert, shapes with whole 512-wide tiles, outside the mid-size
+    kernels' range)."""
     return (not decode_form(t, k, e, h, f) and not gemm_form(t, k, e, h, f) and t > 4
+            and not mid_form(t, k, e, h, f)
             and h % 512 == 0 and f % 512 == 0 and (f // 64) % 8 == 0 and t * k <= 2048)
 
 
@@ -264,8 +273,12 @@ def _moe_pass(lib, layers, xs, bias, T, H, F, E, K, steps, warmup, events=True, 
     layer_gbps = ly_bytes / (layer_us * 1e-6) / 1e9
 
     streamed = midbatch_form(T, K, E, H, F)
+    mid = mid_form(T, K, E, H, F)
     if decode_form(T, K, E, H, F):
         gu_kernel = "decode_gateup_kernel (routing + NF4 w1/w3 GEMV + SwiGLU)"
+    elif mid:
+        gu_kernel = ("mid16_gateup_kernel (routing or grouping in the launch + NF4 w1/w3 "
+                     "16x16x32 MFMA + SwiGLU)")
     elif gemm_form(T, K, E, H, F):
         gu_kernel = "expert_gemm_kernel<gate/up> (LDS-staged NF4 GEMM + SwiGLU)"
     elif streamed:
@@ -273,13 +286,13 @@ def _moe_pass(lib, layers, xs, bias, T, H, F, E, K, steps, warmup, events=True, 
     else:
         gu_kernel = "skinny_kernel / gemv4_kernel (NF4 w1/w3 + SwiGLU)"
     roofline = None
-    if gu_us and (decode_form(T, K, E, H, F) or streamed):
+    if gu_us and (decode_form(T, K, E, H, F) or streamed or mid):
         # Weight streaming: the routed experts' w1/w3 NF4 bytes per launch on the HBM roofline.
         ach = gu_bytes / (gu_us * 1e-6) / 1e9
         roofline = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBPS,
                     "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBPS, 4),
-                    "traffic": _traffic("gateup_nf4_midbatch_t%d_%s" % (T, routing) if streamed
-                                        else "gateup_nf4_decode_t%d" % T), "kernel": gu_kernel,
+                    "traffic": _traffic("gateup_nf4_decode_t%d" % T) if decode_form(T, K, E, H, F)
+                    else None, "kernel": gu_kernel,
                     "bytes_per_launch": int(gu_bytes), "avg_launch_us": round(gu_us, 2)}
     elif gu_us:
         # Batches (prefill): the w1/w3 GEMMs, 2 x 2 * (T*k) * H * F flops per launch, on the
