@@ -1798,7 +1798,9 @@ mid16_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x, int T
   auto tile_step = [&](TileRegs &R, int t, int t_next, bool live) {
     // The slot's next load goes out only after its last use (the lookup addresses), so that
     // it can take the same registers: a load into other registers would need a copy at the
-    // loop's back edge, which waits for it.
+    // loop's back edge, which waits for it.  Slots 2j and 2j + 1 read the two halves of one
+    // 128-byte line and go out together, after slot 2j + 1's last use: the L2 then serves
+    // both from one fill (measured 2-4 % faster than one load per step).
     auto lookups = [&](int i, bf16x8 (&bo)[4]) {
       const int p = i / S, s = i % S;
       const u32x4 w = R.w[p][s];
@@ -1812,7 +1814,10 @@ mid16_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x, int T
         for (int j = 0; j < 4; ++j)
           addr[q][j] = __builtin_amdgcn_perm(src[q], lane_const[p], 0x0c0c0400u + (j << 8));
       __builtin_amdgcn_sched_barrier(0);
-      load_w(R, t_next, p, s);
+      if (s & 1) {
+        load_w(R, t_next, p, s - 1);
+        load_w(R, t_next, p, s);
+      }
 #pragma unroll
       for (int q = 0; q < 4; ++q)
         bo[q] = as_bf16x8(lds_lookup(s_tbl, addr[q][0]), lds_lookup(s_tbl, addr[q][1]),
@@ -1980,7 +1985,9 @@ mid16_down_kernel(const ExpertTable tab, const uint16_t *__restrict__ h, int H, 
   // Tile t from R (then tile t_next's loads into R); ypart rows written when `live`.  The
   // table lookups of step i + 1 go out before the MFMAs of step i.
   auto tile_step = [&](TileRegs &R, int t, int t_next, bool live) {
-    auto lookups = [&](int i, bf16x8 (&bo)[4]) {  // the next load after the last use
+    // The next loads after the last use, the two halves of a 128-byte line together
+    // (mid16_gateup_kernel).
+    auto lookups = [&](int i, bf16x8 (&bo)[4]) {
       const int cb = i >> 1, s = i & 1;
       const u32x4 w = R.w[cb][s];
       const auto lo = __builtin_amdgcn_permlane32_swap(w[0], w[2], false, false);
@@ -1993,7 +2000,10 @@ mid16_down_kernel(const ExpertTable tab, const uint16_t *__restrict__ h, int H, 
         for (int j = 0; j < 4; ++j)
           addr[q][j] = __builtin_amdgcn_perm(src[q], lane_const, 0x0c0c0400u + (j << 8));
       __builtin_amdgcn_sched_barrier(0);
-      load_w(R, t_next, cb, s);
+      if (s & 1) {
+        load_w(R, t_next, cb, s - 1);
+        load_w(R, t_next, cb, s);
+      }
 #pragma unroll
       for (int q = 0; q < 4; ++q)
         bo[q] = as_bf16x8(lds_lookup(s_tbl, addr[q][0]), lds_lookup(s_tbl, addr[q][1]),
