@@ -330,7 +330,8 @@ def test_layer_absent_expert(cuda_device, T):
 
 # ------------------------------------------------------------------------------ mid-size batches
 # Between the decode form (T <= 4) and the batched GEMM (>= 32 routed rows per expert on
-# average) the layer runs the mid-batch kernels: the streamed form (expert_midbatch.hip;
+# average), outside the mid-size kernels' shapes (H 2048 / 4096, up to 64 tokens; those are
+# below), the layer runs the mid-batch kernels: the streamed form (expert_midbatch.hip;
 # H and F multiples of 512, K splits of the down projection when few experts are active)
 # or, for other shapes, the K-split form (expert_skinny.hip; F = 768 here).  32-token
 # chunks per expert (a hot expert under skewed routing takes several), uniform and skewed
@@ -429,10 +430,11 @@ def test_layer_mid_batch_mixtral(cuda_device, T, skew):
 
 
 # ------------------------------------------------------------------------------ mid-size gate/up
-# 5 to 16 tokens at hidden size 2048 or 4096: gate/up streams like the decode form, one
-# virtual expert (<= 8 rows of one expert, staged in LDS, lookup table from the expert's own
-# codebooks) per workgroup; an expert with more than 8 rows is two virtual experts.  Hidden
-# 2048 here (four stages per row; the Mixtral shape's eight are in the full-shape tests).
+# 5 to 64 tokens at hidden size 2048 or 4096: 16-row weight tiles on the 16x16x32 MFMA, one
+# virtual expert (<= 16 rows of one expert, each wave's K slice of them in registers) per
+# workgroup; an expert with more rows is several virtual experts, which read its tiles side
+# by side.  Up to 16 tokens every workgroup routes the tokens itself.  Hidden 2048 here
+# (the Mixtral shape is in the full-shape tests).
 def _check_layer(want, i_want, got, i_got, lg, bias=None):
     tie = near_tie_rows(lg, bias=bias)
     np.testing.assert_array_equal(i_got[~tie], i_want[~tie])
@@ -517,3 +519,39 @@ def test_layer_mid_gateup_hot_and_absent(cuda_device, T):
                                        bias=bias.to(cuda_device))
     torch.cuda.synchronize()
     _check_layer(want, i_w, bits(out), idx.cpu().numpy(), lg_w, bias=bias.numpy())
+
+
+def test_layer_mid_many_experts_hot(cuda_device):
+    """32 experts at 64 tokens: one expert takes every token (+1e4 bias: 64 rows, four
+    virtual experts that read its tiles side by side), the other 31 share the second slots
+    (one virtual expert each); gate/up and down both on the mid-size kernels (F = 2048: one
+    part), so the workgroups are dealt to 35 virtual experts of very different experts."""
+    from moeinfra_amd import ops
+
+    H, F, E, T, hot = 2048, 2048, 32, 64, 3
+    gate, experts, x = build_layer(H, F, E, T, 131)
+    bias = torch.zeros(E, dtype=torch.float32)
+    bias[hot] = 1.0e4
+    want, (lg_w, w_w, i_w) = oracle_layer(gate, experts, x, bias=bias)
+    assert (i_w == hot).any(axis=1).all()
+    assert ops.choose_nsplit(T, 2, E, H, F) == 1  # the mid-size down projection's one part
+    for ex in experts:
+        ex.to(cuda_device)
+    table = ops.expert_table([ex.c_struct() for ex in experts])
+    out, _, w, idx = ops.layer_forward(table, E, gate.to(cuda_device), x.to(cuda_device), 2, F,
+                                       bias=bias.to(cuda_device))
+    torch.cuda.synchronize()
+    _check_layer(want, i_w, bits(out), idx.cpu().numpy(), lg_w, bias=bias.numpy())
+
+
+def test_mid_down_needs_a_workgroup_per_pair(cuda_device):
+    """The mid-size down projection gives every (virtual expert, part of 2048 values of F)
+    pair a workgroup of its own: at 64 tokens, top-2 and F = 14336 (7 parts), 8 experts
+    (at most 16 virtual experts, 112 pairs) take it, 32 experts (up to 40 virtual experts,
+    280 pairs) take another path."""
+    from moeinfra_amd import ops
+
+    cus = torch.cuda.get_device_properties(cuda_device).multi_processor_count
+    assert ops.choose_nsplit(64, 2, 8, 2048, 14336) == 7
+    if (32 + 64 * 2 // 16) * 7 > cus:
+        assert ops.choose_nsplit(64, 2, 32, 2048, 14336) != 7
