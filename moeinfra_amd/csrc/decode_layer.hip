@@ -1462,6 +1462,10 @@ __device__ __forceinline__ void mid_group(const int (&se)[2], int ns, int k, int
   }
 }
 
+// Offset (values) of lane group kq's 8-value pieces within a 64-value NF4 block in the
+// 16x16x32 MFMA operands of the mid-size kernels ({0, 32, 16, 48}, see mid16_gateup_kernel).
+__device__ __forceinline__ int m16_off(int kq) { return ((kq & 1) << 5) | ((kq >> 1) << 4); }
+
 // Routing of T <= kMidMaxT tokens by one workgroup (the gate is small and stays in L2): the
 // gate products into s_scratch (the waves' partials, kDecWaves x kMidMaxT x EMAX floats),
 // then per-token routing (route_rows: slot experts and weights into s_sle / s_slw, logits
@@ -1469,37 +1473,43 @@ __device__ __forceinline__ void mid_group(const int (&se)[2], int ns, int k, int
 // loads are in flight.  Ends with a workgroup barrier.
 //
 // Gate products on the 16x16x32 MFMA (H = 1024 S): wave w takes values [w H/8, (w+1) H/8)
-// of H, 4S MFMAs of 32 values.  Lane l = 16 kq + n supplies values 8kq .. 8kq+7 of each 32
-// of token n (A rows; tokens >= T repeat token T - 1) and of expert n (B columns; experts
-// >= E repeat expert E - 1), and ends with the wave's sum D[token 4 kq + r][expert n] in
-// register r, stored as it is.
+// of H, 4S MFMAs.  Lane l = 16 kq + n supplies token n's values (A rows; tokens >= T repeat
+// token T - 1) and expert n's (B columns; experts >= E repeat expert E - 1) in the layout of
+// the weight stream's activation operands (mid16_gateup_kernel: MFMA (s, j) takes values
+// m16_off(kq) + 8 (j & 1) .. +7 of block 2s + (j >> 1) of the wave's slice), and ends with the
+// wave's sum D[token 4 kq + r][expert n] in register r, stored as it is.  The token operands
+// stay in xt for the stream.
 template <int EMAX, int S, typename TableFn>
 __device__ __forceinline__ void mid_gate_route(const uint16_t *__restrict__ x, int T, int H, int E,
                                                int k, const uint16_t *gate, const float *bias,
                                                uint16_t *logits, float *s_scratch, int32_t *s_sle,
-                                               float *s_slw, TableFn &&table) {
+                                               float *s_slw, bf16x8 (&xt)[S][4], TableFn &&table) {
   static_assert(EMAX <= 16, "one MFMA column per expert");
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  constexpr int NM = 4 * S;  // MFMAs of the wave's K slice
   const int n = lane & 15, kq = lane >> 4;
-  const size_t k0 = (size_t)wave * (128 * S) + 8 * kq;
+  const size_t k0 = (size_t)wave * (128 * S) + m16_off(kq);
   const gx_t xr = (gx_t)x + (size_t)(n < T ? n : T - 1) * H + k0;
   const gx_t gr = (gx_t)gate + (size_t)(n < E ? n : E - 1) * H + k0;
   // Every load goes out at once, then the table is built under them.
-  bf16x8 xa[NM], ga[NM];
+  bf16x8 ga[S][4];
 #pragma unroll
-  for (int i = 0; i < NM; ++i) {
-    xa[i] = as_bf16x8(ld_u4(xr + 32 * i));
-    ga[i] = as_bf16x8(ld_u4(gr + 32 * i));
-  }
+  for (int sq = 0; sq < S; ++sq)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int o = 128 * sq + 64 * (j >> 1) + 8 * (j & 1);
+      xt[sq][j] = as_bf16x8(ld_u4(xr + o));
+      ga[sq][j] = as_bf16x8(ld_u4(gr + o));
+    }
   __builtin_amdgcn_sched_barrier(0);
   table();
   __builtin_amdgcn_sched_barrier(0);
   f32x4 d = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-  for (int i = 0; i < NM; ++i) d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[i], ga[i], d, 0, 0, 0);
+  for (int sq = 0; sq < S; ++sq)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xt[sq][j], ga[sq][j], d, 0, 0, 0);
   float(*s_part)[kMidMaxT][EMAX] = reinterpret_cast<float(*)[kMidMaxT][EMAX]>(s_scratch);
   if (n < E) {
 #pragma unroll
@@ -1520,11 +1530,12 @@ template <int EMAX, int S, typename TableFn>
 __device__ __forceinline__ void mid_route(const uint16_t *__restrict__ x, int T, int H, int E,
                                           int k, const MidRouteOut &ro, float *s_scratch,
                                           int32_t *s_sle, float *s_slw, int32_t *s_cnt,
-                                          int32_t *s_off, int32_t *s_ptok, TableFn &&table) {
+                                          int32_t *s_off, int32_t *s_ptok, bf16x8 (&xt)[S][4],
+                                          TableFn &&table) {
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   mid_gate_route<EMAX, S>(x, T, H, E, k, ro.gate, ro.bias, blockIdx.x == 0 ? ro.logits : nullptr,
-                       s_scratch, s_sle, s_slw, table);
+                       s_scratch, s_sle, s_slw, xt, table);
   // ---- grouping of the T k slots by expert (ascending expert, then slot), by wave 0;
   // workgroup 0 also writes the router's outputs.
   if (wave == 0) {
@@ -1565,8 +1576,6 @@ __device__ __forceinline__ void mid_route(const uint16_t *__restrict__ x, int T,
 // and the A operand of MFMA (s, j) holds the same values of the lane's token row.  The
 // absmax of a block (the lane's row) scales each pair of MFMA sums in fp32.
 constexpr int kM16Rows = 16;  // rows of a virtual expert = weight rows of a tile
-
-__device__ __forceinline__ int m16_off(int kq) { return ((kq & 1) << 5) | ((kq >> 1) << 4); }
 
 // Four packed bytes (values 2j, 2j+1 per byte) -> eight bf16 code values (B operand).
 __device__ __forceinline__ bf16x8 m16_lookup(const uint32_t *tbl, uint32_t w, uint32_t lane_const) {
@@ -1680,9 +1689,12 @@ mid16_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x, int T
     build_table_regs<kDecThreads>(s_tbl, cst, cst);
   };
   if constexpr (!ROUTE) table_from_constants();
+  // ROUTE: every token's K slice of the wave (lane 16 kq + t: token t), loaded by the routing
+  // in the layout of the activation operands below.
+  bf16x8 xt[ROUTE ? S : 1][4];
   if constexpr (ROUTE) {
     mid_route<EMAX, S>(x, T, H, E, k, ro, &s_red[0][0][0][0], s_sle, s_slw, s_cnt, s_off, s_ptok,
-                    table_from_constants);
+                       xt, table_from_constants);
   }
   if constexpr (RT == kRtGroup) {  // the router's slots, grouped by wave 0
     if (wave == 0) {
@@ -1757,15 +1769,31 @@ mid16_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x, int T
   load_tile(A, min(t_lo, last));
 
   // The wave's K slice of the token rows, as A operands (s, j): lane (m = lane & 15, kq) holds
-  // values kM16Off[kq] + 8 (j & 1) .. +7 of block 2s + (j >> 1) of the slice of token row m
-  // (the first row again past n).
+  // values m16_off(kq) + 8 (j & 1) .. +7 of block 2s + (j >> 1) of the slice of token row m
+  // (the first row again past n).  With the routing in the launch, the routing's registers
+  // hold every token's slice in this layout (lane 16 kq + t: token t): each lane takes its
+  // row's from lane 16 kq + token in the same lane group, with no memory read.
   const int tok = g_ptok[r0 + (nl < n ? nl : 0)];
-  const gx_t xrow = (gx_t)x + (size_t)tok * H + (size_t)wave * kSlice + m16_off(kq);
   bf16x8 xa[S][4];
+  if constexpr (ROUTE) {
+    const int src = (16 * kq + tok) << 2;  // byte address of the source lane
 #pragma unroll
-  for (int s = 0; s < S; ++s)
+    for (int s = 0; s < S; ++s)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) xa[s][j] = as_bf16x8(ld_u4(xrow + 128 * s + 64 * (j >> 1) + 8 * (j & 1)));
+      for (int j = 0; j < 4; ++j) {
+        const u32x4 v = __builtin_bit_cast(u32x4, xt[s][j]);
+        u32x4 r;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) r[q] = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)v[q]);
+        xa[s][j] = as_bf16x8(r);
+      }
+  } else {
+    const gx_t xrow = (gx_t)x + (size_t)tok * H + (size_t)wave * kSlice + m16_off(kq);
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) xa[s][j] = as_bf16x8(ld_u4(xrow + 128 * s + 64 * (j >> 1) + 8 * (j & 1)));
+  }
   load_tile(B, min(t_lo + 1, last));
 
   // An expert whose w1 / w3 codebooks differ bitwise from the NF4 constants gets a table of
