@@ -39,8 +39,13 @@ struct MidRouteArgs {
   const void *gate;
   const void *bias;
   void *logits, *w, *idx64, *idx32, *counts, *offsets, *perm_tok, *slot_pos, *active;
+  const void *parts;
 };
-static_assert(sizeof(MidRouteArgs) == 11 * sizeof(void *), "MidRouteOut layout");
+static_assert(sizeof(MidRouteArgs) == 12 * sizeof(void *), "MidRouteOut layout");
+bool mid_parts_supported(int64_t T, int32_t k, int32_t E, int32_t H, int32_t F);
+int64_t mid_parts_bytes();
+int launch_mid_gate_parts(const void *x, const void *gate, int64_t T, int32_t H, int32_t E,
+                          void *parts, hipStream_t s);
 int64_t mid_route_out_bytes();
 int64_t decode_route_bytes();
 int launch_decode_layer(const moe_nf4_expert_t *experts, int32_t E, const void *gate,
@@ -70,7 +75,8 @@ int64_t align_up(int64_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
 // Byte offsets of the layer workspace regions.
 struct LayerWs {
-  int64_t idx32, counts, offsets, perm_tok, slot_pos, active, counter, droute, h, ypart, total;
+  int64_t idx32, counts, offsets, perm_tok, slot_pos, active, counter, droute, h, ypart,
+      ypart_bytes, total;
   int nsplit;
 };
 
@@ -90,6 +96,7 @@ LayerWs layer_ws(int64_t T, int32_t k, int32_t E, int32_t H, int32_t F, int nspl
   w.droute = o;   o = align_up(o + decode_route_bytes());
   w.h = o;        o = align_up(o + rows * (int64_t)F * 2);
   w.ypart = o;    o = align_up(o + (int64_t)w.nsplit * rows * H * 4);
+  w.ypart_bytes = o - w.ypart;
   w.total = o;
   return w;
 }
@@ -201,15 +208,29 @@ int layer_forward(const moe_nf4_expert_t *experts, int32_t E, const void *gate_b
     // Routing and grouping inside the gate/up launch: events 0 and 1 back to back.
     if (ev) MOE_HIP_CHECK(hipEventRecord(ev[1], s));
     const MidRouteArgs ro{gate_bf16, bias_f32, logits_bf16, weights_f32, idx_i64, idx32, counts,
-                          offsets, perm_tok, slot_pos, active};
+                          offsets, perm_tok, slot_pos, active, nullptr};
     rc = launch_mid_layer_gateup(experts, E, x_bf16, T, k, H, F, at<void>(workspace, w.h), &ro, s);
+  } else if (mid_group && mid_parts_supported(T, k, E, H, F)) {
+    // The gate products split over K by a small launch (no CU reads more than a slice of the
+    // tokens and the gate), the routing and grouping in the gate/up launch.  The partials sit
+    // at the start of the ypart region, which the down projection writes only after the
+    // gate/up launch has read them.
+    MOE_REQUIRE(w.ypart_bytes >= mid_parts_bytes(), "workspace too small for the gate partials");
+    void *parts = at<void>(workspace, w.ypart);
+    rc = launch_mid_gate_parts(x_bf16, gate_bf16, T, H, E, parts, s);
+    if (rc == MOE_STATUS_OK) {
+      if (ev) MOE_HIP_CHECK(hipEventRecord(ev[1], s));
+      const MidRouteArgs ro{nullptr, bias_f32, logits_bf16, weights_f32, idx_i64, idx32, counts,
+                            offsets, perm_tok, slot_pos, active, parts};
+      rc = launch_mid_layer_gateup(experts, E, x_bf16, T, k, H, F, at<void>(workspace, w.h), &ro, s);
+    }
   } else if (mid_group) {
     rc = moe_router_topk(x_bf16, gate_bf16, bias_f32, T, H, E, k, logits_bf16, weights_f32,
                          idx_i64, idx32, s);
     if (rc == MOE_STATUS_OK) {
       if (ev) MOE_HIP_CHECK(hipEventRecord(ev[1], s));
       const MidRouteArgs ro{nullptr, nullptr, nullptr, nullptr, nullptr, idx32, counts,
-                            offsets, perm_tok, slot_pos, active};
+                            offsets, perm_tok, slot_pos, active, nullptr};
       rc = launch_mid_layer_gateup(experts, E, x_bf16, T, k, H, F, at<void>(workspace, w.h), &ro, s);
     }
   } else if (small) {

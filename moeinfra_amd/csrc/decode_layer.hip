@@ -1381,8 +1381,9 @@ constexpr int kMidMaxH = 4096;
 // The routing a mid-size gate/up launch computes itself: the gate, the optional per-expert
 // logit bias, and where workgroup 0 writes the router's outputs (logits may be null) and the
 // grouping the down projection and the combine read (the layout of moe_permute: offsets
-// [E + 1], active = {n, ids ascending}, slot_pos of every slot).  With a null gate the
-// launch only groups the slots of a separate router launch, read from idx32.
+// [E + 1], active = {n, ids ascending}, slot_pos of every slot).  With a null gate and
+// `parts` set, the launch routes from the gate products of a mid_gate_parts_kernel launch
+// (parts); with both null it only groups the slots of a separate router launch (idx32).
 struct MidRouteOut {
   const uint16_t *gate;
   const float *bias;
@@ -1395,13 +1396,21 @@ struct MidRouteOut {
   int32_t *perm_tok;
   int32_t *slot_pos;
   int32_t *active;
+  const float *parts;
 };
 constexpr int kMidMaxT = 16;
 constexpr int kMidMaxSlots = kMidMaxT * 2;
 constexpr int kMidGroupMaxSlots = 2 * kWave;  // slots the in-launch grouping takes
 // How a mid-size gate/up launch gets its grouping: from the caller (Route), by routing the
-// tokens itself, or by grouping the slots of a separate router launch.
-constexpr int kRtExternal = 0, kRtRoute = 1, kRtGroup = 2;
+// tokens itself, by grouping the slots of a separate router launch, or by routing from the
+// gate products of a separate K-split launch.
+constexpr int kRtExternal = 0, kRtRoute = 1, kRtGroup = 2, kRtParts = 3;
+// The K-split gate products: [slice][token][expert] fp32, 8 slices of H/8 values (the waves'
+// K slices of mid_gate_route), up to 64 tokens and 16 experts.
+constexpr int kMidPartSlices = kDecWaves;
+constexpr int kMidPartTokens = 64;
+constexpr int kMidPartExperts = 16;
+constexpr int64_t kMidPartsBytes = (int64_t)kMidPartSlices * kMidPartTokens * kMidPartExperts * 4;
 
 // Grouping of ns <= 2 * kWave routed slots (slot s = t k + j routed to expert se) by expert,
 // ascending expert then slot (the order of moe_permute), by one wave: lane l holds slots l
@@ -1658,6 +1667,46 @@ __device__ __forceinline__ M16Share m16_share(int nv, int parts, int tiles, int 
   return r;
 }
 
+// Gate products of up to 64 tokens for a mid-size layer, split over K so that no CU reads
+// more than a slice: workgroup (token group tg of 16, slice ks) is one wave computing, for
+// tokens 16 tg .. +15 and every expert, the sums over values [ks H/8, (ks+1) H/8) of H on the
+// 16x16x32 MFMA in the operand layout of mid_gate_route (whose wave ks computes the same
+// sums), into parts[ks][token][expert].  The mid-size gate/up launch adds the 8 slices in
+// slice order and routes (kRtParts), as the routing inside the launch does for its waves.
+template <int S>
+__global__ void __launch_bounds__(kWave)
+mid_gate_parts_kernel(const uint16_t *__restrict__ x, const uint16_t *__restrict__ gate, int T,
+                      int H, int E, float *__restrict__ parts) {
+  const int lane = threadIdx.x;
+  const int ks = blockIdx.x % kMidPartSlices, tg = blockIdx.x / kMidPartSlices;
+  const int n = lane & 15, kq = lane >> 4;
+  const int t = 16 * tg + n;
+  const size_t k0 = (size_t)ks * (128 * S) + m16_off(kq);
+  const gx_t xr = (gx_t)x + (size_t)(t < T ? t : T - 1) * H + k0;
+  const gx_t gr = (gx_t)gate + (size_t)(n < E ? n : E - 1) * H + k0;
+  bf16x8 xa[S][4], ga[S][4];
+#pragma unroll
+  for (int sq = 0; sq < S; ++sq)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int o = 128 * sq + 64 * (j >> 1) + 8 * (j & 1);
+      xa[sq][j] = as_bf16x8(ld_u4(xr + o));
+      ga[sq][j] = as_bf16x8(ld_u4(gr + o));
+    }
+  f32x4 d = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int sq = 0; sq < S; ++sq)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[sq][j], ga[sq][j], d, 0, 0, 0);
+  if (n < E) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int tt = 16 * tg + 4 * kq + r;
+      if (tt < T) parts[((size_t)ks * kMidPartTokens + tt) * kMidPartExperts + n] = d[r];
+    }
+  }
+}
+
 template <int S, int EMAX, int RT>
 __global__ void __launch_bounds__(kDecThreads, 1)
 mid16_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x, int T, int H, int F,
@@ -1669,11 +1718,16 @@ mid16_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x, int T
   // first tile (ROUTE) the waves' gate partials.
   __shared__ __attribute__((aligned(16))) float s_red[2][kDecWaves][2][kWave * 4];
   constexpr bool ROUTE = RT == kRtRoute;
-  __shared__ int32_t s_sle[ROUTE ? kMidMaxSlots : 1];
-  __shared__ float s_slw[ROUTE ? kMidMaxSlots : 1];
+  constexpr bool PARTS = RT == kRtParts;
+  constexpr int kSlots = ROUTE ? kMidMaxSlots : PARTS ? kMidGroupMaxSlots : 1;
+  __shared__ int32_t s_sle[kSlots];
+  __shared__ float s_slw[kSlots];
   __shared__ int32_t s_cnt[RT != kRtExternal ? kWave : 1], s_off[RT != kRtExternal ? kWave : 1];
-  __shared__ int32_t s_ptok[ROUTE ? kMidMaxSlots : RT == kRtGroup ? kMidGroupMaxSlots : 1];
+  __shared__ int32_t s_ptok[ROUTE ? kMidMaxSlots : RT != kRtExternal ? kMidGroupMaxSlots : 1];
   static_assert(!ROUTE || kDecWaves * kMidMaxT * EMAX * 4 <= (int)sizeof(s_red), "gate partials fit");
+  static_assert(!PARTS || (kMidPartSlices * kMidPartTokens * EMAX * 4 <= (int)sizeof(s_red) &&
+                           EMAX <= kMidPartExperts && kMidPartSlices == kDecWaves),
+                "K-split gate products fit");
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
@@ -1688,6 +1742,22 @@ mid16_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x, int T
     for (int q = 0; q < 16; ++q) cst[q] = kNf4Code[q];
     build_table_regs<kDecThreads>(s_tbl, cst, cst);
   };
+  // PARTS: the 8 slices' gate products of every token ([slice][token][expert], experts < EMAX)
+  // are loaded first, so that they arrive while the table is built.
+  constexpr int kPartQ = EMAX / 4;  // 16-byte pieces of a token's experts
+  constexpr int kPartLoads = PARTS ? kMidPartSlices * kMidPartTokens * kPartQ / kDecThreads : 1;
+  static_assert(!PARTS || kMidPartSlices * kMidPartTokens * kPartQ % kDecThreads == 0, "whole rounds");
+  f32x4 pv[kPartLoads];
+  if constexpr (PARTS) {
+#pragma unroll
+    for (int r = 0; r < kPartLoads; ++r) {
+      const int i = tid + kDecThreads * r;
+      const int q = i % kPartQ, t = (i / kPartQ) % kMidPartTokens, ks = i / (kPartQ * kMidPartTokens);
+      pv[r] = t < T ? *reinterpret_cast<const f32x4 *>(
+                          ro.parts + ((size_t)ks * kMidPartTokens + t) * kMidPartExperts + 4 * q)
+                    : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+  }
   if constexpr (!ROUTE) table_from_constants();
   // ROUTE: every token's K slice of the wave (lane 16 kq + t: token t), loaded by the routing
   // in the layout of the activation operands below.
@@ -1695,6 +1765,47 @@ mid16_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x, int T
   if constexpr (ROUTE) {
     mid_route<EMAX, S>(x, T, H, E, k, ro, &s_red[0][0][0][0], s_sle, s_slw, s_cnt, s_off, s_ptok,
                        xt, table_from_constants);
+  }
+  if constexpr (PARTS) {
+    // The gate products into LDS ([slice][token][EMAX]; experts past E unused), then each
+    // wave routes tokens 4w .. 4w+3 and 32 + 4w .. (route_rows adds the slices in slice
+    // order), and wave 0 groups the slots; workgroup 0 publishes.
+    float(*s_part)[kMidPartTokens][EMAX] =
+        reinterpret_cast<float(*)[kMidPartTokens][EMAX]>(&s_red[0][0][0][0]);
+#pragma unroll
+    for (int r = 0; r < kPartLoads; ++r) {
+      const int i = tid + kDecThreads * r;
+      const int q = i % kPartQ, t = (i / kPartQ) % kMidPartTokens, ks = i / (kPartQ * kMidPartTokens);
+      if (t < T) *reinterpret_cast<f32x4 *>(&s_part[ks][t][4 * q]) = pv[r];
+    }
+    __syncthreads();
+    const bool wg0 = blockIdx.x == 0;
+#pragma unroll
+    for (int h = 0; h < kMidPartTokens / (4 * kDecWaves); ++h) {
+      const int t0 = 4 * kDecWaves * h + 4 * wave;
+      if (t0 < T)
+        route_rows<EMAX, kMidPartSlices, kMidPartTokens>(s_sle, s_slw, s_part, t0, ro.bias, T, E, k,
+                                                         wg0 ? ro.logits : nullptr);
+    }
+    __syncthreads();
+    if (wave == 0) {
+      const int ns = T * k;
+      const int se[2] = {lane < ns ? s_sle[lane] : -1, lane + kWave < ns ? s_sle[lane + kWave] : -1};
+      int pos[2];
+      mid_group(se, ns, k, E, s_cnt, s_off, s_ptok, wg0, ro, pos);
+      if (wg0) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int sl = lane + kWave * h;
+          if (sl < ns) {
+            ro.w[sl] = s_slw[sl];
+            ro.idx64[sl] = se[h];
+            ro.idx32[sl] = se[h];
+          }
+        }
+      }
+    }
+    __syncthreads();
   }
   if constexpr (RT == kRtGroup) {  // the router's slots, grouped by wave 0
     if (wave == 0) {
@@ -2142,6 +2253,32 @@ bool mid_group_supported(int64_t T, int32_t k, int32_t E, int32_t H, int32_t F) 
   return mid_gateup_supported(T, k, E, H, F) && T * k <= kMidGroupMaxSlots;
 }
 
+// With the routing from a K-split gate-product launch: up to 64 tokens, top-k <= 2 and at
+// most 16 experts (one MFMA column each).
+bool mid_parts_supported(int64_t T, int32_t k, int32_t E, int32_t H, int32_t F) {
+  return mid_group_supported(T, k, E, H, F) && T <= kMidPartTokens && k <= 2 &&
+         E <= kMidPartExperts;
+}
+int64_t mid_parts_bytes() { return kMidPartsBytes; }
+
+int launch_mid_gate_parts(const void *x, const void *gate, int64_t T, int32_t H, int32_t E,
+                          void *parts, hipStream_t s) {
+  MOE_REQUIRE(T >= 1 && T <= kMidPartTokens && E >= 1 && E <= kMidPartExperts &&
+                  (H == 2048 || H == 4096),
+              "shape not supported by the K-split gate products");
+  MOE_REQUIRE(((uintptr_t)x | (uintptr_t)gate | (uintptr_t)parts) % 16 == 0,
+              "x, gate and the partials must be 16-byte aligned");
+  const dim3 grid((unsigned)(((T + 15) / 16) * kMidPartSlices)), blk(kWave);
+  if (H == 4096)
+    hipLaunchKernelGGL(mid_gate_parts_kernel<4>, grid, blk, 0, s, (const uint16_t *)x,
+                       (const uint16_t *)gate, (int)T, H, E, (float *)parts);
+  else
+    hipLaunchKernelGGL(mid_gate_parts_kernel<2>, grid, blk, 0, s, (const uint16_t *)x,
+                       (const uint16_t *)gate, (int)T, H, E, (float *)parts);
+  MOE_LAUNCH_CHECK();
+  return MOE_STATUS_OK;
+}
+
 // The mid-size down projection: F a multiple of 2048 (the parts), at most 16 parts (the
 // combine's plane limit), H a multiple of the 64-row output tile.
 // Every (virtual expert, part) pair needs a workgroup of its own: at most E + T k / 16
@@ -2170,9 +2307,13 @@ int launch_mid_gateup(const void *tab_v, const void *x, int64_t T, int32_t k, in
                       int32_t E, const void *route_v, void *h_ws, hipStream_t s,
                       const void *route_out) {
   const MidRouteOut ro = route_out ? *static_cast<const MidRouteOut *>(route_out) : MidRouteOut{};
-  const int mode = route_out == nullptr ? kRtExternal : ro.gate ? kRtRoute : kRtGroup;
+  const int mode = route_out == nullptr ? kRtExternal
+                   : ro.gate            ? kRtRoute
+                   : ro.parts           ? kRtParts
+                                        : kRtGroup;
   MOE_REQUIRE(mode == kRtExternal ? mid_gateup_supported(T, k, E, H, F)
                   : mode == kRtRoute ? mid_layer_supported(T, k, E, H, F)
+                  : mode == kRtParts ? mid_parts_supported(T, k, E, H, F)
                                      : mid_group_supported(T, k, E, H, F),
               "shape not supported by the mid-size gate/up");
   MOE_REQUIRE(((uintptr_t)x % 16) == 0, "x must be 16-byte aligned");
@@ -2185,6 +2326,10 @@ int launch_mid_gateup(const void *tab_v, const void *x, int64_t T, int32_t k, in
   if (mode != kRtExternal)
     MOE_REQUIRE(ro.idx32 && ro.counts && ro.offsets && ro.perm_tok && ro.slot_pos && ro.active,
                 "null routing output");
+  if (mode == kRtParts) {
+    MOE_REQUIRE(ro.w && ro.idx64, "null routing output");
+    MOE_REQUIRE(((uintptr_t)ro.parts % 16) == 0, "the gate partials must be 16-byte aligned");
+  }
   const dim3 grid((unsigned)device_cu_count()), blk(kDecThreads);
   auto go = [&](auto kern) {
     hipLaunchKernelGGL(kern, grid, blk, 0, s, tab, (const uint16_t *)x, (int)T, H, F, E, k, rt, ro,
@@ -2194,6 +2339,10 @@ int launch_mid_gateup(const void *tab_v, const void *x, int64_t T, int32_t k, in
     go(H == 4096 ? mid16_gateup_kernel<4, 8, kRtExternal> : mid16_gateup_kernel<2, 8, kRtExternal>);
   else if (mode == kRtGroup)
     go(H == 4096 ? mid16_gateup_kernel<4, 8, kRtGroup> : mid16_gateup_kernel<2, 8, kRtGroup>);
+  else if (mode == kRtParts && E <= 8)
+    go(H == 4096 ? mid16_gateup_kernel<4, 8, kRtParts> : mid16_gateup_kernel<2, 8, kRtParts>);
+  else if (mode == kRtParts)
+    go(H == 4096 ? mid16_gateup_kernel<4, 16, kRtParts> : mid16_gateup_kernel<2, 16, kRtParts>);
   else if (E <= 8)
     go(H == 4096 ? mid16_gateup_kernel<4, 8, kRtRoute> : mid16_gateup_kernel<2, 8, kRtRoute>);
   else
