@@ -774,6 +774,7 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
   // Single-token path: per item of the workgroup, the per-lane sums of w1 and w3 (row
   // j = lane % 4 of the tile, block lane / 4).
   __shared__ float s_raw[kRawSlots][2][kWave];
+  __shared__ uint8_t s_mine[kDecWaves][kRawSlots];  // the raw slots each wave filled
   // NORM: the normalised token (gate products read it here) and the norm's wave sums.
   __shared__ __attribute__((aligned(16))) uint16_t s_xn[NORM ? kDecNormMaxH : 8];
   __shared__ float s_npart[kDecWaves];
@@ -1055,8 +1056,9 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
   if (!slow && bc && nsq == 8 && T == 1) {
     // Single token: the workgroup's items are shared through the work counter.  With at
     // most kRawSlots items per workgroup, an item's per-lane sums go to LDS as they are (no
-    // cross-lane reduction or SwiGLU in the stream) and the workgroup reduces them after
-    // the stream (blocks 0 to 15 in order) and writes h.
+    // cross-lane reduction or SwiGLU in the stream), and after its stream each wave reduces
+    // the items it streamed (blocks 0 to 15 in order) and writes h: no workgroup barrier
+    // holds the waves that finish first.
     auto grab = [&]() -> int {
       int t = 0;
       if (lane == 0) t = __hip_atomic_fetch_add(&s_ticket, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -1076,9 +1078,12 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
             grab, set_ptrs, finish1, hook, s_tbl, lane_const, row_blocks, s_aslot[wave], xb, (gq_t)gate);
       return;
     }
+    int nmine = 0;  // wave-uniform
     auto finish_raw = [&](f32x4 (&ac)[2], int i) {
       s_raw[i - wlo][0][lane] = ac[0][0];
       s_raw[i - wlo][1][lane] = ac[1][0];
+      if (lane == 0) s_mine[wave][nmine] = (uint8_t)(i - wlo);
+      ++nmine;
     };
     if (NORM)
       stream_aligned<2, 8, kGateUpDepth, true, kXRegs, kLookahead>(
@@ -1086,19 +1091,22 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
     else
       stream_aligned<2, 8, kGateUpDepth, true, kXRegs, kLookahead>(
           grab, set_ptrs, finish_raw, hook, s_tbl, lane_const, row_blocks, s_aslot[wave], xb, (gq_t)gate);
-    __syncthreads();
-    if (tid < 4 * nit) {
-      const int slot = tid >> 2;
-      const int j = tid & 3;
-      float g = 0.0f, up = 0.0f;
+    wave_lds_sync();  // the wave's own raw slots, written by its other lanes
+    for (int c = 0; c < nmine; c += kWave / 4) {  // lane 4 m + j: row j of the wave's item c + m
+      const int m = c + (lane >> 2);
+      if (m < nmine) {
+        const int slot = s_mine[wave][m];
+        const int j = lane & 3;
+        float g = 0.0f, up = 0.0f;
 #pragma unroll
-      for (int b = 0; b < 16; ++b) {
-        g += s_raw[slot][0][4 * b + j];
-        up += s_raw[slot][1][4 * b + j];
+        for (int b = 0; b < 16; ++b) {
+          g += s_raw[slot][0][4 * b + j];
+          up += s_raw[slot][1][4 * b + j];
+        }
+        int tile;
+        const int a = item_expert(wlo + slot, tile);
+        h_out[(size_t)s_rt.offsets[a] * F + tile * 4 + j] = swiglu_bf16(g, up);
       }
-      int tile;
-      const int a = item_expert(wlo + slot, tile);
-      h_out[(size_t)s_rt.offsets[a] * F + tile * 4 + j] = swiglu_bf16(g, up);
     }
     return;
   }
