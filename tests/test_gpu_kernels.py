@@ -148,6 +148,13 @@ def _layer_case(dev, H, F, E, T, seed, skew=False, codes=None):
                                         bias=None if bias is None else bias.to(dev),
                                         want_logits=True)
     torch.cuda.synchronize()
+    # The router's logits output against the oracle's: both round an fp32 sum of the same
+    # products to bf16, summed in different orders, so they may differ by the two sums'
+    # distance (2 x the reordering bound of logit_slack) and one bf16 step.
+    lg_g = orc.bf16_to_f32(bits(lg)).astype(np.float64)
+    lg_o = orc.bf16_to_f32(lg_w).astype(np.float64)
+    slack = logit_slack(bits(x), bits(gate))[:, None]
+    assert (np.abs(lg_g - lg_o) <= 2.0 ** -7 * np.maximum(np.abs(lg_g), np.abs(lg_o)) + 2.0 * slack).all()
     return want, i_w, bits(out), idx.cpu().numpy(), lg_w
 
 
