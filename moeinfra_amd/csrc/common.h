@@ -52,11 +52,66 @@ __device__ __forceinline__ uint4 ld_stream16(const void *p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// ---------------------------------------------------------------- kernel arguments
+// Kernel arguments arrive through scalar loads from the argument buffer, a memory round trip
+// each time the kernel waits for them.  When the first arithmetic needs only some arguments
+// (an index division, a loop bound), the compiler waits for those first and issues the
+// loads of the others after it, so a second round trip sits before the first global load.
+// MOE_ARGS_FIRST(scalars, pointers) is an empty asm that takes every pointer argument
+// as an SGPR input and every scalar argument as an SGPR in/out operand: all later code
+// depends on it, so every argument is loaded in one batch ahead of it.  Pointers are inputs
+// only, so the compiler still knows they point to global memory.  Each operand list is
+// wrapped in MOE_LIST(...).
+#define MOE_LIST(...) __VA_ARGS__
+#define MOE_ARGS_FIRST(outs, ins) asm volatile("" : outs : ins)
+
 // ---------------------------------------------------------------- wave reductions
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
   return v;
+}
+
+// DPP move of v with control CTRL (row_mask and bank_mask all set, no bound control).
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xf,
+                                                            0xf, false));
+}
+
+// Sums (MAX: maxima) of N values over aligned groups of n lanes (n a power of two <= 64,
+// uniform), every lane of a group getting its group's result.  Within a 16-lane DPP row the
+// steps are register moves: quad_perm [1,0,3,2] (lane ^ 1), quad_perm [2,3,0,1] (lane ^ 2),
+// then, with every quad holding one value, row_half_mirror (the other quad of the 8) and
+// row_mirror (the other 8 of the 16); beyond 16 lanes, shuffles through LDS.  The N
+// reductions advance step by step together, so their latencies overlap.
+template <bool MAX, int N>
+__device__ __forceinline__ void lane_groups_reduce(float (&v)[N], int n) {
+  auto op = [](float a, float b) { return MAX ? fmaxf(a, b) : a + b; };
+  if (n >= 2) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = op(v[i], dpp_mov<0xB1>(v[i]));
+  }
+  if (n >= 4) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = op(v[i], dpp_mov<0x4E>(v[i]));
+  }
+  if (n >= 8) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = op(v[i], dpp_mov<0x141>(v[i]));
+  }
+  if (n >= 16) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = op(v[i], dpp_mov<0x140>(v[i]));
+  }
+  if (n >= 32) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = op(v[i], __shfl_xor(v[i], 16, kWave));
+  }
+  if (n >= 64) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = op(v[i], __shfl_xor(v[i], 32, kWave));
+  }
 }
 
 }  // namespace moe

@@ -105,14 +105,60 @@ rope_kv_kernel(const uint16_t *__restrict__ qkv, int nq, int nkv, int hd,
 constexpr int kAttnThreads = 256;
 constexpr int kAttnMaxKeys = 8192;
 constexpr int kAttnMaxHeadDim = 256;
-constexpr int kAttnRowsInFlight = 4;  // cache rows per thread per pass
+constexpr int kAttnRowsInFlight = 8;  // cache rows per thread per pass
+
+// Scores of the pass starting at key j0 from its loaded K rows: s_p[j] = bf16(bf16(q.k_j) *
+// scaling) for the keys j < nkeys, and the running maximum.  The eight rows' lane partials
+// are formed first and summed over each row's lpr lanes together (DPP within a 16-lane row).
+__device__ __forceinline__ void attn_scores(const uint4 (&kv)[kAttnRowsInFlight], const float (&qf)[8],
+                                            int j0, int nkeys, int rpp, int rr, int lpr, int sub,
+                                            float scaling, float *s_p, float &mx) {
+  float dot[kAttnRowsInFlight];
+#pragma unroll
+  for (int u = 0; u < kAttnRowsInFlight; ++u) {
+    float kf[8];
+    unpack8(kv[u], kf);
+    float d = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) d = fmaf(qf[e], kf[e], d);
+    dot[u] = d;
+  }
+  lane_groups_reduce<false>(dot, lpr);
+#pragma unroll
+  for (int u = 0; u < kAttnRowsInFlight; ++u) {
+    const int j = j0 + u * rpp + rr;
+    const float sc = bf16r(bf16r(dot[u]) * scaling);
+    const bool ok = j < nkeys;
+    mx = ok ? fmaxf(mx, sc) : mx;
+    if (ok && sub == 0) s_p[j] = sc;
+  }
+}
+
+// acc += p_j v_j over the pass's rows j < nkeys, in row order.
+__device__ __forceinline__ void attn_pv(const uint4 (&vv)[kAttnRowsInFlight], int j0, int nkeys,
+                                        int rpp, int rr, const float *s_p, float (&acc)[8]) {
+#pragma unroll
+  for (int u = 0; u < kAttnRowsInFlight; ++u) {
+    const int j = j0 + u * rpp + rr;
+    if (j < nkeys) {
+      const float p = s_p[j];
+      float vf[8];
+      unpack8(vv[u], vf);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] = fmaf(p, vf[e], acc[e]);
+    }
+  }
+}
 
 // One workgroup per (query head, token): scores of keys 0 .. pos0 + t (causal), bf16 scores
 // scaled in bf16, fp32 softmax rounded to bf16, then the bf16 probabilities times V with
 // fp32 accumulation.  A cache row of hd bf16 is read by hd/8 consecutive lanes, 16 bytes
-// each, so the workgroup covers 256/(hd/8) rows per load instruction and keeps 4 such
-// loads in flight per thread; a score is the xor-shuffle sum over its row's lanes.  Rows
-// past the last key are clamped to it (in bounds) and their results discarded.
+// each, so the workgroup covers rpp = 256/(hd/8) rows per load instruction and a pass takes
+// 8 such loads per thread (128 rows at hd = 128); a score is the xor-shuffle sum over its
+// row's lanes.  The first pass's K and V rows are loaded together with q and the position,
+// before the key count is known (row indexes clamped to the cache, results of rows past the
+// last key discarded), so a context of up to one pass of keys costs one memory round trip;
+// later passes load rows clamped to the last key.
 __global__ void __launch_bounds__(kAttnThreads)
 attention_kernel(const uint16_t *__restrict__ q, const uint16_t *__restrict__ kc,
                  const uint16_t *__restrict__ vc, int nq, int nkv, int hd,
@@ -121,46 +167,44 @@ attention_kernel(const uint16_t *__restrict__ q, const uint16_t *__restrict__ kc
   __shared__ float s_p[kAttnMaxKeys];
   __shared__ float s_red[kAttnThreads / kWave];
   __shared__ __attribute__((aligned(16))) float s_acc[kAttnThreads * 8];
+  MOE_ARGS_FIRST(MOE_LIST("+s"(nq), "+s"(nkv), "+s"(hd), "+s"(max_seq), "+s"(scaling)),
+                 MOE_LIST("s"(q), "s"(kc), "s"(vc), "s"(pos0), "s"(out)));
   const int h = blockIdx.x, t = blockIdx.y;
   const int kvh = h / (nq / nkv);
-  // Keys 0 .. pos0 + t, bounded by the cache (a position past it is a caller error).
-  const int nkeys = min(*pos0 + t + 1, (int)max_seq);
   const int lpr = hd >> 3;               // lanes per row: a power of two <= 32
   const int rpp = kAttnThreads / lpr;    // rows per load instruction of the workgroup
+  const int npass = kAttnRowsInFlight * rpp;
   const int sub = threadIdx.x & (lpr - 1), rr = threadIdx.x / lpr;
   float qf[8];
   unpack8(*reinterpret_cast<const uint4 *>(q + ((size_t)t * nq + h) * hd + sub * 8), qf);
   const uint16_t *kbase = kc + (size_t)kvh * max_seq * hd + sub * 8;
   const uint16_t *vbase = vc + (size_t)kvh * max_seq * hd + sub * 8;
+  uint4 kv[kAttnRowsInFlight], vv[kAttnRowsInFlight];
+#pragma unroll
+  for (int u = 0; u < kAttnRowsInFlight; ++u) {
+    const int j = min(u * rpp + rr, (int)max_seq - 1);
+    kv[u] = *reinterpret_cast<const uint4 *>(kbase + (size_t)j * hd);
+    vv[u] = *reinterpret_cast<const uint4 *>(vbase + (size_t)j * hd);
+  }
+  // Keys 0 .. pos0 + t, bounded by the cache (a position past it is a caller error).
+  const int nkeys = min(*pos0 + t + 1, (int)max_seq);
   float mx = -INFINITY;
-  for (int j0 = 0; j0 < nkeys; j0 += kAttnRowsInFlight * rpp) {
-    uint4 kv[kAttnRowsInFlight];
+  attn_scores(kv, qf, 0, nkeys, rpp, rr, lpr, sub, scaling, s_p, mx);
+  for (int j0 = npass; j0 < nkeys; j0 += npass) {
 #pragma unroll
     for (int u = 0; u < kAttnRowsInFlight; ++u) {
       const int j = min(j0 + u * rpp + rr, nkeys - 1);
       kv[u] = *reinterpret_cast<const uint4 *>(kbase + (size_t)j * hd);
     }
-#pragma unroll
-    for (int u = 0; u < kAttnRowsInFlight; ++u) {
-      float kf[8];
-      unpack8(kv[u], kf);
-      float dot = 0.0f;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) dot = fmaf(qf[e], kf[e], dot);
-      for (int o = lpr >> 1; o > 0; o >>= 1) dot += __shfl_xor(dot, o, kWave);
-      const int j = j0 + u * rpp + rr;
-      if (j < nkeys) {
-        const float sc = bf16r(bf16r(dot) * scaling);
-        if (sub == 0) s_p[j] = sc;
-        mx = fmaxf(mx, sc);
-      }
-    }
+    attn_scores(kv, qf, j0, nkeys, rpp, rr, lpr, sub, scaling, s_p, mx);
   }
-  // block max
+  // block max, then the block sum of the exponentials (each a wave reduction, then the
+  // four waves' values through LDS in wave order)
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
   {
-    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
-    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
-    if (lane == 0) s_red[wave] = mx;
+    float m[1] = {mx};
+    lane_groups_reduce<true>(m, kWave);
+    if (lane == 0) s_red[wave] = m[0];
     __syncthreads();
     mx = s_red[0];
     for (int w = 1; w < kAttnThreads / kWave; ++w) mx = fmaxf(mx, s_red[w]);
@@ -172,32 +216,30 @@ attention_kernel(const uint16_t *__restrict__ q, const uint16_t *__restrict__ kc
     s_p[j] = e;
     sum += e;
   }
-  sum = block_sum(sum, s_red);
+  {
+    float v[1] = {sum};
+    lane_groups_reduce<false>(v, kWave);
+    if (lane == 0) s_red[wave] = v[0];
+    __syncthreads();
+    sum = 0.0f;
+    for (int w = 0; w < kAttnThreads / kWave; ++w) sum += s_red[w];
+    __syncthreads();
+  }
   for (int j = threadIdx.x; j < nkeys; j += kAttnThreads) s_p[j] = bf16r(s_p[j] / sum);
   __syncthreads();
   // out[d] = sum_j p_j v_j[d]: thread (rr, sub) accumulates dims sub*8 .. sub*8+7 over rows
-  // rr, rr + rpp, ...; then the rpp partial rows are summed through LDS.
+  // rr, rr + rpp, ... in order; then the rpp partial rows are summed through LDS.
   float acc[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
-  for (int j0 = 0; j0 < nkeys; j0 += kAttnRowsInFlight * rpp) {
-    uint4 vv[kAttnRowsInFlight];
+  attn_pv(vv, 0, nkeys, rpp, rr, s_p, acc);
+  for (int j0 = npass; j0 < nkeys; j0 += npass) {
 #pragma unroll
     for (int u = 0; u < kAttnRowsInFlight; ++u) {
       const int j = min(j0 + u * rpp + rr, nkeys - 1);
       vv[u] = *reinterpret_cast<const uint4 *>(vbase + (size_t)j * hd);
     }
-#pragma unroll
-    for (int u = 0; u < kAttnRowsInFlight; ++u) {
-      const int j = j0 + u * rpp + rr;
-      if (j < nkeys) {
-        const float p = s_p[j];
-        float vf[8];
-        unpack8(vv[u], vf);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[e] = fmaf(p, vf[e], acc[e]);
-      }
-    }
+    attn_pv(vv, j0, nkeys, rpp, rr, s_p, acc);
   }
   float4 *sa = reinterpret_cast<float4 *>(s_acc + rr * hd + sub * 8);
   sa[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
@@ -339,10 +381,10 @@ __device__ __forceinline__ void gemv1_pair(const uint16_t *w0, const uint16_t *w
 
 // y = W x for one token, rows in pairs (n, n + 1) per wave, x read from xl's slices.
 __device__ __forceinline__ void gemv1_rows(const uint16_t *W, const uint16_t *xl, int N, int K,
-                                           uint16_t *y) {
+                                           int nblocks, uint16_t *y) {
   const int lane = threadIdx.x & (kWave - 1);
   const int gw = blockIdx.x * kGemvWaves + (threadIdx.x >> 6);
-  const int nw = gridDim.x * kGemvWaves;
+  const int nw = nblocks * kGemvWaves;
   const int nchunk = K / 512;
   uint4 a[kGemv1Chunks], b[kGemv1Chunks];
   for (int n0 = gw * 2; n0 < N; n0 += nw * 2) {
@@ -366,7 +408,9 @@ __device__ __forceinline__ void gemv1_rows(const uint16_t *W, const uint16_t *xl
 __global__ void __launch_bounds__(kGemvThreads)
 gemv1_kernel(const uint16_t *__restrict__ W, const uint16_t *__restrict__ x, int N, int K,
              uint16_t *__restrict__ y) {
-  gemv1_rows(W, x + (threadIdx.x & (kWave - 1)) * 8, N, K, y);
+  int nblocks = gridDim.x;
+  MOE_ARGS_FIRST(MOE_LIST("+s"(N), "+s"(K), "+s"(nblocks)), MOE_LIST("s"(W), "s"(x), "s"(y)));
+  gemv1_rows(W, x + (threadIdx.x & (kWave - 1)) * 8, N, K, nblocks, y);
 }
 
 // ---------------------------------------------------------------- fused decode-step kernels
@@ -392,9 +436,14 @@ qkv_rope_kernel(const uint16_t *__restrict__ W, const uint16_t *__restrict__ x,
                 uint16_t *__restrict__ vc) {
   __shared__ __attribute__((aligned(16))) uint16_t s_x[kFusedMaxH];
   __shared__ float s_part[kNormThreads / kWave];
+  int nblocks = gridDim.x;
+  MOE_ARGS_FIRST(MOE_LIST("+s"(x_rows), "+s"(eps), "+s"(H), "+s"(nq), "+s"(nkv), "+s"(hd), "+s"(max_seq),
+                          "+s"(nblocks)),
+                 MOE_LIST("s"(W), "s"(x), "s"(x_row), "s"(res), "s"(nw), "s"(inv_freq), "s"(pos0),
+                      "s"(res_out), "s"(q_out), "s"(kc), "s"(vc)));
   const int lane = threadIdx.x & (kWave - 1);
   const int gw = blockIdx.x * kGemvWaves + (threadIdx.x >> 6);
-  const int nwv = gridDim.x * kGemvWaves;
+  const int nwv = nblocks * kGemvWaves;
   const int half = hd >> 1;
   const int pairs = (nq + 2 * nkv) * half;
   const int nchunk = H / 512;
@@ -550,6 +599,8 @@ argmax_finish_kernel(const float *__restrict__ cand_v, const int32_t *__restrict
                      int64_t *__restrict__ gen_ctr, int32_t *__restrict__ pos) {
   __shared__ float s_bv[kGemvWaves];
   __shared__ int s_bi[kGemvWaves];
+  MOE_ARGS_FIRST(MOE_LIST("+s"(n), "+s"(gen_cap)),
+                 MOE_LIST("s"(cand_v), "s"(cand_i), "s"(token), "s"(gen), "s"(gen_ctr), "s"(pos)));
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
   float bv = -INFINITY;
   int bi = 0x7fffffff;

@@ -95,13 +95,6 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// DPP move of v with control CTRL (row_mask and bank_mask all set, no bound control).
-template <int CTRL>
-__device__ __forceinline__ float dpp_mov(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xf,
-                                                            0xf, false));
-}
-
 __device__ __forceinline__ float lanes_sum16(float v) {
   // Sum over the 16 lanes that share l % 4 (the block index occupies lane bits 2..5):
   // rotations by 4 and 8 within each 16-lane row (DPP), then the two cross-row pairs.
