@@ -114,6 +114,14 @@ __device__ __forceinline__ void lane_groups_reduce(float (&v)[N], int n) {
   }
 }
 
+// Two sums over the whole wave, every lane getting both.
+__device__ __forceinline__ void wave_sum_pair(float &a, float &b) {
+  float v[2] = {a, b};
+  lane_groups_reduce<false>(v, kWave);
+  a = v[0];
+  b = v[1];
+}
+
 }  // namespace moe
 
 // Status helpers for the C-ABI entry points.

@@ -308,13 +308,17 @@ gemv_kernel(const uint16_t *__restrict__ W, const uint16_t *__restrict__ x, int 
         }
       }
     }
+    float sums[2 * T];
 #pragma unroll
     for (int r = 0; r < 2; ++r)
 #pragma unroll
-      for (int t = 0; t < T; ++t) {
-        const float v = wave_sum(acc[r][t]);
-        if (lane == 0 && (r == 0 || n1 != n0)) y[(size_t)t * N + (r ? n1 : n0)] = f32_to_bf16(v);
-      }
+      for (int t = 0; t < T; ++t) sums[r * T + t] = acc[r][t];
+    lane_groups_reduce<false>(sums, kWave);
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+      for (int t = 0; t < T; ++t)
+        if (lane == 0 && (r == 0 || n1 != n0)) y[(size_t)t * N + (r ? n1 : n0)] = f32_to_bf16(sums[r * T + t]);
   }
 }
 
@@ -392,8 +396,7 @@ __device__ __forceinline__ void gemv1_rows(const uint16_t *W, const uint16_t *xl
     float acc0, acc1;
     gemv1_pair(W + (size_t)n0 * K + lane * 8, W + (size_t)n1 * K + lane * 8, xl, nchunk, a, b, false,
                acc0, acc1);
-    acc0 = wave_sum(acc0);
-    acc1 = wave_sum(acc1);
+    wave_sum_pair(acc0, acc1);
     if (lane == 0) {
       y[n0] = f32_to_bf16(acc0);
       if (n1 != n0) y[n1] = f32_to_bf16(acc1);
@@ -476,8 +479,7 @@ qkv_rope_kernel(const uint16_t *__restrict__ W, const uint16_t *__restrict__ x,
     if (!loaded) rows_of(p, w0, w1);
     float acc0, acc1;
     gemv1_pair(w0, w1, s_x + lane * 8, nchunk, a, b, loaded, acc0, acc1);
-    acc0 = wave_sum(acc0);
-    acc1 = wave_sum(acc1);
+    wave_sum_pair(acc0, acc1);
     if (lane == 0) {
       const int head = p / half, i = p - head * half;
       const float y1 = bf16r(acc0), y2 = bf16r(acc1);
@@ -558,8 +560,7 @@ head_logits_kernel(const uint16_t *__restrict__ W, const uint16_t *__restrict__ 
     float acc0, acc1;
     gemv1_pair(W + (size_t)n0 * K + lane * 8, W + (size_t)n1 * K + lane * 8, s_x + lane * 8, nchunk,
                a, b, n0 == f0, acc0, acc1);
-    acc0 = wave_sum(acc0);
-    acc1 = wave_sum(acc1);
+    wave_sum_pair(acc0, acc1);
     const float y0 = bf16r(acc0), y1 = bf16r(acc1);
     if (argmax_better(y0, n0, bv, bi)) {
       bv = y0;

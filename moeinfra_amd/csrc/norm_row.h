@@ -25,8 +25,9 @@ __device__ __forceinline__ void lds_barrier() {
 
 __device__ __forceinline__ float block_sum(float v, float *s_part) {
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
-  v = wave_sum(v);
-  if (lane == 0) s_part[wave] = v;
+  float ws[1] = {v};
+  lane_groups_reduce<false>(ws, kWave);
+  if (lane == 0) s_part[wave] = ws[0];
   lds_barrier();
   float t = 0.0f;
   for (int w = 0; w < (int)(blockDim.x >> 6); ++w) t += s_part[w];
