@@ -66,10 +66,31 @@ __device__ __forceinline__ uint4 ld_stream16(const void *p) {
 #define MOE_ARGS_FIRST(outs, ins) asm volatile("" : outs : ins)
 
 // ---------------------------------------------------------------- wave reductions
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
-  return v;
+
+// op(v, v of lane l ^ 32) and op(v, v of lane l ^ 16) in every lane l (op: + or max), by one
+// v_permlane32_swap / v_permlane16_swap (VALU, no LDS round trip).  With both operands v, the
+// swap returns [v(0..31), v(0..31)] and [v(32..63), v(32..63)] (16: rows 0, 0, 2, 2 and
+// 1, 1, 3, 3), so lane l adds its own value and its partner's, in one order or the other:
+// bit-identical to v + __shfl_xor(v, 32) as IEEE addition and max are commutative.  The
+// second result passes through an empty asm: without it the compiler reads the first result
+// twice when both feed one operation.
+template <bool MAX>
+__device__ __forceinline__ float op_xor32(float v) {
+  const unsigned w = __builtin_bit_cast(unsigned, v);
+  const auto x = __builtin_amdgcn_permlane32_swap(w, w, false, false);
+  unsigned hi = x[1];
+  asm volatile("" : "+v"(hi));
+  const float a = __builtin_bit_cast(float, (unsigned)x[0]), b = __builtin_bit_cast(float, hi);
+  return MAX ? fmaxf(a, b) : a + b;
+}
+template <bool MAX>
+__device__ __forceinline__ float op_xor16(float v) {
+  const unsigned w = __builtin_bit_cast(unsigned, v);
+  const auto x = __builtin_amdgcn_permlane16_swap(w, w, false, false);
+  unsigned hi = x[1];
+  asm volatile("" : "+v"(hi));
+  const float a = __builtin_bit_cast(float, (unsigned)x[0]), b = __builtin_bit_cast(float, hi);
+  return MAX ? fmaxf(a, b) : a + b;
 }
 
 // DPP move of v with control CTRL (row_mask and bank_mask all set, no bound control).
@@ -79,11 +100,24 @@ __device__ __forceinline__ float dpp_mov(float v) {
                                                             0xf, false));
 }
 
+// Sum over the wave by the butterfly l ^ 32, 16, 8, 4, 2, 1 (every lane gets the sum): the
+// exchanges with lane l ^ 8 (row_ror:8 within a 16-lane row), l ^ 2 and l ^ 1 (quad_perm)
+// are DPP moves, l ^ 32 and l ^ 16 permlane swaps, l ^ 4 an LDS shuffle.
+__device__ __forceinline__ float wave_sum(float v) {
+  v = op_xor32<false>(v);
+  v = op_xor16<false>(v);
+  v += dpp_mov<0x128>(v);
+  v += __shfl_xor(v, 4, kWave);
+  v += dpp_mov<0x4E>(v);
+  v += dpp_mov<0xB1>(v);
+  return v;
+}
+
 // Sums (MAX: maxima) of N values over aligned groups of n lanes (n a power of two <= 64,
 // uniform), every lane of a group getting its group's result.  Within a 16-lane DPP row the
 // steps are register moves: quad_perm [1,0,3,2] (lane ^ 1), quad_perm [2,3,0,1] (lane ^ 2),
 // then, with every quad holding one value, row_half_mirror (the other quad of the 8) and
-// row_mirror (the other 8 of the 16); beyond 16 lanes, shuffles through LDS.  The N
+// row_mirror (the other 8 of the 16); beyond 16 lanes, permlane swaps.  The N
 // reductions advance step by step together, so their latencies overlap.
 template <bool MAX, int N>
 __device__ __forceinline__ void lane_groups_reduce(float (&v)[N], int n) {
@@ -106,11 +140,11 @@ __device__ __forceinline__ void lane_groups_reduce(float (&v)[N], int n) {
   }
   if (n >= 32) {
 #pragma unroll
-    for (int i = 0; i < N; ++i) v[i] = op(v[i], __shfl_xor(v[i], 16, kWave));
+    for (int i = 0; i < N; ++i) v[i] = op_xor16<MAX>(v[i]);
   }
   if (n >= 64) {
 #pragma unroll
-    for (int i = 0; i < N; ++i) v[i] = op(v[i], __shfl_xor(v[i], 32, kWave));
+    for (int i = 0; i < N; ++i) v[i] = op_xor32<MAX>(v[i]);
   }
 }
 

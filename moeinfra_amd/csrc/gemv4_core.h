@@ -100,8 +100,8 @@ __device__ __forceinline__ float lanes_sum16(float v) {
   // rotations by 4 and 8 within each 16-lane row (DPP), then the two cross-row pairs.
   v += dpp_mov<0x124>(v);  // row_ror:4
   v += dpp_mov<0x128>(v);  // row_ror:8
-  v += __shfl_xor(v, 16, kWave);
-  v += __shfl_xor(v, 32, kWave);
+  v = op_xor16<false>(v);
+  v = op_xor32<false>(v);
   return v;
 }
 

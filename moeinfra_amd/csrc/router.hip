@@ -52,7 +52,7 @@ constexpr int kRtChunkBytes = 8192;  // gate bytes per LDS chunk (all expert row
 constexpr int kRtWholeBytes = 65536;
 constexpr int kRtPad = 8;  // values of padding per LDS gate row (rows 16 bytes apart in banks)
 
-// Over lanes 0..N-1 (N = 16: DPP within the row; N = 32, 64: then shuffles): every lane
+// Over lanes 0..N-1 (N = 16: DPP within the row; N = 32, 64: then permlane swaps): every lane
 // of those rows gets the result, the same bits in all of them (each step combines two
 // partials that the partner combines in the other order).
 template <int N>
@@ -61,14 +61,20 @@ __device__ __forceinline__ float rt_max(float v) {
   v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xf, 0xf, false)));
   v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x124, 0xf, 0xf, false)));
   v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x128, 0xf, 0xf, false)));
-#pragma unroll
-  for (int o = 16; o < N; o <<= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  if constexpr (N > 16) v = op_xor16<true>(v);
+  if constexpr (N > 32) v = op_xor32<true>(v);
   return v;
 }
+// Sum over lanes 0..N-1 by the butterfly l ^ 1, 2, 4, ... (DPP for 1, 2 and 8, permlane
+// swaps for 16 and 32, an LDS shuffle for 4).
 template <int N>
 __device__ __forceinline__ float rt_sum(float v) {
-#pragma unroll
-  for (int o = 1; o < N; o <<= 1) v += __shfl_xor(v, o, kWave);
+  if constexpr (N > 1) v += dpp_mov<0xB1>(v);
+  if constexpr (N > 2) v += dpp_mov<0x4E>(v);
+  if constexpr (N > 4) v += __shfl_xor(v, 4, kWave);
+  if constexpr (N > 8) v += dpp_mov<0x128>(v);
+  if constexpr (N > 16) v = op_xor16<false>(v);
+  if constexpr (N > 32) v = op_xor32<false>(v);
   return v;
 }
 
@@ -80,8 +86,8 @@ __device__ __forceinline__ rt_s16x4 rt_pair(uint32_t lo, uint32_t hi) {
 __device__ __forceinline__ float rt_sum16(float v) {
   v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x124, 0xf, 0xf, false));
   v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x128, 0xf, 0xf, false));
-  v += __shfl_xor(v, 16, kWave);
-  v += __shfl_xor(v, 32, kWave);
+  v = op_xor16<false>(v);
+  v = op_xor32<false>(v);
   return v;
 }
 
@@ -398,8 +404,8 @@ route_small_kernel(const uint16_t *__restrict__ x, const uint16_t *__restrict__ 
 #pragma unroll
     for (int e = 0; e < EMAX; ++e) {
       float v = acc[e];
-      v += __shfl_xor(v, 16, kWave);
-      v += __shfl_xor(v, 32, kWave);
+      v = op_xor16<false>(v);
+      v = op_xor32<false>(v);
       if (lane < kRouteMaxTokens) s_tpart[CHUNKED ? wave : 0][lane][e] = v;
     }
   } else if (t < T) {
