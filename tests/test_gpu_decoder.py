@@ -80,12 +80,15 @@ def test_rope_and_cache_write(cuda_device):
     assert not kc[:, :p0].any() and not kc[:, p0 + T:].any()              # other rows untouched
 
 
-@pytest.mark.parametrize("T,p0,max_seq", [(1, 0, 256), (1, 71, 256), (40, 0, 256), (7, 20, 256),
-                                          (1, 3000, 4096), (16, 2040, 4096)])
-def test_attention(cuda_device, T, p0, max_seq):
+@pytest.mark.parametrize("T,p0,max_seq,hd", [(1, 0, 256, 128), (1, 71, 256, 128), (40, 0, 256, 128),
+                                             (7, 20, 256, 128), (1, 3000, 4096, 128),
+                                             (16, 2040, 4096, 128),
+                                             # a score sums over hd / 8 lanes: 4, 8 and 32 lanes
+                                             (1, 71, 256, 32), (3, 200, 512, 64), (2, 129, 256, 256)])
+def test_attention(cuda_device, T, p0, max_seq, hd):
     from moeinfra_amd import _lib
 
-    nq, nkv, hd = 32, 8, 128
+    nq, nkv = 32, 8
     S = p0 + T
     q = _bf16((T, nq, hd), 5)
     k = _bf16((nkv, S, hd), 6)
