@@ -752,7 +752,7 @@ __device__ __forceinline__ RouteSummary route_wave(RouteHead &rh, int32_t (&sl_e
   return RouteSummary{n_active, !multi, present};
 }
 
-template <int EMAX, bool NORM>
+template <int EMAX, bool NORM, bool N1 = false>
 __global__ void __launch_bounds__(kDecThreads, 1)
 decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
                      const uint16_t *__restrict__ gate, const float *__restrict__ bias, int T,
@@ -778,6 +778,7 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
   // NORM: the normalised token (gate products read it here) and the norm's wave sums.
   __shared__ __attribute__((aligned(16))) uint16_t s_xn[NORM ? kDecNormMaxH : 8];
   __shared__ float s_npart[kDecWaves];
+  __shared__ float s_nsq[N1 ? kNormThreads : 1][4];  // N1: the second half's squared pairs
   // Multi-token steps (no fused norm): the tokens, swizzled as xlds_piece describes.
   __shared__ uint4 s_xt[NORM ? 1 : kXtMaxVals / 8];
 
@@ -787,11 +788,16 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
   const bool wg0 = blockIdx.x == 0;
   if (tid == 0) s_ticket = 0;
   // NORM: the norm's loads (x, residual, weight; L2-resident) go first, so that waiting
-  // for them does not wait for the gate rows issued after them.  Every wave loads (waves
-  // 4-7 duplicates, unused): no load behind a branch.
-  NormRegs<kDecNormChunks> ng;
+  // for them does not wait for the gate rows issued after them.  N1 (H <= 4096): one chunk
+  // per thread of the workgroup; otherwise threads 0..255 take up to four and the other
+  // waves repeat loads (unused): no load behind a branch.
+  NormRegs<N1 ? 1 : kDecNormChunks> ng;
+  NormOneRegs n1;
   if (NORM) {
-    norm_load<kDecNormChunks, true>(ng, x, nrm.res, nrm.w, H);
+    if constexpr (N1)
+      norm_load_one<true>(n1, x, nrm.res, nrm.w, H);
+    else
+      norm_load<kDecNormChunks, true>(ng, x, nrm.res, nrm.w, H);
     __builtin_amdgcn_sched_barrier(0);  // keep them ahead of the gate rows
   }
   // The token the expert stream reads: x, or this workgroup's row of normalised values.
@@ -875,11 +881,14 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
   }
   __builtin_amdgcn_sched_barrier(0);
   if (NORM) {
-    // r = x + res (workgroup 0 writes it), xn = rmsnorm(r) by threads 0..255 exactly as the
+    // r = x + res (workgroup 0 writes it), xn = rmsnorm(r) with the sums of the 256-thread
     // norm kernel, into LDS (the single-token stream reads it there; other paths copy it to
     // the workgroup's xs row first).
-    norm_finish<kDecNormChunks, true>(ng, nrm.eps, H, wg0 ? nrm.res_out : nullptr, s_xn, s_npart,
-                                      tid < kNormThreads);
+    if constexpr (N1)
+      norm_finish_one<true>(n1, nrm.eps, H, wg0 ? nrm.res_out : nullptr, s_xn, s_npart, s_nsq);
+    else
+      norm_finish<kDecNormChunks, true>(ng, nrm.eps, H, wg0 ? nrm.res_out : nullptr, s_xn, s_npart,
+                                        tid < kNormThreads);
     lds_barrier();
   }
   for (int c0 = 0; c0 < n_chunks; c0 += CPR) {
@@ -2414,7 +2423,10 @@ int launch_decode_layer(const moe_nf4_expert_t *experts, int32_t E, const void *
                        F, E, k, (uint16_t *)logits, (float *)weights, (int64_t *)idx64,
                        (DecodeRoute *)route_ws, (uint16_t *)h_ws, nrm);
   };
-  if (norm != nullptr)
+  const bool n1 = H <= 2 * kNormThreads * 8;  // the fused norm's one-chunk-per-thread form
+  if (norm != nullptr && n1)
+    gateup(E <= 8 ? decode_gateup_kernel<8, true, true> : decode_gateup_kernel<16, true, true>);
+  else if (norm != nullptr)
     gateup(E <= 8 ? decode_gateup_kernel<8, true> : decode_gateup_kernel<16, true>);
   else
     gateup(E <= 8 ? decode_gateup_kernel<8, false> : decode_gateup_kernel<16, false>);

@@ -111,6 +111,80 @@ __device__ __forceinline__ void norm_finish(NormRegs<CH> &g, float eps, int H, u
   }
 }
 
+// The same row by 2 kNormThreads threads for H <= 2 kNormThreads * 8 (the order of
+// norm_finish<2>): thread t loads chunk t only, and thread kNormThreads + t hands its chunk's
+// four squared pairs to thread t through LDS, which adds them after its own exactly as
+// norm_finish<2> adds its second chunk.  The statistics and outputs are those of the
+// kNormThreads form bit for bit, without the loads of a second chunk per thread or of
+// chunks past H.
+struct NormOneRegs {
+  uint4 x, r, w;
+};
+template <bool RES>
+__device__ __forceinline__ void norm_load_one(NormOneRegs &g, const uint16_t *x, const uint16_t *res,
+                                              const uint16_t *w, int H) {
+  int c = threadIdx.x * 8;
+  c = c < H ? c : H - 8;
+  g.w = *reinterpret_cast<const uint4 *>(w + c);
+  g.x = *reinterpret_cast<const uint4 *>(x + c);
+  if (RES) g.r = *reinterpret_cast<const uint4 *>(res + c);
+}
+template <bool RES>
+__device__ __forceinline__ void norm_finish_one(NormOneRegs &g, float eps, int H, uint16_t *res_out,
+                                                uint16_t *out, float *s_part,
+                                                float (*s_sq)[4]) {
+  const int tid = threadIdx.x;
+  const int c = tid * 8;
+  uint4 v = g.x;
+  if (RES) {
+    const uint32_t a[4] = {v.x, v.y, v.z, v.w}, b[4] = {g.r.x, g.r.y, g.r.z, g.r.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      o[j] = pack_bf16x2(bf16lo_to_f32(a[j]) + bf16lo_to_f32(b[j]),
+                         bf16hi_to_f32(a[j]) + bf16hi_to_f32(b[j]));
+    v = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+  g.x = v;
+  float sq[4];
+  {
+    const uint32_t a[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float lo = bf16lo_to_f32(a[j]), hi = bf16hi_to_f32(a[j]);
+      sq[j] = lo * lo + hi * hi;
+    }
+  }
+  if (tid >= kNormThreads) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) s_sq[tid - kNormThreads][j] = sq[j];
+  }
+  lds_barrier();
+  float ss = 0.0f;
+  if (tid < kNormThreads) {
+    float t = ss;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) t += sq[j];
+    ss = c < H ? t : ss;
+    t = ss;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) t += s_sq[tid][j];
+    ss = c + kNormThreads * 8 < H ? t : ss;
+  }
+  const float inv = 1.0f / sqrtf(block_sum(ss, s_part) / (float)H + eps);
+  if (c < H) {
+    const uint32_t a[4] = {g.x.x, g.x.y, g.x.z, g.x.w};
+    const uint32_t gw[4] = {g.w.x, g.w.y, g.w.z, g.w.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      o[j] = pack_bf16x2(bf16lo_to_f32(gw[j]) * bf16r(bf16lo_to_f32(a[j]) * inv),
+                         bf16hi_to_f32(gw[j]) * bf16r(bf16hi_to_f32(a[j]) * inv));
+    if (res_out != nullptr) *reinterpret_cast<uint4 *>(res_out + c) = g.x;
+    *reinterpret_cast<uint4 *>(out + c) = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+}
+
 template <int CH, bool RES>
 __device__ __forceinline__ void rmsnorm_row(const uint16_t *x, const uint16_t *res, const uint16_t *w,
                                             float eps, int H, uint16_t *res_out, uint16_t *out,
