@@ -776,11 +776,11 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
   __shared__ float s_raw[kRawSlots][2][kWave];
   __shared__ uint8_t s_mine[kDecWaves][kRawSlots];  // the raw slots each wave filled
   // NORM: the normalised token (gate products read it here) and the norm's wave sums.
-  __shared__ __attribute__((aligned(16))) uint16_t s_xn[NORM ? kDecNormMaxH : 8];
+  __shared__ __attribute__((aligned(16))) uint16_t s_xn[NORM || N1 ? kDecNormMaxH : 8];
   __shared__ float s_npart[kDecWaves];
   __shared__ float s_nsq[N1 ? kNormThreads : 1][4];  // N1: the second half's squared pairs
   // Multi-token steps (no fused norm): the tokens, swizzled as xlds_piece describes.
-  __shared__ uint4 s_xt[NORM ? 1 : kXtMaxVals / 8];
+  __shared__ uint4 s_xt[NORM || N1 ? 1 : kXtMaxVals / 8];
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
@@ -790,15 +790,21 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
   // NORM: the norm's loads (x, residual, weight; L2-resident) go first, so that waiting
   // for them does not wait for the gate rows issued after them.  N1 (H <= 4096): one chunk
   // per thread of the workgroup; otherwise threads 0..255 take up to four and the other
-  // waves repeat loads (unused): no load behind a branch.
+  // waves repeat loads (unused): no load behind a branch.  N1 without NORM (one token):
+  // the token is copied into s_xn one 16-byte chunk per thread, and the gate products and
+  // the stream read it there as they read the normalised token.
   NormRegs<N1 ? 1 : kDecNormChunks> ng;
   NormOneRegs n1;
+  uint4 xcopy;  // N1 without NORM: this thread's chunk of the token (a plain register value)
   if (NORM) {
     if constexpr (N1)
       norm_load_one<true>(n1, x, nrm.res, nrm.w, H);
     else
       norm_load<kDecNormChunks, true>(ng, x, nrm.res, nrm.w, H);
     __builtin_amdgcn_sched_barrier(0);  // keep them ahead of the gate rows
+  } else if constexpr (N1) {
+    xcopy = *reinterpret_cast<const uint4 *>(x + (tid * 8 < H ? tid * 8 : H - 8));
+    __builtin_amdgcn_sched_barrier(0);  // keep it ahead of the gate rows
   }
   // The token the expert stream reads: x, or this workgroup's row of normalised values.
   const uint16_t *xt = NORM ? nrm.xs + (size_t)blockIdx.x * H : x;
@@ -832,7 +838,7 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
 #pragma unroll
     for (int c = 0; c < CPR; ++c) {
       const int cc = c0 + c < n_chunks ? c0 + c : 0;  // past the end: chunk 0 again, unused
-      if (!NORM) xv[c] = ld_u4(xrow + (size_t)cc * (128 * kDecWaves));
+      if (!NORM && !N1) xv[c] = ld_u4(xrow + (size_t)cc * (128 * kDecWaves));
 #pragma unroll
       for (int g = 0; g < G; ++g) gv[c][g] = ld_u4(grow[g] + (size_t)cc * (128 * kDecWaves));
     }
@@ -841,7 +847,7 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
   // Multi-token steps: this thread's pieces of the tokens for the LDS copy (stored before
   // the routing barrier).  Only T > 1 loads them; on the single-token path the compiler's
   // waits stay exact.
-  const bool xlds = !NORM && T > 1 && T * H <= kXtMaxVals;
+  const bool xlds = !NORM && !N1 && T > 1 && T * H <= kXtMaxVals;  // N1 runs one token only
   constexpr int kXtPer = kXtMaxVals / 8 / kDecThreads;  // pieces per thread at most
   uint4 xtv[kXtPer];
   if (xlds) {
@@ -890,13 +896,16 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
       norm_finish<kDecNormChunks, true>(ng, nrm.eps, H, wg0 ? nrm.res_out : nullptr, s_xn, s_npart,
                                         tid < kNormThreads);
     lds_barrier();
+  } else if constexpr (N1) {
+    if (tid * 8 < H) *reinterpret_cast<uint4 *>(s_xn + tid * 8) = xcopy;
+    lds_barrier();
   }
   for (int c0 = 0; c0 < n_chunks; c0 += CPR) {
     if (c0 > 0) {
       load_round(c0);
       __builtin_amdgcn_sched_barrier(0);
     }
-    if (NORM) {  // this round's x chunks from LDS (T = 1)
+    if (NORM || N1) {  // this round's x chunks from LDS (T = 1)
 #pragma unroll
       for (int c = 0; c < CPR; ++c) {
         const int cc = c0 + c < n_chunks ? c0 + c : 0;
@@ -1079,7 +1088,7 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
     const int nit = whi - wlo;
     if (nit > kRawSlots) {
       auto finish1 = [&](f32x4 (&ac)[2], int i) { finish_item(ac, i, 1); };
-      if (NORM)
+      if (NORM || N1)
         stream_aligned<2, 8, kGateUpDepth, true, kXRegs, kLookahead>(
             grab, set_ptrs, finish1, hook, s_tbl, lane_const, row_blocks, s_aslot[wave], xl, (gq_t)gate);
       else
@@ -1094,7 +1103,7 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
       if (lane == 0) s_mine[wave][nmine] = (uint8_t)(i - wlo);
       ++nmine;
     };
-    if (NORM)
+    if (NORM || N1)
       stream_aligned<2, 8, kGateUpDepth, true, kXRegs, kLookahead>(
           grab, set_ptrs, finish_raw, hook, s_tbl, lane_const, row_blocks, s_aslot[wave], xl, (gq_t)gate);
     else
@@ -2428,6 +2437,8 @@ int launch_decode_layer(const moe_nf4_expert_t *experts, int32_t E, const void *
     gateup(E <= 8 ? decode_gateup_kernel<8, true, true> : decode_gateup_kernel<16, true, true>);
   else if (norm != nullptr)
     gateup(E <= 8 ? decode_gateup_kernel<8, true> : decode_gateup_kernel<16, true>);
+  else if (T == 1 && n1)  // the token from the workgroup's LDS copy
+    gateup(E <= 8 ? decode_gateup_kernel<8, false, true> : decode_gateup_kernel<16, false, true>);
   else
     gateup(E <= 8 ? decode_gateup_kernel<8, false> : decode_gateup_kernel<16, false>);
   MOE_LAUNCH_CHECK();
