@@ -251,19 +251,22 @@ def test_head_argmax(cuda_device):
     assert gen.tolist() == [-1, 777, 777] and int(gctr.item()) == 4 and int(pos.item()) == 11
 
 
-@pytest.mark.parametrize("full", [True, False])
-def test_layer_norm_fused_matches_unfused(cuda_device, full):
+@pytest.mark.parametrize("form", ["full", "small", "wide"])
+def test_layer_norm_fused_matches_unfused(cuda_device, form):
     """The single-token MoE layer with the post-attention residual add + norm in its gate/up
     kernel == moe_add_rmsnorm_bf16 then moe_layer_forward_nf4, bit for bit (output,
-    residual, routing weights and ids), on two calls in a row."""
+    residual, routing weights and ids), on two calls in a row.  Hidden 4096 and 512 take the
+    one-chunk-per-thread norm, 6144 the form with up to four chunks per thread."""
     from moeinfra_amd import _lib
     from moeinfra_amd.engine.decoder import MixtralShape, synthesize
 
     lib = _lib.lib()
     dev = cuda_device
-    shape = (MixtralShape(layers=1) if full else
-             MixtralShape(hidden=512, ffn=1024, layers=1, n_heads=8, n_kv_heads=2, head_dim=64,
-                          vocab=64))
+    shape = {"full": MixtralShape(layers=1),
+             "small": MixtralShape(hidden=512, ffn=1024, layers=1, n_heads=8, n_kv_heads=2,
+                                   head_dim=64, vocab=64),
+             "wide": MixtralShape(hidden=6144, ffn=1536, layers=1, n_heads=48, n_kv_heads=8,
+                                  head_dim=128, vocab=64)}[form]
     w = synthesize(shape, seed=41, device=dev)
     lw = w.layers[0]
     H, F, E, k = shape.hidden, shape.ffn, shape.experts, shape.top_k
