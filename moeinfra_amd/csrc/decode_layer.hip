@@ -775,7 +775,8 @@ decode_gateup_kernel(const ExpertTable tab, const uint16_t *__restrict__ x,
   // j = lane % 4 of the tile, block lane / 4).
   __shared__ float s_raw[kRawSlots][2][kWave];
   __shared__ uint8_t s_mine[kDecWaves][kRawSlots];  // the raw slots each wave filled
-  // NORM: the normalised token (gate products read it here) and the norm's wave sums.
+  // NORM or N1: the token the gate products and the single-token stream read (normalised
+  // with NORM), and the norm's wave sums.
   __shared__ __attribute__((aligned(16))) uint16_t s_xn[NORM || N1 ? kDecNormMaxH : 8];
   __shared__ float s_npart[kDecWaves];
   __shared__ float s_nsq[N1 ? kNormThreads : 1][4];  // N1: the second half's squared pairs
