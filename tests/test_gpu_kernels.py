@@ -177,9 +177,11 @@ def test_layer_matches_oracle(cuda_device, H, F, E, T, seed, skew):
     assert err <= 1e-2, err
 
 
-@pytest.mark.parametrize("H,F,T", [(512, 1024, 3), (256, 512, 12)])
+@pytest.mark.parametrize("H,F,T", [(512, 1024, 3), (256, 512, 12), (4096, 1024, 1), (512, 1024, 1)])
 def test_layer_mixed_codebooks(cuda_device, H, F, T):
-    """Experts whose codebooks differ from the first active one (per-expert fallback)."""
+    """Experts whose codebooks differ from the first active one (per-expert fallback).  One
+    token: the gate products read the workgroup's LDS copy of the token while the per-nibble
+    stream reads it from global memory."""
     codes = {e: (orc.NF4_CODE * np.float32(0.75 + 0.05 * e)).astype(np.float32)
              for e in (1, 4, 6)}
     want, i_want, got, i_got, lg = _layer_case(cuda_device, H, F, 8, T, 10 + T, codes=codes)
