@@ -439,9 +439,15 @@ expert_gemm_kernel(const ExpertTable tab, const uint16_t *__restrict__ act, uint
       u32x4 a[kGmMT];
       f32x2 c[kGmNF][4];
     };
+    // Token tiles t >= live (wave-uniform; kGmMT except in the unpipelined forms' items of
+    // at most 32 rows) read no A operands and run no MFMAs: their sums stay zero and their
+    // rows are past the expert's count.
+    int live = kGmMT;
     auto issue = [&](Pre &P, const GM_LDS uint8_t *plane, const GM_LDS char *tb, int slot, int q) {
 #pragma unroll
-      for (int t = 0; t < kGmMT; ++t) P.a[t] = *reinterpret_cast<const GM_LDS u32x4 *>(plane + a_lds[q] + t * 32 * 128);
+      for (int t = 0; t < kGmMT; ++t)
+        if (t == 0 || kPipe || t < live)
+          P.a[t] = *reinterpret_cast<const GM_LDS u32x4 *>(plane + a_lds[q] + t * 32 * 128);
 #pragma unroll
       for (int f = 0; f < kGmNF; ++f)
 #pragma unroll
@@ -463,9 +469,11 @@ expert_gemm_kernel(const ExpertTable tab, const uint16_t *__restrict__ act, uint
     auto mfmas = [&](const Pre &P, const bf16x8 (&bv)[kGmNF]) {
 #pragma unroll
       for (int t = 0; t < kGmMT; ++t)
+        if (t == 0 || kPipe || t < live) {
 #pragma unroll
-        for (int f = 0; f < kGmNF; ++f)
-          acc[t][f] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(P.a[t]), bv[f], acc[t][f], 0, 0, 0);
+          for (int f = 0; f < kGmNF; ++f)
+            acc[t][f] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(P.a[t]), bv[f], acc[t][f], 0, 0, 0);
+        }
     };
 
 #pragma unroll
@@ -572,6 +580,9 @@ expert_gemm_kernel(const ExpertTable tab, const uint16_t *__restrict__ act, uint
         gm_lds_barrier();
       }
     };
+    // An item of at most 32 live rows (an expert's last, partial token tile: about half the
+    // experts of a 512-token batch spill a few rows past 128) computes one token tile.
+    live = cnt - mt * kGmM <= 32 ? 1 : kGmMT;
     int pb = 0;  // plane of block b: b % kPlanes
     for (int b0 = 0; b0 < NBp; b0 += kGmBDepth) {
 #pragma unroll
