@@ -439,8 +439,9 @@ expert_gemm_kernel(const ExpertTable tab, const uint16_t *__restrict__ act, uint
       u32x4 a[kGmMT];
       f32x2 c[kGmNF][4];
     };
-    // Token tiles t >= live (wave-uniform; kGmMT except in the unpipelined forms' items of
-    // at most 32 rows) read no A operands and run no MFMAs: their sums stay zero and their
+    // Token tiles t >= live (wave-uniform: the tiles holding the item's rows; always kGmMT in
+    // the pipelined forms, whose accumulators do not survive a branch around their MFMAs
+    // without spilling) read no A operands and run no MFMAs: their sums stay zero and their
     // rows are past the expert's count.
     int live = kGmMT;
     auto issue = [&](Pre &P, const GM_LDS uint8_t *plane, const GM_LDS char *tb, int slot, int q) {
@@ -580,9 +581,9 @@ expert_gemm_kernel(const ExpertTable tab, const uint16_t *__restrict__ act, uint
         gm_lds_barrier();
       }
     };
-    // An item of at most 32 live rows (an expert's last, partial token tile: about half the
-    // experts of a 512-token batch spill a few rows past 128) computes one token tile.
-    live = cnt - mt * kGmM <= 32 ? 1 : kGmMT;
+    // An expert's last token tile is often partial (about half the experts of a 512-token
+    // batch spill a few rows past 128).
+    live = min(kGmMT, (cnt - mt * kGmM + 31) >> 5);
     int pb = 0;  // plane of block b: b % kPlanes
     for (int b0 = 0; b0 < NBp; b0 += kGmBDepth) {
 #pragma unroll
